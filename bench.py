@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Q4_K linear() path (one JSON line on stdout).
+
+Headline (BASELINE.json metric, config 1): the ragged decode batch of 8
+sequences x 1 token through the Qwen3.5-9B-shaped MLP with Q4_K weights --
+fused gate/up (K=4096 -> N=12288, x2, SiLU(gate)*up into the gate buffer) then
+down (K=12288 -> N=4096, residual added in place).  A step is one such MLP
+pass; `value` is algorithmic HBM bytes per step / step time (GB/s), with the
+inputs resident in HBM and weights rotating over enough copies (> 256 MB
+Infinity Cache) that every step streams its weights from HBM.  Steps are
+replayed from a HIP graph (launch-bound 5-20 us kernels).
+
+Also reported: config 4 (M=2048 prefill MLP, three Q4_K GEMMs) in TFLOP/s,
+the dominant kernels' rooflines from per-launch HIP events, a measured
+device-copy bandwidth, and the CPU oracle timed on host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
+FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, AMD published
+BLOCK_BYTES = 144
+
+
+def q4k_bytes(n, k):
+    return n * (k // 256) * BLOCK_BYTES
+
+
+def make_q4k(rng, n, k):
+    """GGUF block_q4_K bytes: d, dmin = fp16(U(0, 0.01)), uniform scale and quant bytes."""
+    import numpy as np
+    nb = k // 256
+    w = rng.integers(0, 256, size=(n, nb, BLOCK_BYTES), dtype=np.uint8)
+    d = rng.uniform(0.0, 0.01, size=(n, nb, 2)).astype(np.float16)
+    w[:, :, 0:4] = d.view(np.uint8).reshape(n, nb, 4)
+    return w.reshape(-1)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed decode MLP steps")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=10, help="rotating weight copies (85 MB each)")
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    return ap.parse_args()
+
+
+def timed_graph(graph, replays):
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def kernel_avg_ms(q4k, family):
+    launches, total, lo, hi = q4k.profile_query(family)
+    return (total / launches if launches else float("nan")), launches
+
+
+def decode_bench(args, dev):
+    import numpy as np
+    import torch
+    import mtlqwen_amd as q4k
+
+    M, K, N = 8, 4096, 12288
+    rng = np.random.default_rng(0x51A70001)
+    raw = [torch.from_numpy(make_q4k(rng, n, k)).to(dev) for n, k in ((N, K), (N, K), (K, N))]
+    sets = [[q4k.Weight(raw[i], *shape) for i, shape in enumerate(((N, K), (N, K), (K, N)))] for _ in range(args.sets)]
+    del raw
+    x = (torch.randn(M, K, device=dev, generator=torch.Generator(device=dev).manual_seed(0x51A71001)) * 0.5)
+    hidden = torch.randn(M, K, device=dev)
+    gate = torch.empty(M, N, device=dev)
+    counts = [1] * M
+
+    def step(s):
+        G, U, D = sets[s]
+        q4k.mlp(x, G, U, D, hidden, gate, M, query_counts=counts)
+
+    for i in range(max(args.warmup, len(sets))):
+        step(i % len(sets))
+    torch.cuda.synchronize()
+
+    # Per-launch event timing of the kernels (eager launches, same streams).
+    q4k.profile_enable(True)
+    for i in range(max(len(sets) * 5, 50)):
+        step(i % len(sets))
+    torch.cuda.synchronize()
+    gated_ms, gated_n = kernel_avg_ms(q4k, q4k.KERNEL_GEMV_GATED)
+    down_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMV)
+    stage_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_STAGE)
+    q4k.profile_enable(False)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for s in range(len(sets)):
+            step(s)
+    replays = max(1, args.steps // len(sets))
+    timed_graph(graph, max(1, args.warmup // len(sets)))
+    elapsed = timed_graph(graph, replays)
+    steps = replays * len(sets)
+    ms = elapsed / steps * 1e3
+
+    wbytes = 2 * q4k_bytes(N, K) + q4k_bytes(K, N)
+    act = 4 * (M * K + M * N)  # gate/up: x in, gate buffer out
+    act += 4 * (M * N + 2 * M * K)  # down: gate buffer in, residual in + out
+    step_bytes = wbytes + act
+    gated_bytes = 2 * q4k_bytes(N, K) + 4 * (M * K + M * N)
+    down_bytes = q4k_bytes(K, N) + 4 * (M * N + 2 * M * K)
+    return {
+        "ms_per_step": ms,
+        "steps": steps,
+        "value": step_bytes / (ms * 1e-3) / 1e9,
+        "step_bytes": step_bytes,
+        "gated": {"avg_us": gated_ms * 1e3, "launches": gated_n, "bytes": gated_bytes,
+                  "gbs": gated_bytes / (gated_ms * 1e-3) / 1e9},
+        "down": {"avg_us": down_ms * 1e3, "bytes": down_bytes, "gbs": down_bytes / (down_ms * 1e-3) / 1e9},
+        "stage_avg_us": stage_ms * 1e3,
+        "weight_sets_mb": len(sets) * wbytes / 1e6,
+    }
+
+
+def prefill_bench(args, dev):
+    import numpy as np
+    import torch
+    import mtlqwen_amd as q4k
+
+    M, K, N = 2048, 4096, 12288
+    rng = np.random.default_rng(0x51A70004)
+    G, U, D = (q4k.Weight(torch.from_numpy(make_q4k(rng, n, k)).to(dev), n, k) for n, k in ((N, K), (N, K), (K, N)))
+    x = torch.randn(M, K, device=dev, generator=torch.Generator(device=dev).manual_seed(0x51A71004))
+    gate = torch.empty(M, N, device=dev)
+    out = torch.empty(M, K, device=dev)
+    counts = [M]
+
+    def step():
+        q4k.mlp_gate_up(x, G, U, M, gate, query_counts=counts)
+        q4k.linear(gate, D, M, out, query_counts=counts)
+
+    step()
+    torch.cuda.synchronize()
+    q4k.profile_enable(True)
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    gemm_ms, gemm_n = kernel_avg_ms(q4k, q4k.KERNEL_GEMM)
+    q4k.profile_enable(False)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    timed_graph(graph, 2)
+    elapsed = timed_graph(graph, args.prefill_steps)
+    ms = elapsed / args.prefill_steps * 1e3
+    flop_gemm = 2.0 * M * N * K
+    return {
+        "ms_per_step": ms,
+        "tflops": 3 * flop_gemm / (ms * 1e-3) / 1e12,
+        "gemm_avg_us": gemm_ms * 1e3,
+        "gemm_launches": gemm_n,
+        "gemm_tflops": flop_gemm / (gemm_ms * 1e-3) / 1e12,
+    }
+
+
+def copy_ceiling(dev):
+    import torch
+    n = 1 << 28  # 1 GiB of fp32
+    a = torch.empty(n, device=dev)
+    b = torch.empty(n, device=dev)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reps = 10
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return 2 * 4 * n * reps / (time.perf_counter() - t0) / 1e9
+
+
+def cpu_baseline(args):
+    """The C oracle (a port of the reference's arithmetic; the reference itself
+    is Metal-only) on the config-1 MLP, on up to 16 host threads."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from q4k_ref import Oracle
+
+    oracle = Oracle()
+    M, K, N = 8, 4096, 12288
+    rng = np.random.default_rng(0x51A70001)
+    wg, wu, wd = make_q4k(rng, N, K), make_q4k(rng, N, K), make_q4k(rng, K, N)
+    x = (rng.standard_normal((M, K)) * 0.5).astype(np.float32)
+    hidden = rng.standard_normal((M, K)).astype(np.float32)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        g = oracle.mlp_gate_up(x, wg, wu, N, K, threads=threads)
+        oracle.linear(g, wd, K, N, aux=hidden, post=1, threads=threads)
+        iters += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    dt = (time.perf_counter() - t0) / iters
+    step_bytes = 2 * q4k_bytes(N, K) + q4k_bytes(K, N) + 4 * (M * K + M * N) + 4 * (M * N + 2 * M * K)
+    return {"value": step_bytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{iters} config-1 MLP steps (M=8, gate/up 4096->12288 x2 + down 12288->4096) "
+                      f"in {dt * iters:.1f} s, {dt * 1e3:.1f} ms/step"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the Q4_K path has no multi-GPU sharding "
+                                   "(a column/row-parallel design is described in DESIGN.md); run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    import mtlqwen_amd  # noqa: F401  (fails loudly if libq4k.so is missing)
+    dev = torch.device("cuda:0")
+
+    dec = decode_bench(args, dev)
+    pre = None if args.no_prefill else prefill_bench(args, dev)
+    copy_gbs = copy_ceiling(dev)
+    cpu = None if args.no_cpu else cpu_baseline(args)
+
+    g = dec["gated"]
+    line = {
+        "metric": "Q4_K linear: HBM GB/s at M=8 decode; TFLOP/s at M=2048 prefill",
+        "value": round(dec["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": dec["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 mfma, f32 accumulate (f32 activations)",
+        "data": "synthetic (seeded Q4_K weights per BASELINE config 0 recipe, N(0,1)*0.5 activations)",
+        "config": {
+            "workload": "config1: ragged decode M=8 (8 seqs x 1 token), Q4_K MLP: fused gate/up 4096->12288 x2 "
+                        "+ down 12288->4096 with in-place residual; HIP-graph replay",
+            "m": 8, "k": 4096, "n": 12288, "weight_sets": len(range(args.sets)),
+            "weight_bytes_per_step": dec["step_bytes"],
+        },
+        "roofline": {
+            "kernel": "q4k_gemv_kernel (fused gate/up, M=8, K=4096, N=12288)",
+            "bound": "hbm",
+            "achieved": round(g["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_us": round(g["avg_us"], 3),
+            "algorithmic_bytes": g["bytes"],
+        },
+        "kernels": {
+            "down_gemv_us": round(dec["down"]["avg_us"], 3),
+            "down_gemv_gbs": round(dec["down"]["gbs"], 1),
+            "stage_us": round(dec["stage_avg_us"], 3),
+        },
+        "copy_ceiling_gbs": round(copy_gbs, 1),
+        "cpu_baseline": cpu,
+    }
+    if pre:
+        line["prefill"] = {
+            "workload": "config4: M=2048 Q4_K MLP (gate, up with in-place SiLU gating, down) on MFMA GEMM",
+            "value": round(pre["tflops"], 2),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(pre["ms_per_step"], 4),
+            "roofline": {
+                "kernel": "q4k_gemm_kernel (M=2048, 206.16 GFLOP per launch)",
+                "bound": "mfma",
+                "achieved": round(pre["gemm_tflops"], 1),
+                "peak": FP16_DENSE_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(pre["gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4),
+                "avg_us": round(pre["gemm_avg_us"], 2),
+            },
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * q4k.h -- C ABI of the MI355X (gfx950) Q4_K linear() path.
+ *
+ * Drop-in for MTLQwen's quantized linear layer: the Weight type with its
+ * four-slot kernel cache, Ops::linear with its decode / prefill_small /
+ * prefill / gated-decode selection, the post 0/1/2 epilogues and the fused
+ * gate/up MLP, over a packed ragged batch of up to 8 sequences.
+ *
+ * Conventions
+ *  - Every entry point returns Q4K_OK (0) or a negative Q4K_E* code; the
+ *    message of the last failure on the calling thread is q4k_last_error().
+ *    (Mirrors the reference's create<T> error capture, runtime/engine.cpp:236-243.)
+ *  - stream is a hipStream_t passed as void* (NULL = the null stream).  Calls
+ *    enqueue work and return without synchronising.
+ *  - Activations are row-major: x [m, k], y and aux [m, n].  dtype selects
+ *    fp32 (Q4K_DTYPE_F32) or fp16 (Q4K_DTYPE_F16) for x, y and aux together.
+ *  - Calls on one device share that device's staging workspace: issue them
+ *    from one submitter / one stream at a time, as the reference engine does
+ *    (single worker thread, one command buffer per pass).
+ */
+#ifndef Q4K_H
+#define Q4K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q4K_OK 0
+#define Q4K_EINVAL (-1) /* null pointer, bad post code, bad dtype, bad count table */
+#define Q4K_ETYPE (-2)  /* ggml type other than Q4_K */
+#define Q4K_ESHAPE (-3) /* k % 256 != 0, n % 16 != 0, m out of range, byte count mismatch */
+#define Q4K_EALIAS (-4) /* x overlaps y (aux may alias y) */
+#define Q4K_EHIP (-5)   /* HIP runtime failure */
+#define Q4K_ENOMEM (-6)
+
+#define Q4K_GGML_TYPE_Q4_K 12u
+
+#define Q4K_DTYPE_F32 0u
+#define Q4K_DTYPE_F16 1u
+
+/* Epilogue ("post") codes: quant_linear.metal:146-147, forward.cpp:67-68. */
+#define Q4K_POST_STORE 0u /* y = acc */
+#define Q4K_POST_ADD 1u   /* y = acc + aux        (aux may be y: in-place residual) */
+#define Q4K_POST_GATE 2u  /* y = silu(aux) * acc  (aux may be y: gate buffer overwritten) */
+
+/* Kernel phases, the index of Weight::kernels[4] (model/qwen35/forward.cpp:52). */
+#define Q4K_PHASE_DECODE 0u
+#define Q4K_PHASE_PREFILL 1u
+#define Q4K_PHASE_PREFILL_SMALL 2u
+#define Q4K_PHASE_GATED_DECODE 3u
+
+/* Rows per query above which a pass is not a decode pass
+ * (model/qwen35/qwen35.hpp:22 maxDecodeRows). */
+#define Q4K_MAX_DECODE_ROWS 5u
+#define Q4K_MAX_QUERIES 8u   /* qwen35.hpp:22 maxBatchSequences */
+#define Q4K_MAX_LOGIT_ROWS 64u /* qwen35.hpp:23 maxLogitRows */
+
+typedef struct q4k_weight q4k_weight;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* q4k_last_error(void);
+
+/* Upload one GGUF tensor of type Q4_K (n rows of k/256 block_q4_K records,
+ * 144 B each; ggml ne[0] = k, ne[1] = n) to device `device`.  The bytes are
+ * re-laid out for the kernels during the upload; the caller's buffer is not
+ * retained.  Replaces the zero-copy Weight view built by loadWeights
+ * (model/qwen35/forward.cpp:12-23, qwen35.hpp:34-37). */
+int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device, q4k_weight** out);
+
+/* Same, from bytes already in device memory of `device` (GGUF order). */
+int q4k_weight_create_from_device(const void* gguf_device_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device,
+                                  void* stream, q4k_weight** out);
+
+int q4k_weight_destroy(q4k_weight* w);
+
+/* n, k, device bytes held. */
+int q4k_weight_info(const q4k_weight* w, uint32_t* n, uint32_t* k, uint64_t* device_bytes);
+
+/* Name of the kernel cached in slot `phase` ("" if the slot was never
+ * resolved).  Mirrors Weight::kernels[phase] (qwen35.hpp:29-37). */
+int q4k_weight_kernel_name(const q4k_weight* w, uint32_t phase, char* buf, size_t buflen);
+
+/* Resolve slot `phase` without launching anything: the engine's prepare
+ * passes (runtime/engine.cpp:104-108) fill every slot ahead of the first pass. */
+int q4k_weight_prepare(q4k_weight* w, uint32_t phase);
+
+/* Ops::linear (model/qwen35/forward.cpp:51-70).
+ * y[m, n] = post(x[m, k] . W^T, aux).  query_counts/nqueries describe the
+ * packed ragged batch (rows per sequence, summing to m); they select the
+ * phase exactly as the reference does: decode iff every query has <= 5 rows,
+ * else prefill_small iff m <= 8, else prefill.  query_counts == NULL means
+ * a single query of m rows.  `aux` is required for post 1 and 2 and may
+ * equal y; x must not overlap y. */
+int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts,
+               uint32_t nqueries, uint32_t post, uint32_t dtype);
+
+/* Gated MLP projection (model/qwen35/forward.cpp:115-118).
+ * Decode passes: one fused gate/up kernel, y = silu(x.Wg^T) * (x.Wu^T)
+ * (fused_kernels.metal:44-78).  Other passes: the reference's two calls,
+ * gate with post 0 into y, then up with post 2 over y in place.
+ * y is the gate buffer [m, n]. */
+int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x, void* y, uint32_t m, const uint32_t* query_counts,
+                    uint32_t nqueries, uint32_t dtype);
+
+/* Phase Ops::linear would use for this batch (forward.cpp:52,190). */
+int q4k_select_phase(const uint32_t* query_counts, uint32_t nqueries, uint32_t m, int gated, uint32_t* phase);
+
+/* Ragged packing of forward.cpp:171-191: start[i] = rows before query i,
+ * logit[i] = sampled rows before query i.  samples may be NULL (all zero).
+ * Writes total rows and total sampled rows. */
+int q4k_pack_queries(const uint32_t* counts, const uint32_t* samples, uint32_t nqueries, uint32_t* start, uint32_t* logit, uint32_t* rows,
+                     uint32_t* logit_rows);
+
+/* LM-head row gather (native_ops.metal:6-15 rms_norm_gather's row choice,
+ * batch.hpp:25-29 queryLogit): out row r = x row
+ * start + count - samples + (r - logit) of the query owning logit row r,
+ * for r < sum(samples) (<= 64).  Copies k elements per row on `stream`. */
+int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const uint32_t* counts, const uint32_t* samples, uint32_t nqueries,
+                    uint32_t dtype, uint32_t* rows_out);
+
+/* Kernel families, for q4k_profile_query. */
+#define Q4K_KERNEL_STAGE 0u      /* activation staging (fp16 + row scale) */
+#define Q4K_KERNEL_GEMV 1u       /* MFMA GEMV, phases 0/2 and small prefill */
+#define Q4K_KERNEL_GEMV_GATED 2u /* fused gate/up GEMV, phase 3 */
+#define Q4K_KERNEL_GEMM 3u       /* LDS-tiled MFMA GEMM, phase 1 */
+
+/* Event timing of every kernel launch (no counterpart in the reference, whose
+ * method is paired A/B timing, agents/KERNELS.md:13-21).  While enabled, each
+ * launch is bracketed by hipEvents recorded on the launch's stream.
+ * q4k_profile_enable(1) clears earlier records; q4k_profile_query
+ * synchronises the recorded events and reports launches and summed, minimum
+ * and maximum durations in milliseconds for one kernel family. */
+int q4k_profile_enable(int on);
+int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, double* min_ms, double* max_ms);
+
+/* The device layout as a host transform (for tests and tooling):
+ * GGUF-order block_q4_K bytes <-> the kernels' tiled order.  Both buffers are
+ * n * (k / 256) * 144 bytes. */
+int q4k_relayout_host(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k);
+int q4k_unrelayout_host(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

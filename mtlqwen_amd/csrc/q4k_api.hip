@@ -1,0 +1,631 @@
+// Host side of the Q4_K linear() path: the C ABI declared in include/q4k.h.
+//
+// Mirrors the reference's Weight / Ops::linear surface
+// (model/qwen35/qwen35.hpp:29-37, model/qwen35/forward.cpp:51-70): a weight
+// owns its device bytes plus a four-slot kernel cache indexed by phase, and
+// linear() picks the phase from the packed batch's per-query row counts.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/q4k.h"
+#include "q4k_internal.h"
+
+using namespace q4k;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(Q4K_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define Q4K_TRY_HIP(expr, what)            \
+  do {                                     \
+    hipError_t e_ = (expr);                \
+    if (e_ != hipSuccess)                  \
+      return hip_fail(e_, what);           \
+  } while (0)
+
+enum KernelKind : int { kNone = 0, kGemv = 1, kGemvGated = 2, kGemm = 3 };
+
+// One resolved slot of Weight::kernels[4] (qwen35.hpp:29-32): which kernel
+// family serves the phase, and its name for introspection.
+struct Kernel {
+  KernelKind kind = kNone;
+  std::string name;
+};
+
+// Per-device staging workspace for activations (fp16 copy + row scales).
+// Outgrown buffers are retired, not freed: a HIP graph captured earlier may
+// still name them.  Growth is bounded by the largest m * k staged.
+struct Workspace {
+  std::mutex mu;
+  _Float16* x = nullptr;
+  size_t x_elems = 0;
+  float* scale = nullptr;
+  size_t scale_elems = 0;
+  std::vector<void*> retired;
+};
+
+Workspace g_ws[64];
+
+// Launch timing (q4k_profile_enable / q4k_profile_query).
+struct Profiler {
+  std::mutex mu;
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events[4];
+
+  void clear() {
+    for (auto& v : events) {
+      for (auto& e : v) {
+        (void)hipEventDestroy(e.first);
+        (void)hipEventDestroy(e.second);
+      }
+      v.clear();
+    }
+  }
+};
+
+Profiler g_prof;
+
+// Brackets one kernel launch with events when profiling is enabled.
+struct LaunchTimer {
+  hipEvent_t start = nullptr, stop = nullptr;
+  hipStream_t stream;
+  int family;
+  LaunchTimer(hipStream_t s, int fam) : stream(s), family(fam) {
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    if (!g_prof.on)
+      return;
+    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) {
+      start = stop = nullptr;
+      return;
+    }
+    (void)hipEventRecord(start, stream);
+  }
+  ~LaunchTimer() {
+    if (!start)
+      return;
+    (void)hipEventRecord(stop, stream);
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    g_prof.events[family].emplace_back(start, stop);
+  }
+};
+
+}  // namespace
+
+struct q4k_weight {
+  int device = 0;
+  uint32_t n = 0, k = 0, type = 0;
+  uint8_t* data = nullptr;
+  size_t bytes = 0;
+  Kernel kernels[4];
+};
+
+namespace {
+
+size_t q4k_bytes(uint32_t n, uint32_t k) {
+  return (size_t)n * (k / 256) * kBlockBytes;
+}
+
+int check_shape(uint32_t n, uint32_t k, uint32_t type, size_t bytes) {
+  if (type != Q4K_GGML_TYPE_Q4_K)
+    return fail(Q4K_ETYPE, "unsupported ggml type %u (only Q4_K = 12)", type);
+  if (n == 0 || k == 0 || k % 256 != 0)
+    return fail(Q4K_ESHAPE, "k must be a positive multiple of 256 (got k=%u, n=%u)", k, n);
+  if (n % 16 != 0)
+    return fail(Q4K_ESHAPE, "n must be a multiple of 16 (got %u)", n);
+  if ((size_t)(k / 256) * kTileBlockBytes > 0x7fffffffull / 16)
+    return fail(Q4K_ESHAPE, "k too large (%u)", k);
+  if (bytes != q4k_bytes(n, k))
+    return fail(Q4K_ESHAPE, "byte count %zu does not match n=%u k=%u (expected %zu)", bytes, n, k, q4k_bytes(n, k));
+  return Q4K_OK;
+}
+
+inline uint32_t swap_middle_bytes(uint32_t v) {
+  return (v & 0xff0000ffu) | ((v & 0x0000ff00u) << 8) | ((v & 0x00ff0000u) >> 8);
+}
+
+// Host form of the tiled layout (q4k_internal.h); `forward` selects
+// GGUF -> tiled, else tiled -> GGUF.  Both directions are a byte permutation.
+void relayout(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, bool forward) {
+  const uint32_t nb = k / 256;
+  for (uint32_t c = 0; c < n / 16; ++c)
+    for (uint32_t b = 0; b < nb; ++b) {
+      const size_t tb = ((size_t)c * nb + b) * kTileBlockBytes;
+      for (uint32_t i = 0; i < 16; ++i) {
+        const size_t blk = ((size_t)(16 * c + i) * nb + b) * kBlockBytes;
+        for (uint32_t j = 0; j < 16; ++j) {
+          if (forward)
+            dst[tb + kHeaderOffset + 16 * i + j] = src[blk + j];
+          else
+            dst[blk + j] = src[tb + kHeaderOffset + 16 * i + j];
+        }
+        for (uint32_t g = 0; g < 4; ++g)
+          for (uint32_t h = 0; h < 2; ++h)
+            for (uint32_t w = 0; w < 4; ++w) {
+              const size_t qoff = blk + 16 + 32 * g + 16 * h + 4 * w;
+              const size_t toff = tb + h * kSlabBytes + 16 * (16 * g + i) + 4 * w;
+              uint32_t v;
+              if (forward) {
+                std::memcpy(&v, src + qoff, 4);
+                v = swap_middle_bytes(v);
+                std::memcpy(dst + toff, &v, 4);
+              } else {
+                std::memcpy(&v, src + toff, 4);
+                v = swap_middle_bytes(v);
+                std::memcpy(dst + qoff, &v, 4);
+              }
+            }
+      }
+    }
+}
+
+// forward.cpp:52 with the decode flag accumulated as in forward.cpp:190.
+uint32_t phase_of(const uint32_t* counts, uint32_t nq, uint32_t m, bool gated) {
+  bool decode = true;
+  if (counts) {
+    for (uint32_t i = 0; i < nq; ++i)
+      decode = decode && counts[i] <= Q4K_MAX_DECODE_ROWS;
+  } else {
+    decode = m <= Q4K_MAX_DECODE_ROWS;
+  }
+  return decode ? (gated ? Q4K_PHASE_GATED_DECODE : Q4K_PHASE_DECODE) : (m <= 8 ? Q4K_PHASE_PREFILL_SMALL : Q4K_PHASE_PREFILL);
+}
+
+int check_counts(const uint32_t* counts, uint32_t nq, uint32_t m) {
+  if (!counts)
+    return nq == 0 ? Q4K_OK : fail(Q4K_EINVAL, "query_counts is NULL but nqueries=%u", nq);
+  if (nq == 0 || nq > Q4K_MAX_QUERIES)
+    return fail(Q4K_EINVAL, "nqueries must be in [1, %u] (got %u)", Q4K_MAX_QUERIES, nq);
+  uint64_t sum = 0;
+  for (uint32_t i = 0; i < nq; ++i)
+    sum += counts[i];
+  if (sum != m)
+    return fail(Q4K_EINVAL, "query counts sum to %llu but m=%u", (unsigned long long)sum, m);
+  return Q4K_OK;
+}
+
+// The kernel family each phase resolves to.  Decode-shaped phases (0, 2, 3)
+// run the MFMA GEMV; prefill (1) runs the LDS-tiled MFMA GEMM, whose slot also
+// serves prefill batches small enough for the GEMV (<= 48 rows) with the GEMV
+// launch shape (run_linear) -- same arithmetic, lower latency.
+Kernel& resolve(q4k_weight* w, uint32_t phase) {
+  Kernel& k = w->kernels[phase];
+  if (k.kind == kNone) {
+    const char* suffix[] = {"decode", "prefill", "prefill_small", "gate_up_decode"};
+    k.kind = phase == Q4K_PHASE_GATED_DECODE ? kGemvGated : phase == Q4K_PHASE_PREFILL ? kGemm : kGemv;
+    k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + "q4_k_k" + std::to_string(w->k) + "_n" + std::to_string(w->n) +
+             "_" + suffix[phase] + (k.kind == kGemm ? "_mfma32x32x16" : "_mfma16x16x32");
+  }
+  return k;
+}
+
+Workspace& workspace(int device) {
+  return g_ws[device & 63];
+}
+
+// Grows the device's staging buffers to hold `rows` x `k` fp16 plus row scales.
+int ensure_workspace(Workspace& ws, int device, size_t rows, size_t k) {
+  const size_t need = rows * k, need_s = rows < 64 ? 64 : rows;
+  if (ws.x_elems >= need && ws.scale_elems >= need_s)
+    return Q4K_OK;
+  if (ws.x_elems < need) {
+    if (ws.x)
+      ws.retired.push_back(ws.x);
+    ws.x = nullptr;
+    ws.x_elems = 0;
+    if (hipMalloc(&ws.x, need * sizeof(_Float16)) != hipSuccess)
+      return fail(Q4K_ENOMEM, "cannot allocate %zu-byte activation workspace on device %d", need * sizeof(_Float16), device);
+    ws.x_elems = need;
+  }
+  if (ws.scale_elems < need_s) {
+    if (ws.scale)
+      ws.retired.push_back(ws.scale);
+    ws.scale = nullptr;
+    ws.scale_elems = 0;
+    if (hipMalloc(&ws.scale, need_s * sizeof(float)) != hipSuccess)
+      return fail(Q4K_ENOMEM, "cannot allocate row-scale workspace on device %d", device);
+    ws.scale_elems = need_s;
+  }
+  return Q4K_OK;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+int set_device(int device) {
+  int cur = -1;
+  Q4K_TRY_HIP(hipGetDevice(&cur), "hipGetDevice");
+  if (cur != device)
+    Q4K_TRY_HIP(hipSetDevice(device), "hipSetDevice");
+  return Q4K_OK;
+}
+
+// One projection (phase already chosen) on the weight's device.
+int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m, uint32_t post, uint32_t dtype,
+               uint32_t phase) {
+  Kernel& kern = resolve(w, phase);
+  if (wu)
+    resolve(wu, phase);
+  Workspace& ws = workspace(w->device);
+  std::lock_guard<std::mutex> lock(ws.mu);
+  const bool gemv = kern.kind != kGemm || m <= 16u * kGemvMaxRowTiles;
+  const size_t rows = gemv ? (size_t)((m + 15) / 16) * 16 : m;
+  int rc = ensure_workspace(ws, w->device, rows, w->k);
+  if (rc)
+    return rc;
+  {
+    LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, ws.scale, (int)m, (int)w->k, gemv), "stage_x launch");
+  }
+  if (gemv) {
+    GemvArgs a;
+    a.w = w->data;
+    a.wu = wu ? wu->data : w->data;
+    a.xf = ws.x;
+    a.rowscale = ws.scale;
+    a.y = y;
+    a.aux = aux;
+    a.m = (int)m;
+    a.n = (int)w->n;
+    a.k = (int)w->k;
+    a.nb = (int)(w->k / 256);
+    a.post = (int)post;
+    LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
+    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape((int)m, (int)w->n, wu != nullptr), wu != nullptr), "gemv launch");
+  } else {
+    GemmArgs a;
+    a.w = w->data;
+    a.xh = ws.x;
+    a.rowscale = ws.scale;
+    a.y = y;
+    a.aux = aux;
+    a.m = (int)m;
+    a.n = (int)w->n;
+    a.k = (int)w->k;
+    a.nb = (int)(w->k / 256);
+    a.post = (int)post;
+    LaunchTimer timer(stream, Q4K_KERNEL_GEMM);
+    Q4K_TRY_HIP(launch_gemm(stream, a, (int)dtype), "gemm launch");
+  }
+  return Q4K_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* q4k_last_error(void) {
+  return g_error.c_str();
+}
+
+int q4k_relayout_host(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k) {
+  if (!gguf_bytes || !tiled)
+    return fail(Q4K_EINVAL, "null buffer");
+  int rc = check_shape(n, k, Q4K_GGML_TYPE_Q4_K, q4k_bytes(n, k));
+  if (rc)
+    return rc;
+  relayout(static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(tiled), n, k, true);
+  return Q4K_OK;
+}
+
+int q4k_unrelayout_host(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k) {
+  if (!gguf_bytes || !tiled)
+    return fail(Q4K_EINVAL, "null buffer");
+  int rc = check_shape(n, k, Q4K_GGML_TYPE_Q4_K, q4k_bytes(n, k));
+  if (rc)
+    return rc;
+  relayout(static_cast<const uint8_t*>(tiled), static_cast<uint8_t*>(gguf_bytes), n, k, false);
+  return Q4K_OK;
+}
+
+int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device, q4k_weight** out) {
+  if (!out)
+    return fail(Q4K_EINVAL, "out is NULL");
+  *out = nullptr;
+  if (!gguf_bytes)
+    return fail(Q4K_EINVAL, "gguf_bytes is NULL");
+  int rc = check_shape(n, k, ggml_type, bytes);
+  if (rc)
+    return rc;
+  if (device < 0 || device > 63)
+    return fail(Q4K_EINVAL, "bad device %d", device);
+  rc = set_device(device);
+  if (rc)
+    return rc;
+  std::vector<uint8_t> tiled(bytes);
+  relayout(static_cast<const uint8_t*>(gguf_bytes), tiled.data(), n, k, true);
+  q4k_weight* w = new (std::nothrow) q4k_weight;
+  if (!w)
+    return fail(Q4K_ENOMEM, "host allocation failed");
+  w->device = device;
+  w->n = n;
+  w->k = k;
+  w->type = ggml_type;
+  w->bytes = bytes;
+  if (hipMalloc(&w->data, bytes) != hipSuccess) {
+    delete w;
+    return fail(Q4K_ENOMEM, "cannot allocate %zu bytes of weights on device %d", bytes, device);
+  }
+  hipError_t e = hipMemcpy(w->data, tiled.data(), bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(w->data);
+    delete w;
+    return hip_fail(e, "weight upload");
+  }
+  *out = w;
+  return Q4K_OK;
+}
+
+int q4k_weight_create_from_device(const void* gguf_device_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device,
+                                  void* stream, q4k_weight** out) {
+  if (!out)
+    return fail(Q4K_EINVAL, "out is NULL");
+  *out = nullptr;
+  if (!gguf_device_bytes)
+    return fail(Q4K_EINVAL, "gguf_device_bytes is NULL");
+  int rc = check_shape(n, k, ggml_type, bytes);
+  if (rc)
+    return rc;
+  if (device < 0 || device > 63)
+    return fail(Q4K_EINVAL, "bad device %d", device);
+  rc = set_device(device);
+  if (rc)
+    return rc;
+  q4k_weight* w = new (std::nothrow) q4k_weight;
+  if (!w)
+    return fail(Q4K_ENOMEM, "host allocation failed");
+  w->device = device;
+  w->n = n;
+  w->k = k;
+  w->type = ggml_type;
+  w->bytes = bytes;
+  if (hipMalloc(&w->data, bytes) != hipSuccess) {
+    delete w;
+    return fail(Q4K_ENOMEM, "cannot allocate %zu bytes of weights on device %d", bytes, device);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k);
+  if (e == hipSuccess)
+    e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    (void)hipFree(w->data);
+    delete w;
+    return hip_fail(e, "device relayout");
+  }
+  *out = w;
+  return Q4K_OK;
+}
+
+int q4k_weight_destroy(q4k_weight* w) {
+  if (!w)
+    return Q4K_OK;
+  int cur = -1;
+  (void)hipGetDevice(&cur);
+  if (cur != w->device)
+    (void)hipSetDevice(w->device);
+  hipError_t e = hipFree(w->data);
+  if (cur != w->device && cur >= 0)
+    (void)hipSetDevice(cur);
+  delete w;
+  return e == hipSuccess ? Q4K_OK : hip_fail(e, "hipFree(weight)");
+}
+
+int q4k_weight_info(const q4k_weight* w, uint32_t* n, uint32_t* k, uint64_t* device_bytes) {
+  if (!w)
+    return fail(Q4K_EINVAL, "weight is NULL");
+  if (n)
+    *n = w->n;
+  if (k)
+    *k = w->k;
+  if (device_bytes)
+    *device_bytes = w->bytes;
+  return Q4K_OK;
+}
+
+int q4k_weight_kernel_name(const q4k_weight* w, uint32_t phase, char* buf, size_t buflen) {
+  if (!w || !buf || buflen == 0)
+    return fail(Q4K_EINVAL, "null argument");
+  if (phase > 3)
+    return fail(Q4K_EINVAL, "phase %u out of range", phase);
+  std::snprintf(buf, buflen, "%s", w->kernels[phase].name.c_str());
+  return Q4K_OK;
+}
+
+int q4k_weight_prepare(q4k_weight* w, uint32_t phase) {
+  if (!w)
+    return fail(Q4K_EINVAL, "weight is NULL");
+  if (phase > 3)
+    return fail(Q4K_EINVAL, "phase %u out of range", phase);
+  resolve(w, phase);
+  return Q4K_OK;
+}
+
+int q4k_select_phase(const uint32_t* query_counts, uint32_t nqueries, uint32_t m, int gated, uint32_t* phase) {
+  if (!phase)
+    return fail(Q4K_EINVAL, "phase is NULL");
+  int rc = check_counts(query_counts, nqueries, m);
+  if (rc)
+    return rc;
+  *phase = phase_of(query_counts, nqueries, m, gated != 0);
+  return Q4K_OK;
+}
+
+int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts, uint32_t nqueries,
+               uint32_t post, uint32_t dtype) {
+  if (!w)
+    return fail(Q4K_EINVAL, "weight is NULL");
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (post > Q4K_POST_GATE)
+    return fail(Q4K_EINVAL, "bad post code %u", post);
+  if (m == 0)
+    return fail(Q4K_ESHAPE, "m must be positive");
+  if (!x || !y)
+    return fail(Q4K_EINVAL, "x and y must be non-NULL");
+  if (post != Q4K_POST_STORE && !aux)
+    return fail(Q4K_EINVAL, "post %u needs aux", post);
+  int rc = check_counts(query_counts, nqueries, m);
+  if (rc)
+    return rc;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (overlaps(x, (size_t)m * w->k * es, y, (size_t)m * w->n * es))
+    return fail(Q4K_EALIAS, "x must not overlap y");
+  if (aux && aux != y && overlaps(aux, (size_t)m * w->n * es, y, (size_t)m * w->n * es))
+    return fail(Q4K_EALIAS, "aux must be y itself or disjoint from it");
+  const uint32_t phase = phase_of(query_counts, nqueries, m, false);
+  if (phase != Q4K_PHASE_PREFILL && m > 16u * kGemvMaxRowTiles)
+    return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
+  rc = set_device(w->device);
+  if (rc)
+    return rc;
+  return run_linear(static_cast<hipStream_t>(stream), w, nullptr, x, y, aux, m, post, dtype, phase);
+}
+
+int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x, void* y, uint32_t m, const uint32_t* query_counts,
+                    uint32_t nqueries, uint32_t dtype) {
+  if (!wg || !wu)
+    return fail(Q4K_EINVAL, "gate and up weights must be non-NULL");
+  if (wg->n != wu->n || wg->k != wu->k || wg->device != wu->device)
+    return fail(Q4K_ESHAPE, "gate (%ux%u) and up (%ux%u) weights differ", wg->n, wg->k, wu->n, wu->k);
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (m == 0)
+    return fail(Q4K_ESHAPE, "m must be positive");
+  if (!x || !y)
+    return fail(Q4K_EINVAL, "x and y must be non-NULL");
+  int rc = check_counts(query_counts, nqueries, m);
+  if (rc)
+    return rc;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (overlaps(x, (size_t)m * wg->k * es, y, (size_t)m * wg->n * es))
+    return fail(Q4K_EALIAS, "x must not overlap y");
+  rc = set_device(wg->device);
+  if (rc)
+    return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t phase = phase_of(query_counts, nqueries, m, true);
+  if (phase == Q4K_PHASE_GATED_DECODE) {
+    if (m > 16u * kGemvMaxRowTiles)
+      return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
+    return run_linear(s, wg, wu, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase);
+  }
+  // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in place.
+  rc = run_linear(s, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase);
+  if (rc)
+    return rc;
+  return run_linear(s, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase);
+}
+
+int q4k_profile_enable(int on) {
+  std::lock_guard<std::mutex> lock(g_prof.mu);
+  if (on)
+    g_prof.clear();
+  g_prof.on = on != 0;
+  return Q4K_OK;
+}
+
+int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, double* min_ms, double* max_ms) {
+  if (kernel > 3)
+    return fail(Q4K_EINVAL, "kernel family %u out of range", kernel);
+  std::lock_guard<std::mutex> lock(g_prof.mu);
+  double total = 0.0, lo = 0.0, hi = 0.0;
+  uint32_t count = 0;
+  for (auto& e : g_prof.events[kernel]) {
+    Q4K_TRY_HIP(hipEventSynchronize(e.second), "hipEventSynchronize");
+    float ms = 0.0f;
+    Q4K_TRY_HIP(hipEventElapsedTime(&ms, e.first, e.second), "hipEventElapsedTime");
+    total += ms;
+    lo = count == 0 ? ms : (ms < lo ? ms : lo);
+    hi = count == 0 ? ms : (ms > hi ? ms : hi);
+    ++count;
+  }
+  if (launches)
+    *launches = count;
+  if (total_ms)
+    *total_ms = total;
+  if (min_ms)
+    *min_ms = lo;
+  if (max_ms)
+    *max_ms = hi;
+  return Q4K_OK;
+}
+
+int q4k_pack_queries(const uint32_t* counts, const uint32_t* samples, uint32_t nqueries, uint32_t* start, uint32_t* logit, uint32_t* rows,
+                     uint32_t* logit_rows) {
+  if (!counts || !start || !logit)
+    return fail(Q4K_EINVAL, "null argument");
+  if (nqueries > Q4K_MAX_QUERIES)
+    return fail(Q4K_EINVAL, "at most %u queries (got %u)", Q4K_MAX_QUERIES, nqueries);
+  uint64_t r = 0, l = 0;
+  for (uint32_t i = 0; i < nqueries; ++i) {
+    if (samples && samples[i] > counts[i])
+      return fail(Q4K_EINVAL, "query %u samples %u rows but has %u", i, samples[i], counts[i]);
+    start[i] = (uint32_t)r;
+    logit[i] = (uint32_t)l;
+    l += samples ? samples[i] : 0u;
+    r += counts[i];
+    if (r > 0xffffffffull)
+      return fail(Q4K_EINVAL, "row count overflows 32 bits");
+  }
+  if (rows)
+    *rows = (uint32_t)r;
+  if (logit_rows)
+    *logit_rows = (uint32_t)l;
+  return Q4K_OK;
+}
+
+int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const uint32_t* counts, const uint32_t* samples, uint32_t nqueries,
+                    uint32_t dtype, uint32_t* rows_out) {
+  if (!x || !out || !counts || !samples)
+    return fail(Q4K_EINVAL, "null argument");
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (k == 0)
+    return fail(Q4K_ESHAPE, "k must be positive");
+  uint32_t start[Q4K_MAX_QUERIES], logit[Q4K_MAX_QUERIES], rows = 0, nlogit = 0;
+  int rc = q4k_pack_queries(counts, samples, nqueries, start, logit, &rows, &nlogit);
+  if (rc)
+    return rc;
+  if (nlogit > Q4K_MAX_LOGIT_ROWS)
+    return fail(Q4K_EINVAL, "%u sampled rows exceed %u", nlogit, Q4K_MAX_LOGIT_ROWS);
+  GatherIndex idx;
+  idx.rows = nlogit;
+  for (uint32_t r = 0; r < nlogit; ++r) {
+    // batch.hpp:25-29: first query with samples whose logit range holds r.
+    uint32_t q = 0;
+    while (!samples[q] || r >= logit[q] + samples[q])
+      ++q;
+    idx.src[r] = start[q] + counts[q] - samples[q] + (r - logit[q]);
+  }
+  if (rows_out)
+    *rows_out = nlogit;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (overlaps(x, (size_t)rows * k * es, out, (size_t)nlogit * k * es))
+    return fail(Q4K_EALIAS, "out must not overlap x");
+  Q4K_TRY_HIP(launch_gather(static_cast<hipStream_t>(stream), x, out, (int)k, (int)dtype, idx), "gather launch");
+  return Q4K_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,84 @@
+// Internal interface between the C-ABI host code (q4k_api.hip) and the
+// kernels (q4k_kernels.hip).  Not installed; the public surface is include/q4k.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace q4k {
+
+// ---- device weight layout --------------------------------------------------
+// GGUF stores row n as k/256 consecutive 144-byte block_q4_K records
+// (d fp16 @0, dmin fp16 @2, 12 packed 6-bit scale/min bytes @4, 128 quant
+// bytes @16).  The device copy groups 16 consecutive rows ("column tile" c)
+// and, for each 256-element block b, stores the 16 records of that tile as one
+// 2304-byte "tile-block" at ((c * nb) + b) * 2304:
+//   [0, 1024)     slab 0: lane l = 16*g + i holds quant bytes 32g..32g+15 of row 16c+i
+//   [1024, 2048)  slab 1: lane l holds quant bytes 32g+16..32g+31 of row 16c+i
+//   [2048, 2304)  row 16c+i's 16 header bytes at 2048 + 16i (unchanged)
+// Within each 4-byte word of a slab the two middle bytes are swapped, so that
+// masking a word with 0x000F000F yields the low nibbles of two *consecutive*
+// quant bytes.  A wave reads a whole slab with one fully-contiguous 16-byte
+// load per lane, and the lane order is the B-operand order of
+// v_mfma_f32_16x16x32_f16 (column = lane % 16, k-group = lane / 16).
+// The byte count is unchanged: 144 bytes per 256 weights.
+constexpr int kTileN = 16;
+constexpr int kBlockBytes = 144;
+constexpr int kTileBlockBytes = kTileN * kBlockBytes;  // 2304
+constexpr int kSlabBytes = 1024;
+constexpr int kHeaderOffset = 2048;
+
+// Rows of a GEMV call are padded to 16-row MFMA tiles; the GEMV handles up to
+// kGemvMaxRowTiles of them (48 rows: the 8 x 5 decode rows of the reference).
+constexpr int kGemvMaxRowTiles = 3;
+
+enum Dtype : int { kF32 = 0, kF16 = 1 };
+
+struct GemvArgs {
+  const uint8_t* w;       // tiled weights (gate weights when gated)
+  const uint8_t* wu;      // up weights when gated, else unused
+  const _Float16* xf;     // staged activations, fragment order
+  const float* rowscale;  // per-row power-of-two unscale factor
+  void* y;
+  const void* aux;
+  int m, n, k, nb, post;
+};
+
+struct GemmArgs {
+  const uint8_t* w;
+  const _Float16* xh;  // staged activations, row-major [m, k]
+  const float* rowscale;
+  void* y;
+  const void* aux;
+  int m, n, k, nb, post;
+};
+
+struct GatherIndex {
+  uint32_t rows;
+  uint32_t src[64];
+};
+
+// Stage x [m, k] (fp32 or fp16) as fp16 scaled by a per-row power of two
+// (so rows with |x| beyond the fp16 range stay finite); rowscale[r] receives
+// the factor that undoes the scaling.  frag selects the GEMV fragment order,
+// otherwise row-major.
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, bool frag);
+
+// Launch geometry of the GEMV: 16-row tiles of activations, 16-column tiles
+// of weights per workgroup, waves per workgroup (each takes 1/waves of K).
+struct GemvShape {
+  int row_tiles = 1, tiles = 1, waves = 8;
+};
+GemvShape gemv_shape(int m, int n, bool gated);
+
+// GEMV for m <= 48.
+hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated);
+
+hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype);
+
+hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx);
+
+// Device-side GGUF -> tiled re-layout (src and dst are device buffers).
+hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
+
+}  // namespace q4k

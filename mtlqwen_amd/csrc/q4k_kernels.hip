@@ -1,0 +1,559 @@
+// Q4_K linear() kernels for gfx950 (MI355X / CDNA4).
+//
+//  stage_x_kernel   activations -> fp16 with a per-row power-of-two scale
+//  q4k_gemv_kernel  decode-shaped (m <= 48) GEMV on v_mfma_f32_16x16x32_f16,
+//                   optionally fused gate/up with the SiLU(gate)*up epilogue
+//  q4k_gemm_kernel  prefill-shaped GEMM: Q4_K tiles dequantised to fp16 in LDS,
+//                   v_mfma_f32_32x32x16_f16, fp32 accumulation, post 0/1/2
+//  gather_rows_kernel, relayout_kernel
+//
+// Reference semantics: backend/metal/kernel/quant_linear.metal (Q4_K parts)
+// and backend/metal/kernel/fused_kernels.metal:11-78.
+#include <float.h>
+#include <hip/hip_runtime.h>
+
+#include "q4k_internal.h"
+
+namespace q4k {
+namespace {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float silu(float g) {
+  return g / (1.0f + expf(-g));
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+__device__ __forceinline__ float round_half(float v) {
+  return (float)(_Float16)v;
+}
+
+template <typename T>
+__device__ __forceinline__ float load_elem(const T* p, size_t i) {
+  return (float)p[i];
+}
+
+template <typename T>
+__device__ __forceinline__ void store_elem(T* p, size_t i, float v) {
+  p[i] = (T)v;
+}
+
+// Loads 8 consecutive activations as fp32.
+__device__ __forceinline__ void load8(const float* p, float* v) {
+  f4_t a = *reinterpret_cast<const f4_t*>(p), b = *reinterpret_cast<const f4_t*>(p + 4);
+  v[0] = a[0], v[1] = a[1], v[2] = a[2], v[3] = a[3], v[4] = b[0], v[5] = b[1], v[6] = b[2], v[7] = b[3];
+}
+
+__device__ __forceinline__ void load8(const _Float16* p, float* v) {
+  h8_t a = *reinterpret_cast<const h8_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    v[i] = (float)a[i];
+}
+
+// Scales and mins of sub-blocks 2g and 2g+1 from the three packed words of a
+// block header (quant_linear.metal:12-20, taken four bytes at a time).
+__device__ __forceinline__ void scale_min_pair(u4_t hd, int g, uint32_t& sc0, uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
+  const uint32_t sh = 16u * (uint32_t)(g & 1);
+  const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
+  if (g < 2) {
+    sc0 = a & 63u;
+    sc1 = (a >> 8) & 63u;
+    m0 = b & 63u;
+    m1 = (b >> 8) & 63u;
+  } else {
+    sc0 = (c & 15u) | ((a >> 2) & 0x30u);
+    sc1 = ((c >> 8) & 15u) | ((a >> 10) & 0x30u);
+    m0 = ((c >> 4) & 15u) | ((b >> 2) & 0x30u);
+    m1 = ((c >> 12) & 15u) | ((b >> 10) & 0x30u);
+  }
+}
+
+// Eight quants of one slab pair as exact fp16 products q * sc.
+// (w & mask) | 0x6400 is the fp16 value 1024 + q (low nibble, mask 0x000F) or
+// 1024 + 16q (high nibble, mask 0x00F0); one fused multiply-add with
+// (sc, -1024 sc) or (sc/16, -64 sc) leaves q*sc <= 945, exact in fp16.
+__device__ __forceinline__ h8_t quant_times_scale(uint32_t wa, uint32_t wb, uint32_t mask, h2_t mul, h2_t add) {
+  const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+  h2_t v0 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wa & mask) | 0x64006400u), mul, add);
+  h2_t v1 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wa8 & mask) | 0x64006400u), mul, add);
+  h2_t v2 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wb & mask) | 0x64006400u), mul, add);
+  h2_t v3 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wb8 & mask) | 0x64006400u), mul, add);
+  return h8_t{v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+}
+
+// ----------------------------------------------------------------------------
+// Activation staging.
+// ----------------------------------------------------------------------------
+template <typename InT, bool FRAG>
+__global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale, int m,
+                                                      int k) {
+  const int row = blockIdx.x;
+  if (row >= m)
+    return;
+  const InT* xr = x + (size_t)row * k;
+  const int chunks = k >> 3, nb = k >> 8;
+  float mx = 0.0f;
+  for (int c = threadIdx.x; c < chunks; c += 256) {
+    float v[8];
+    load8(xr + c * 8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      mx = fmaxf(mx, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    mx = fmaxf(mx, __shfl_xor(mx, off));
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0)
+    red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // Scale the row so its largest magnitude lands in [2^14, 2^15): finite in
+  // fp16 with the full 11-bit significand for every large element.
+  float up = 1.0f, down = 1.0f;
+  if (mx > 0.0f && mx <= FLT_MAX) {
+    int e;
+    frexpf(mx, &e);
+    e = e < -80 ? -80 : e;
+    up = ldexpf(1.0f, 15 - e);
+    down = ldexpf(1.0f, e - 15);
+  }
+  if (threadIdx.x == 0)
+    rowscale[row] = down;
+  for (int c = threadIdx.x; c < chunks; c += 256) {
+    float v[8];
+    load8(xr + c * 8, v);
+    h8_t o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      o[i] = (_Float16)(v[i] * up);
+    size_t dst;
+    if (FRAG) {
+      const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, s = ((e >> 5) & 1) * 4 + ((e >> 3) & 3);
+      dst = ((((size_t)(row >> 4) * nb + b) * 8 + s) * 64 + (g * 16 + (row & 15))) * 8;
+    } else {
+      dst = (size_t)row * k + (size_t)c * 8;
+    }
+    *reinterpret_cast<h8_t*>(xo + dst) = o;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// GEMV (decode / small prefill / gated decode).
+//
+// Workgroup = W waves over T column tiles (16T output columns); the K blocks
+// are split into W contiguous ranges, one per wave, and the partial sums are
+// reduced through LDS.  Per tile-block a wave issues three fully contiguous
+// 16-byte loads per lane (two quant slabs + header) and, per 16-row tile of
+// activations, 16 MFMAs: 8 with B = q*sc (exact fp16) and 8 with B = m_j, then
+// acc += d * C_q - dmin * C_m in fp32 -- the decode form of
+// quant_linear.metal:288-302 with the integer parts on the matrix core.
+// ----------------------------------------------------------------------------
+template <int T, int NM>
+struct TileWords {
+  u4_t q0[NM][T], q1[NM][T], hd[NM][T];
+};
+
+template <int T, int NM>
+__device__ __forceinline__ void load_tile_words(TileWords<T, NM>& tw, const GemvArgs& a, int ct0, int b, int nb, int lane, int col) {
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint8_t* p = (mi ? a.wu : a.w) + ((size_t)(ct0 + t) * nb + b) * kTileBlockBytes;
+      tw.q0[mi][t] = *reinterpret_cast<const u4_t*>(p + 16 * lane);
+      tw.q1[mi][t] = *reinterpret_cast<const u4_t*>(p + kSlabBytes + 16 * lane);
+      tw.hd[mi][t] = *reinterpret_cast<const u4_t*>(p + kHeaderOffset + 16 * col);
+    }
+}
+
+template <int RT, int T, int W, bool GATED, typename OutT>
+__global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
+  constexpr int NM = GATED ? 2 : 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  const int nb = a.nb;
+  const int ct0 = blockIdx.x * T;
+  const int b0 = nb * wave / W, b1 = nb * (wave + 1) / W;
+
+  f4_t acc[NM][T][RT];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        acc[mi][t][rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  TileWords<T, NM> cur, next;
+  if (b0 < b1)
+    load_tile_words(cur, a, ct0, b0, nb, lane, col);
+  for (int b = b0; b < b1; ++b) {
+    // Activations of this block first, then the next block's weights: the
+    // in-order vmcnt wait for the activations then leaves the prefetch in flight.
+    h8_t xa[RT][8];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const bool live = rt * 16 + col < a.m;
+      const h8_t* xp = reinterpret_cast<const h8_t*>(a.xf) + (size_t)(rt * nb + b) * 8 * 64 + lane;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        xa[rt][s] = live ? xp[s * 64] : h8_t{};
+    }
+    if (b + 1 < b1)
+      load_tile_words(next, a, ct0, b + 1, nb, lane, col);
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const u4_t h = cur.hd[mi][t];
+        const float d = half_bits_to_float(h.x & 0xffffu), dmin = half_bits_to_float(h.x >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        scale_min_pair(h, g, sc0, m0, sc1, m1);
+        const _Float16 fsc0 = (_Float16)(float)sc0;
+        const h2_t mul_lo = {fsc0, fsc0};
+        const h2_t add_lo = {(_Float16)(-1024.0f * (float)sc0), (_Float16)(-1024.0f * (float)sc0)};
+        const h2_t mul_hi = {(_Float16)((float)sc1 * 0.0625f), (_Float16)((float)sc1 * 0.0625f)};
+        const h2_t add_hi = {(_Float16)(-64.0f * (float)sc1), (_Float16)(-64.0f * (float)sc1)};
+        const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1;
+        const h8_t bm_lo = {fm0, fm0, fm0, fm0, fm0, fm0, fm0, fm0};
+        const h8_t bm_hi = {fm1, fm1, fm1, fm1, fm1, fm1, fm1, fm1};
+        f4_t cq[RT], cm[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          cq[rt] = cm[rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const u4_t q = u < 2 ? cur.q0[mi][t] : cur.q1[mi][t];
+          const uint32_t wa = q[2 * (u & 1)], wb = q[2 * (u & 1) + 1];
+          const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, mul_lo, add_lo);
+          const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, mul_hi, add_hi);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            cq[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][u], blo, cq[rt], 0, 0, 0);
+            cq[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][4 + u], bhi, cq[rt], 0, 0, 0);
+            cm[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][u], bm_lo, cm[rt], 0, 0, 0);
+            cm[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][4 + u], bm_hi, cm[rt], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            acc[mi][t][rt][v] = fmaf(d, cq[rt][v], fmaf(-dmin, cm[rt][v], acc[mi][t][rt][v]));
+      }
+    cur = next;
+  }
+
+  // Cross-wave reduction: lane-major so each wave's store is conflict free.
+  constexpr int NV = NM * T * RT;
+  __shared__ f4_t red[W][NV][64];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        red[wave][(mi * T + t) * RT + rt][lane] = acc[mi][t][rt];
+  __syncthreads();
+
+  for (int item = tid; item < T * RT * 64; item += 64 * W) {
+    const int l = item & 63, tr = item >> 6, t = tr / RT, rt = tr % RT;
+    f4_t s[NM];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      s[mi] = red[0][(mi * T + t) * RT + rt][l];
+#pragma unroll
+      for (int w = 1; w < W; ++w)
+        s[mi] += red[w][(mi * T + t) * RT + rt][l];
+    }
+    const int n = (ct0 + t) * 16 + (l & 15);
+    OutT* y = reinterpret_cast<OutT*>(a.y);
+    const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = rt * 16 + 4 * (l >> 4) + v;
+      if (row >= a.m)
+        continue;
+      const float scale = a.rowscale[row];
+      const size_t o = (size_t)row * a.n + n;
+      float out;
+      if (GATED) {
+        float gv = s[0][v] * scale, uv = s[NM - 1][v] * scale;
+        if (sizeof(OutT) == 2) {
+          gv = round_half(gv);
+          uv = round_half(uv);
+        }
+        out = silu(gv) * uv;
+      } else {
+        float acc_v = s[0][v] * scale;
+        if (sizeof(OutT) == 2)
+          acc_v = round_half(acc_v);
+        out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
+      }
+      store_elem(y, o, out);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// GEMM (prefill).  Workgroup tile 128 x 128, 4 waves of 64 x 64, k-step 64
+// (one quarter of a Q4_K block).  Per k-step: the 128x64 fp16 activation tile
+// is copied to LDS; 256 threads dequantise the 128x64 weight tile to
+// h(d*sc*q - dmin*m) (quant_linear.metal:43,45) into LDS; each wave then runs
+// 16 v_mfma_f32_32x32x16_f16.
+// ----------------------------------------------------------------------------
+constexpr int kBM = 128, kBN = 128, kBK = 64, kLds = kBK + 8;
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLds];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[kBN * kLds];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int nb = a.nb;
+
+  f16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        acc[i][j][v] = 0.0f;
+
+  // A copy: thread -> (row, 32-element half of the k-step).
+  const int ar = tid >> 1, ak = (tid & 1) * 32;
+  const bool a_live = m0 + ar < a.m;
+  const _Float16* a_src = a.xh + (size_t)(m0 + ar) * a.k + ak;
+  // B dequant: thread -> (column, slab).
+  const int bc = tid >> 1, hh = tid & 1;
+  const int bn = n0 + bc;
+  const bool b_live = bn < a.n;
+  const uint8_t* b_tile = a.w + (size_t)(bn >> 4) * nb * kTileBlockBytes;
+  const int bi = bn & 15;
+
+  for (int kb = 0; kb < nb; ++kb) {
+    const uint8_t* tb = b_tile + (size_t)kb * kTileBlockBytes;
+    u4_t hd = b_live ? *reinterpret_cast<const u4_t*>(tb + kHeaderOffset + 16 * bi) : u4_t{0u, 0u, 0u, 0u};
+    const float d = half_bits_to_float(hd.x & 0xffffu), dmin = half_bits_to_float(hd.x >> 16);
+    for (int gq = 0; gq < 4; ++gq) {
+      // Stage A.
+      h8_t av[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        av[j] = a_live ? *reinterpret_cast<const h8_t*>(a_src + (size_t)kb * 256 + gq * 64 + j * 8) : h8_t{};
+      // Dequantise B: 16 quant bytes = 16 low-nibble + 16 high-nibble weights.
+      u4_t raw = b_live ? *reinterpret_cast<const u4_t*>(tb + hh * kSlabBytes + 16 * (gq * 16 + bi)) : u4_t{0u, 0u, 0u, 0u};
+      uint32_t sc0, mn0, sc1, mn1;
+      scale_min_pair(hd, gq, sc0, mn0, sc1, mn1);
+      const float ds0 = d * (float)sc0, dm0 = dmin * (float)mn0, ds1 = d * (float)sc1, dm1 = dmin * (float)mn1;
+      h8_t lo[2], hi[2];
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        const uint32_t wv = raw[wd];
+        // Stored byte order within a word is (0, 2, 1, 3) of the quant bytes.
+        const uint32_t qb[4] = {wv & 0xffu, (wv >> 16) & 0xffu, (wv >> 8) & 0xffu, wv >> 24};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[wd >> 1][(wd & 1) * 4 + e] = (_Float16)(ds0 * (float)(qb[e] & 15u) - dm0);
+          hi[wd >> 1][(wd & 1) * 4 + e] = (_Float16)(ds1 * (float)(qb[e] >> 4) - dm1);
+        }
+      }
+      __syncthreads();  // previous k-step's MFMA reads are done
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<h8_t*>(&As[ar * kLds + ak + j * 8]) = av[j];
+      _Float16* bdst = &Bs[bc * kLds + 16 * hh];
+      *reinterpret_cast<h8_t*>(bdst) = lo[0];
+      *reinterpret_cast<h8_t*>(bdst + 8) = lo[1];
+      *reinterpret_cast<h8_t*>(bdst + 32) = hi[0];
+      *reinterpret_cast<h8_t*>(bdst + 40) = hi[1];
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < kBK / 16; ++kk) {
+        h8_t af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          af[i] = *reinterpret_cast<const h8_t*>(&As[(wm * 64 + i * 32 + (lane & 31)) * kLds + kk * 16 + 8 * (lane >> 5)]);
+          bf[i] = *reinterpret_cast<const h8_t*>(&Bs[(wn * 64 + i * 32 + (lane & 31)) * kLds + kk * 16 + 8 * (lane >> 5)]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+      if (n >= a.n)
+        continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row >= a.m)
+          continue;
+        const size_t o = (size_t)row * a.n + n;
+        float acc_v = acc[i][j][v] * a.rowscale[row];
+        if (sizeof(OutT) == 2)
+          acc_v = round_half(acc_v);
+        const float out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
+        store_elem(y, o, out);
+      }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Row gather and device re-layout.
+// ----------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ x, T* __restrict__ out, int k, GatherIndex idx) {
+  const int r = blockIdx.x;
+  const T* src = x + (size_t)idx.src[r] * k;
+  T* dst = out + (size_t)r * k;
+  for (int i = threadIdx.x; i < k; i += 256)
+    dst[i] = src[i];
+}
+
+__device__ __forceinline__ uint32_t swap_middle_bytes(uint32_t v) {
+  return (v & 0xff0000ffu) | ((v & 0x0000ff00u) << 8) | ((v & 0x00ff0000u) >> 8);
+}
+
+// One workgroup of 64 lanes per tile-block.
+__global__ __launch_bounds__(64) void relayout_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t n, uint32_t nb) {
+  const size_t tb = blockIdx.x;
+  const uint32_t c = (uint32_t)(tb / nb), b = (uint32_t)(tb % nb);
+  const int lane = threadIdx.x, i = lane & 15, g = lane >> 4;
+  const uint8_t* blk = src + ((size_t)(16 * c + i) * nb + b) * kBlockBytes;
+  uint8_t* out = dst + tb * kTileBlockBytes;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint8_t* q = blk + 16 + 32 * g + 16 * h;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = swap_middle_bytes((uint32_t)q[4 * j] | ((uint32_t)q[4 * j + 1] << 8) | ((uint32_t)q[4 * j + 2] << 16) | ((uint32_t)q[4 * j + 3] << 24));
+    *reinterpret_cast<u4_t*>(out + h * kSlabBytes + 16 * lane) = u4_t{w[0], w[1], w[2], w[3]};
+  }
+  if (g == 0) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)blk[4 * j] | ((uint32_t)blk[4 * j + 1] << 8) | ((uint32_t)blk[4 * j + 2] << 16) | ((uint32_t)blk[4 * j + 3] << 24);
+    *reinterpret_cast<u4_t*>(out + kHeaderOffset + 16 * i) = u4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+template <int RT, int T, int W, bool GATED>
+hipError_t gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
+  const dim3 grid((unsigned)(a.n / (16 * T))), block(64 * W);
+  if (dtype == kF32)
+    q4k_gemv_kernel<RT, T, W, GATED, float><<<grid, block, 0, s>>>(a);
+  else
+    q4k_gemv_kernel<RT, T, W, GATED, _Float16><<<grid, block, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+template <bool GATED>
+hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape) {
+  // Instances (see gemv_shape): one row tile with (1 tile, 16 waves),
+  // (1 tile, 8 waves) or (2 tiles, 8 waves); two or three row tiles with
+  // 8 waves, two column tiles only without the gate/up pair (register budget).
+  if (shape.row_tiles == 1) {
+    if (shape.tiles == 2)
+      return gemv_launch<1, 2, 8, GATED>(s, a, dtype);
+    return shape.waves == 16 ? gemv_launch<1, 1, 16, GATED>(s, a, dtype) : gemv_launch<1, 1, 8, GATED>(s, a, dtype);
+  }
+  if constexpr (!GATED) {
+    if (shape.tiles == 2)
+      return shape.row_tiles == 2 ? gemv_launch<2, 2, 8, false>(s, a, dtype) : gemv_launch<3, 2, 8, false>(s, a, dtype);
+  }
+  return shape.row_tiles == 2 ? gemv_launch<2, 1, 8, GATED>(s, a, dtype) : gemv_launch<3, 1, 8, GATED>(s, a, dtype);
+}
+
+}  // namespace
+
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, bool frag) {
+  if (m <= 0)
+    return hipSuccess;
+  const dim3 grid((unsigned)m), block(256);
+  if (dtype == kF32) {
+    if (frag)
+      stage_x_kernel<float, true><<<grid, block, 0, s>>>(static_cast<const float*>(x), xo, rowscale, m, k);
+    else
+      stage_x_kernel<float, false><<<grid, block, 0, s>>>(static_cast<const float*>(x), xo, rowscale, m, k);
+  } else {
+    if (frag)
+      stage_x_kernel<_Float16, true><<<grid, block, 0, s>>>(static_cast<const _Float16*>(x), xo, rowscale, m, k);
+    else
+      stage_x_kernel<_Float16, false><<<grid, block, 0, s>>>(static_cast<const _Float16*>(x), xo, rowscale, m, k);
+  }
+  return hipGetLastError();
+}
+
+GemvShape gemv_shape(int m, int n, bool gated) {
+  GemvShape sh;
+  sh.row_tiles = m <= 16 ? 1 : m <= 32 ? 2 : 3;
+  // Two column tiles per workgroup once that still leaves >= 384 workgroups
+  // (1.5 per CU) and the registers allow it; otherwise one.  Grids of fewer
+  // than 1024 single-tile workgroups get 16 waves each so that enough weight
+  // bytes are in flight per CU.
+  sh.tiles = (n % 32 == 0 && n / 32 >= 384 && (sh.row_tiles == 1 || !gated)) ? 2 : 1;
+  sh.waves = (sh.row_tiles == 1 && sh.tiles == 1 && n / 16 < 1024) ? 16 : 8;
+  return sh;
+}
+
+hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated) {
+  if (shape.row_tiles < 1 || shape.row_tiles > kGemvMaxRowTiles || a.n % (16 * shape.tiles) != 0 || a.m > 16 * shape.row_tiles)
+    return hipErrorInvalidValue;
+  return gated ? gemv_dispatch<true>(s, a, dtype, shape) : gemv_dispatch<false>(s, a, dtype, shape);
+}
+
+hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype) {
+  const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + kBM - 1) / kBM)), block(256);
+  if (dtype == kF32)
+    q4k_gemm_kernel<float><<<grid, block, 0, s>>>(a);
+  else
+    q4k_gemm_kernel<_Float16><<<grid, block, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx) {
+  if (idx.rows == 0)
+    return hipSuccess;
+  const dim3 grid(idx.rows), block(256);
+  if (dtype == kF32)
+    gather_rows_kernel<float><<<grid, block, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(out), k, idx);
+  else
+    gather_rows_kernel<_Float16><<<grid, block, 0, s>>>(static_cast<const _Float16*>(x), static_cast<_Float16*>(out), k, idx);
+  return hipGetLastError();
+}
+
+hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k) {
+  const uint32_t nb = k / 256;
+  const size_t tiles = (size_t)(n / 16) * nb;
+  if (tiles == 0)
+    return hipSuccess;
+  relayout_kernel<<<dim3((unsigned)tiles), dim3(64), 0, s>>>(src, dst, n, nb);
+  return hipGetLastError();
+}
+
+}  // namespace q4k

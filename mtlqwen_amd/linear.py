@@ -1,0 +1,200 @@
+"""Python face of the Q4_K linear() path, shaped like the reference's host API.
+
+``Weight`` mirrors ``struct Weight`` (model/qwen35/qwen35.hpp:34-37): a Q4_K
+tensor of n rows by k columns plus a four-slot kernel cache indexed by phase.
+``linear`` mirrors ``Ops::linear`` (model/qwen35/forward.cpp:51-70) and
+``mlp`` the MLP section of ``Ops::decoder`` (forward.cpp:114-119).  All work
+is done by libq4k.so through its C ABI; tensors are torch tensors on the GPU
+(torch supplies device memory and the current stream, nothing else).
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from ._lib import (DTYPE_F16, DTYPE_F32, GGML_TYPE_Q4_K, POST_ADD, POST_GATE, POST_STORE, Q4KError, check, lib,
+                   u32_array)
+
+BLOCK_BYTES = 144
+PHASE_NAMES = ("decode", "prefill", "prefill_small", "gated_decode")
+
+
+def q4k_nbytes(n, k):
+    return n * (k // 256) * BLOCK_BYTES
+
+
+def _dtype_code(t):
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.float16:
+        return DTYPE_F16
+    raise TypeError(f"activations must be float32 or float16, got {t.dtype}")
+
+
+def _stream(stream):
+    if stream is None:
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, torch.cuda.Stream):
+        return ctypes.c_void_p(stream.cuda_stream)
+    return ctypes.c_void_p(stream)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("tensors passed to the Q4_K path must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensors passed to the Q4_K path must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class Weight:
+    """A Q4_K weight uploaded once to HBM (re-laid out for the kernels).
+
+    ``data`` holds GGUF block_q4_K bytes for n rows of k/256 blocks: a host
+    numpy/bytes buffer, or a uint8 CUDA tensor (re-laid out on the device).
+    """
+
+    def __init__(self, data, n, k, ggml_type=GGML_TYPE_Q4_K, device=0):
+        handle = ctypes.c_void_p()
+        if isinstance(data, torch.Tensor) and data.is_cuda:
+            if data.dtype != torch.uint8 or not data.is_contiguous():
+                raise ValueError("device weight bytes must be a contiguous uint8 tensor")
+            rc = lib.q4k_weight_create_from_device(ctypes.c_void_p(data.data_ptr()), data.numel(), n, k, ggml_type,
+                                                   device, _stream(None), ctypes.byref(handle))
+        else:
+            buf = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), dtype=np.uint8)
+                                       if not isinstance(data, np.ndarray) else data.view(np.uint8).reshape(-1))
+            rc = lib.q4k_weight_create(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, n, k, ggml_type, device,
+                                       ctypes.byref(handle))
+        check(rc)
+        self._h = handle
+        self.n, self.k, self.type, self.device = n, k, ggml_type, device
+
+    @property
+    def handle(self):
+        if self._h is None:
+            raise ValueError("weight has been released")
+        return self._h
+
+    def kernel_name(self, phase):
+        buf = ctypes.create_string_buffer(256)
+        check(lib.q4k_weight_kernel_name(self.handle, phase, buf, 256))
+        return buf.value.decode()
+
+    def prepare(self, phase):
+        """Resolve a kernel slot ahead of use (the engine's prepare passes)."""
+        check(lib.q4k_weight_prepare(self.handle, phase))
+
+    @property
+    def nbytes(self):
+        return q4k_nbytes(self.n, self.k)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None:
+            lib.q4k_weight_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def select_phase(query_counts, m=None, gated=False):
+    """Phase of Ops::linear for a packed batch (forward.cpp:52,190)."""
+    arr, nq = u32_array(query_counts)
+    if m is None:
+        m = sum(query_counts)
+    out = ctypes.c_uint32()
+    check(lib.q4k_select_phase(arr, nq, m, int(bool(gated)), ctypes.byref(out)))
+    return out.value
+
+
+def pack_queries(counts, samples=None):
+    """Ragged packing (forward.cpp:171-191): (start, logit, rows, logit_rows)."""
+    c, nq = u32_array(counts)
+    s, _ = u32_array(samples)
+    start = (ctypes.c_uint32 * max(nq, 1))()
+    logit = (ctypes.c_uint32 * max(nq, 1))()
+    rows, lrows = ctypes.c_uint32(), ctypes.c_uint32()
+    check(lib.q4k_pack_queries(c, s, nq, start, logit, ctypes.byref(rows), ctypes.byref(lrows)))
+    return list(start[:nq]), list(logit[:nq]), rows.value, lrows.value
+
+
+def linear(x, w, count, output, auxiliary=None, gated=False, query_counts=None, stream=None):
+    """Ops::linear(x, w, count, output, auxiliary, gated) (forward.cpp:51-70).
+
+    post = 2 when gated, 1 when an auxiliary tensor is given, else 0.  With
+    gated=True and a Weight as auxiliary (the decode form of forward.cpp:118),
+    runs the fused gate/up projection with ``w`` as gate and ``auxiliary`` as up.
+    query_counts are the rows of each packed sequence (default: one sequence).
+    """
+    if gated and isinstance(auxiliary, Weight):
+        return mlp_gate_up(x, w, auxiliary, count, output, query_counts=query_counts, stream=stream)
+    dt = _dtype_code(x)
+    if output.dtype != x.dtype or (auxiliary is not None and auxiliary.dtype != x.dtype):
+        raise TypeError("x, output and auxiliary must share a dtype")
+    post = POST_GATE if gated else (POST_ADD if auxiliary is not None else POST_STORE)
+    counts, nq = u32_array(query_counts if query_counts is not None else [count])
+    check(lib.q4k_linear(_stream(stream), w.handle, _ptr(x), _ptr(output), _ptr(auxiliary), count, counts, nq, post, dt))
+    return output
+
+
+def mlp_gate_up(x, gate, up, count, output, query_counts=None, stream=None):
+    """silu(x . gate^T) * (x . up^T) into ``output`` (the gate buffer)."""
+    dt = _dtype_code(x)
+    counts, nq = u32_array(query_counts if query_counts is not None else [count])
+    check(lib.q4k_mlp_gate_up(_stream(stream), gate.handle, up.handle, _ptr(x), _ptr(output), count, counts, nq, dt))
+    return output
+
+
+def mlp(x, gate, up, down, hidden, gate_buffer, count, query_counts=None, stream=None):
+    """MLP of Ops::decoder (forward.cpp:115-119): gate/up into gate_buffer,
+    then down with the residual added in place into ``hidden``."""
+    mlp_gate_up(x, gate, up, count, gate_buffer, query_counts=query_counts, stream=stream)
+    return linear(gate_buffer, down, count, hidden, auxiliary=hidden, query_counts=query_counts, stream=stream)
+
+
+def gather_rows(x, out, counts, samples, stream=None):
+    """LM-head row gather (native_ops.metal:12-15): returns the gathered row count."""
+    dt = _dtype_code(x)
+    c, nq = u32_array(counts)
+    s, _ = u32_array(samples)
+    rows = ctypes.c_uint32()
+    check(lib.q4k_gather_rows(_stream(stream), _ptr(x), _ptr(out), x.shape[-1], c, s, nq, dt, ctypes.byref(rows)))
+    return rows.value
+
+
+def profile_enable(on=True):
+    """Bracket every kernel launch with hipEvents (clears earlier records)."""
+    check(lib.q4k_profile_enable(int(bool(on))))
+
+
+def profile_query(kernel):
+    """(launches, total_ms, min_ms, max_ms) of one kernel family (KERNEL_*)."""
+    n = ctypes.c_uint32()
+    tot, lo, hi = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    check(lib.q4k_profile_query(kernel, ctypes.byref(n), ctypes.byref(tot), ctypes.byref(lo), ctypes.byref(hi)))
+    return n.value, tot.value, lo.value, hi.value
+
+
+def relayout_host(gguf, n, k):
+    src = np.ascontiguousarray(gguf, dtype=np.uint8).reshape(-1)
+    dst = np.empty_like(src)
+    check(lib.q4k_relayout_host(src.ctypes.data_as(ctypes.c_void_p), dst.ctypes.data_as(ctypes.c_void_p), n, k))
+    return dst
+
+
+def unrelayout_host(tiled, n, k):
+    src = np.ascontiguousarray(tiled, dtype=np.uint8).reshape(-1)
+    dst = np.empty_like(src)
+    check(lib.q4k_unrelayout_host(src.ctypes.data_as(ctypes.c_void_p), dst.ctypes.data_as(ctypes.c_void_p), n, k))
+    return dst
+
+
+__all__ = ["Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "relayout_host",
+           "profile_enable", "profile_query",
+           "unrelayout_host", "q4k_nbytes", "Q4KError", "PHASE_NAMES"]

@@ -1,0 +1,88 @@
+/*
+ * q4k_oracle.h -- CPU restatement of MTLQwen's Q4_K linear() arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP path is
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library (mtlqwen_amd/) never
+ * links, loads or falls back to it.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the MTLQwen source tree).  Activations default to the fp32 domain of the
+ * benchmark configs; the *_f16 variants apply the reference's fp16 rounding
+ * points for engine-style half activations.
+ */
+#ifndef Q4K_ORACLE_H
+#define Q4K_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q4O_BLOCK_ELEMS 256
+#define Q4O_BLOCK_BYTES 144
+
+/* IEEE binary16 <-> binary32.  half->float is exact; float->half rounds to
+ * nearest-even (the conversion Metal's half(float) performs). */
+float q4o_half_to_float(uint16_t h);
+uint16_t q4o_float_to_half(float f);
+
+/* 6-bit scale / min of sub-block j (0..7) from the 12 packed bytes at block+4.
+ * backend/metal/kernel/quant_linear.metal:12-20 (scale_min_k4). */
+void q4o_scale_min(int j, const uint8_t* q12, uint8_t* sc, uint8_t* m);
+
+/* Inverse of q4o_scale_min: pack 8 scales and 8 mins (each < 64) into 12 bytes. */
+void q4o_pack_scale_min(const uint8_t sc[8], const uint8_t m[8], uint8_t q12[12]);
+
+/* Dequantize one 144-byte block_q4_K into 256 fp32 values d*sc*q - dmin*m.
+ * quant_linear.metal:32-48 (dequant_tile<q4_k_tag>, before its half() store). */
+void q4o_dequant_block(const uint8_t* blk, float* out);
+
+/* Same value rounded to fp16, as the reference's prefill tiles store it
+ * (quant_linear.metal:43,45).  Returns fp16 bit patterns. */
+void q4o_dequant_block_f16(const uint8_t* blk, uint16_t* out);
+
+/* y[M,N] = x[M,K] . W[N,K]^T with W in GGUF block_q4_K rows (N rows of K/256
+ * blocks).  fp32 accumulation in the decode kernel's algebraic form
+ * (quant_linear.metal:259-303): per sub-block sum(x*q) and sum(x), then
+ * d*sc and dmin*m applied.
+ * post 0: y = acc;  post 1: y = acc + aux;  post 2: y = silu(aux) * acc
+ * (quant_linear.metal:146-147 epilogue, forward.cpp:67-68 post codes).
+ * aux may alias y.  threads <= 0 means all hardware threads.
+ * Returns 0, or -1 on invalid arguments. */
+int q4o_linear_f32(float* y, const float* x, const uint8_t* w, const float* aux, int M, int N, int K, int post, int threads);
+
+/* fp16 activations, reference rounding points:
+ * post 0: h(acc); post 1: h(h(acc) + aux) (quant_linear.metal:237-243);
+ * post 2: h(silu(aux) * h(acc)) (quant_linear.metal:146-147). */
+int q4o_linear_f16(uint16_t* y, const uint16_t* x, const uint8_t* w, const uint16_t* aux, int M, int N, int K, int post, int threads);
+
+/* Fused gate/up: y = silu(x.Wg^T) * (x.Wu^T).
+ * backend/metal/kernel/fused_kernels.metal:44-78.  f16 variant rounds g and u
+ * to half before the SiLU and rounds the product (fused_kernels.metal:74-75). */
+int q4o_mlp_gate_up_f32(float* y, const float* x, const uint8_t* wg, const uint8_t* wu, int M, int N, int K, int threads);
+int q4o_mlp_gate_up_f16(uint16_t* y, const uint16_t* x, const uint8_t* wg, const uint8_t* wu, int M, int N, int K, int threads);
+
+/* Same contraction, double-precision dequantize-then-dot (quant_linear.metal:32-48
+ * values, no fp16 rounding).  A second formulation used to cross-check the
+ * fp32 decode form. */
+int q4o_linear_f64(double* y, const double* x, const uint8_t* w, int M, int N, int K, int threads);
+
+/* Kernel phase of Ops::linear: 0 decode, 1 prefill, 2 prefill_small, 3 gated
+ * decode.  decode holds iff every query contributes <= 5 rows
+ * (model/qwen35/forward.cpp:52,190; qwen35.hpp:22). */
+int q4o_phase(const uint32_t* counts, int nqueries, int gated);
+
+/* Ragged packing (model/qwen35/forward.cpp:171-191): start = running row count,
+ * logit = running sample count.  Returns total rows. */
+uint32_t q4o_pack(const uint32_t* counts, const uint32_t* samples, int nqueries, uint32_t* start, uint32_t* logit);
+
+/* Input row read by LM-head output row r (native_ops.metal:12-15 with
+ * batch.hpp:25-29 queryLogit): start + count - samples + (r - logit) of the
+ * query that owns logit row r.  Returns -1 if r is not owned by any query. */
+int64_t q4o_gather_row(const uint32_t* start, const uint32_t* count, const uint32_t* samples, const uint32_t* logit, int nqueries, uint32_t r);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,206 @@
+"""Shared test helpers: seeded Q4_K data, the oracle's ctypes binding, and an
+independent numpy formulation of the Q4_K format used to pin the oracle.
+
+The oracle (oracle/libq4k_oracle.so) is test infrastructure: tests use it as
+the checker of the HIP path, never as the thing measured.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libq4k_oracle.so")
+BLOCK_BYTES = 144
+
+# --------------------------------------------------------------------------
+# Synthetic data (the BASELINE config-0 recipe).
+# --------------------------------------------------------------------------
+
+
+def make_q4k(rng, n, k, dmax=0.01):
+    """GGUF block_q4_K bytes [n, k/256*144]: d, dmin = fp16(U(0, dmax)),
+    12 uniform scale bytes (uniform 6-bit scales/mins), uniform quant bytes."""
+    nb = k // 256
+    w = rng.integers(0, 256, size=(n, nb, BLOCK_BYTES), dtype=np.uint8)
+    d = rng.uniform(0.0, dmax, size=(n, nb, 2)).astype(np.float16)
+    w[:, :, 0:4] = d.view(np.uint8).reshape(n, nb, 4)
+    return w.reshape(n, nb * BLOCK_BYTES)
+
+
+def make_x(rng, m, k, scale=1.0):
+    return (rng.standard_normal((m, k)) * scale).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# Independent numpy formulation.
+#
+# Element addressing follows embedding_q4_k (quant_linear.metal:585-590):
+#   j = r >> 5, qj = (r >> 6) * 32 + (r & 31), v = (r & 32) ? q >> 4 : q & 15
+# and the 6-bit fields use the kmask form of quant_linear.metal:278-284
+# (four fields per 16-bit word), not the per-j branches the oracle restates.
+# --------------------------------------------------------------------------
+
+
+def scale_min_kmask(hdr12):
+    """[..., 12] uint8 -> (sc[..., 8], m[..., 8]) via the 0x3f3f/0x0f0f/0xc0c0 masks."""
+    q = hdr12.astype(np.uint32)
+    w = q[..., 0::2] | (q[..., 1::2] << 8)  # six little-endian 16-bit words
+    k1, k2, k3 = 0x3F3F, 0x0F0F, 0xC0C0
+    sc, mn = np.zeros(hdr12.shape[:-1] + (8,), np.uint32), np.zeros(hdr12.shape[:-1] + (8,), np.uint32)
+    # iq = 0 team: words 0, 2, 4 give (j0, j1) scales / mins and (j4, j5)
+    # iq = 1 team: words 1, 3, 5 give (j2, j3) and (j6, j7)
+    for iq in range(2):
+        s0, s2, s4 = w[..., iq], w[..., iq + 2], w[..., iq + 4]
+        a = s0 & k1
+        b = s2 & k1
+        c = (s4 & k2) | ((s0 & k3) >> 2)
+        d = ((s4 >> 4) & k2) | ((s2 & k3) >> 2)
+        j = 2 * iq
+        sc[..., j], sc[..., j + 1] = a & 0xFF, a >> 8
+        mn[..., j], mn[..., j + 1] = b & 0xFF, b >> 8
+        sc[..., j + 4], sc[..., j + 5] = c & 0xFF, c >> 8
+        mn[..., j + 4], mn[..., j + 5] = d & 0xFF, d >> 8
+    return sc, mn
+
+
+def dequant_numpy(w, n, k):
+    """[n, k] float64 weights from GGUF Q4_K bytes."""
+    nb = k // 256
+    blk = w.reshape(n, nb, BLOCK_BYTES)
+    d = blk[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    dmin = blk[:, :, 2:4].copy().view(np.float16).astype(np.float64)[..., 0]
+    sc, mn = scale_min_kmask(blk[:, :, 4:16])
+    r = np.arange(256)
+    j = r >> 5
+    qj = (r >> 6) * 32 + (r & 31)
+    qb = blk[:, :, 16 + qj].astype(np.uint32)
+    v = np.where((r & 32) != 0, qb >> 4, qb & 15).astype(np.float64)
+    out = d[..., None] * sc[..., j].astype(np.float64) * v - dmin[..., None] * mn[..., j].astype(np.float64)
+    return out.reshape(n, k)
+
+
+def silu64(g):
+    return g / (1.0 + np.exp(-g))
+
+
+# --------------------------------------------------------------------------
+# Oracle binding.
+# --------------------------------------------------------------------------
+
+
+def _build_oracle():
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+
+
+def load_oracle():
+    if not os.path.exists(ORACLE_SO):
+        _build_oracle()
+    lib = ctypes.CDLL(ORACLE_SO)
+    p, i, u8p = ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p
+    lib.q4o_half_to_float.restype = ctypes.c_float
+    lib.q4o_half_to_float.argtypes = [ctypes.c_uint16]
+    lib.q4o_float_to_half.restype = ctypes.c_uint16
+    lib.q4o_float_to_half.argtypes = [ctypes.c_float]
+    lib.q4o_scale_min.argtypes = [i, u8p, ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_uint8)]
+    lib.q4o_pack_scale_min.argtypes = [u8p, u8p, u8p]
+    lib.q4o_dequant_block.argtypes = [u8p, p]
+    lib.q4o_dequant_block_f16.argtypes = [u8p, p]
+    for name in ("q4o_linear_f32", "q4o_linear_f16"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = [p, p, u8p, p, i, i, i, i, i]
+    for name in ("q4o_mlp_gate_up_f32", "q4o_mlp_gate_up_f16"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = [p, p, u8p, u8p, i, i, i, i]
+    lib.q4o_linear_f64.restype = i
+    lib.q4o_linear_f64.argtypes = [p, p, u8p, i, i, i, i]
+    lib.q4o_phase.restype = i
+    lib.q4o_phase.argtypes = [ctypes.POINTER(ctypes.c_uint32), i, i]
+    lib.q4o_pack.restype = ctypes.c_uint32
+    lib.q4o_pack.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 2 + [i] + [ctypes.POINTER(ctypes.c_uint32)] * 2
+    lib.q4o_gather_row.restype = ctypes.c_int64
+    lib.q4o_gather_row.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 4 + [i, ctypes.c_uint32]
+    return lib
+
+
+# Host threads for the oracle: the GPU box's CPU share is 16 cores per GPU.
+DEFAULT_THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+class Oracle:
+    """numpy-level wrappers of the C oracle."""
+
+    def __init__(self):
+        self.lib = load_oracle()
+
+    @staticmethod
+    def _p(a):
+        return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+    def linear(self, x, w, n, k, aux=None, post=0, threads=DEFAULT_THREADS):
+        x = np.ascontiguousarray(x)
+        m = x.shape[0]
+        if x.dtype == np.float16:
+            y = np.empty((m, n), np.float16)
+            auxa = None if aux is None else np.ascontiguousarray(aux, np.float16)
+            rc = self.lib.q4o_linear_f16(self._p(y), self._p(x.view(np.uint16)), self._p(w), self._p(auxa), m, n, k, post,
+                                         threads)
+        else:
+            x = x.astype(np.float32, copy=False)
+            y = np.empty((m, n), np.float32)
+            auxa = None if aux is None else np.ascontiguousarray(aux, np.float32)
+            rc = self.lib.q4o_linear_f32(self._p(y), self._p(x), self._p(w), self._p(auxa), m, n, k, post, threads)
+        assert rc == 0
+        return y
+
+    def mlp_gate_up(self, x, wg, wu, n, k, threads=DEFAULT_THREADS):
+        x = np.ascontiguousarray(x)
+        m = x.shape[0]
+        if x.dtype == np.float16:
+            y = np.empty((m, n), np.float16)
+            rc = self.lib.q4o_mlp_gate_up_f16(self._p(y), self._p(x), self._p(wg), self._p(wu), m, n, k, threads)
+        else:
+            y = np.empty((m, n), np.float32)
+            rc = self.lib.q4o_mlp_gate_up_f32(self._p(y), self._p(x.astype(np.float32, copy=False)), self._p(wg),
+                                              self._p(wu), m, n, k, threads)
+        assert rc == 0
+        return y
+
+    def linear_f64(self, x, w, n, k, threads=DEFAULT_THREADS):
+        x = np.ascontiguousarray(x, np.float64)
+        y = np.empty((x.shape[0], n), np.float64)
+        assert self.lib.q4o_linear_f64(self._p(y), self._p(x), self._p(w), x.shape[0], n, k, threads) == 0
+        return y
+
+    def dequant_block(self, blk):
+        out = np.empty(256, np.float32)
+        self.lib.q4o_dequant_block(self._p(np.ascontiguousarray(blk, np.uint8)), self._p(out))
+        return out
+
+    def phase(self, counts, gated=False):
+        arr = (ctypes.c_uint32 * len(counts))(*counts)
+        return self.lib.q4o_phase(arr, len(counts), int(gated))
+
+    def pack(self, counts, samples):
+        n = len(counts)
+        c = (ctypes.c_uint32 * n)(*counts)
+        s = (ctypes.c_uint32 * n)(*samples)
+        start, logit = (ctypes.c_uint32 * n)(), (ctypes.c_uint32 * n)()
+        rows = self.lib.q4o_pack(c, s, n, start, logit)
+        return list(start), list(logit), rows
+
+    def gather_row(self, start, count, samples, logit, r):
+        n = len(start)
+        arrs = [(ctypes.c_uint32 * n)(*v) for v in (start, count, samples, logit)]
+        return self.lib.q4o_gather_row(*arrs, n, r)
+
+
+def row_rel_err(y, ref):
+    """Max over rows of ||y - ref|| / ||ref|| (the BASELINE tolerance metric)."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    num = np.linalg.norm(y - ref, axis=-1)
+    den = np.linalg.norm(ref, axis=-1)
+    den = np.where(den == 0, 1.0, den)
+    return float(np.max(num / den)) if num.size else 0.0

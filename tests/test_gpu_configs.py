@@ -1,0 +1,132 @@
+"""The five BASELINE configurations at their full shapes, HIP path vs oracle.
+
+Config 4 (M=2048) is checked on a 64-row subset against the oracle (the GPU
+computes all rows; the oracle recomputes the subset) plus a size-independent
+property over all rows: stage-wise linearity y(x_a + x_b) = y(x_a) + y(x_b).
+"""
+import numpy as np
+import pytest
+import torch
+
+from q4k_ref import make_q4k, make_x, row_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+SEED_W, SEED_X = 0x51A70000, 0x51A71000
+
+
+def weights(idx, n, k):
+    return make_q4k(np.random.default_rng(SEED_W + idx), n, k)
+
+
+def acts(cfg, m, k, scale=1.0):
+    return make_x(np.random.default_rng(SEED_X + cfg), m, k, scale)
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_config0_single_linear(q4k, oracle, gpu):
+    w = weights(0, 4096, 4096)
+    x = acts(0, 1, 4096)
+    W = q4k.Weight(w, 4096, 4096)
+    y = torch.empty((1, 4096), device=gpu)
+    q4k.linear(_t(x, gpu), W, 1, y, query_counts=[1])
+    torch.cuda.synchronize()
+    assert "decode" in W.kernel_name(0)
+    assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, 4096, 4096)) <= TOL
+
+
+def _mlp_case(q4k, oracle, gpu, cfg, m, counts, scale, widx=1):
+    wg, wu, wd = weights(widx, 12288, 4096), weights(widx + 1, 12288, 4096), weights(widx + 2, 4096, 12288)
+    G, U, D = q4k.Weight(wg, 12288, 4096), q4k.Weight(wu, 12288, 4096), q4k.Weight(wd, 4096, 12288)
+    x = acts(cfg, m, 4096, scale)
+    hidden0 = acts(cfg + 100, m, 4096)
+    gate = torch.empty((m, 12288), device=gpu)
+    hidden = _t(hidden0, gpu)
+    q4k.mlp_gate_up(_t(x, gpu), G, U, m, gate, query_counts=counts)
+    torch.cuda.synchronize()
+    g_ref = oracle.mlp_gate_up(x, wg, wu, 12288, 4096)
+    g_gpu = gate.cpu().numpy()
+    assert row_rel_err(g_gpu, g_ref) <= TOL
+    # Down projection, residual in place, from the GPU's own gate buffer.
+    q4k.linear(gate, D, m, hidden, auxiliary=hidden, query_counts=counts)
+    torch.cuda.synchronize()
+    h_ref = oracle.linear(g_gpu, wd, 4096, 12288, aux=hidden0, post=1)
+    assert row_rel_err(hidden.cpu().numpy(), h_ref) <= TOL
+    return G, U, D
+
+
+def test_config1_decode_mlp(q4k, oracle, gpu):
+    G, U, D = _mlp_case(q4k, oracle, gpu, 1, 8, [1] * 8, 0.5)
+    assert "gate_up_decode" in G.kernel_name(3) and "decode" in D.kernel_name(0)
+
+
+def test_config2_speculative_verify(q4k, oracle, gpu):
+    counts = [5] * 8
+    m = 40
+    for name, n, k, post, idx in [("qkv", 6144, 4096, 0, 10), ("o", 4096, 4096, 1, 11)]:
+        w = weights(idx, n, k)
+        W = q4k.Weight(w, n, k)
+        x = acts(2, m, k)
+        res = acts(2 + 200 + idx, m, n)
+        y = _t(res, gpu) if post else torch.empty((m, n), device=gpu)
+        q4k.linear(_t(x, gpu), W, m, y, auxiliary=y if post else None, query_counts=counts)
+        torch.cuda.synchronize()
+        assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k, aux=res if post else None, post=post)) <= TOL, name
+    _mlp_case(q4k, oracle, gpu, 2, m, counts, 1.0)
+
+
+def test_config3_ragged_prefill(q4k, oracle, gpu):
+    lengths = [512, 37, 1, 1, 200, 5, 1, 64]
+    m = sum(lengths)
+    assert m == 821
+    for name, n, k, idx in [("qkv", 6144, 4096, 20), ("o", 4096, 4096, 21)]:
+        w = weights(idx, n, k)
+        W = q4k.Weight(w, n, k)
+        x = acts(3, m, k)
+        y = torch.empty((m, n), device=gpu)
+        q4k.linear(_t(x, gpu), W, m, y, query_counts=lengths)
+        torch.cuda.synchronize()
+        assert "prefill" in W.kernel_name(1)
+        assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k)) <= TOL, name
+    _mlp_case(q4k, oracle, gpu, 3, m, lengths, 1.0, widx=22)
+    # LM head on each sequence's last token (M=8, phase 2: prefill_small).
+    hidden = torch.randn(m, 4096, device=gpu, generator=torch.Generator(device=gpu).manual_seed(3))
+    rows = torch.empty((8, 4096), device=gpu)
+    assert q4k.gather_rows(hidden, rows, lengths, [1] * 8) == 8
+    wl = weights(30, 248320, 4096)
+    L = q4k.Weight(wl, 248320, 4096)
+    logits = torch.empty((8, 248320), device=gpu)
+    q4k.linear(rows, L, 8, logits, query_counts=[8])
+    torch.cuda.synchronize()
+    assert "prefill_small" in L.kernel_name(2)
+    ref = oracle.linear(rows.cpu().numpy(), wl, 248320, 4096)
+    assert row_rel_err(logits.cpu().numpy(), ref) <= TOL
+
+
+def test_config4_long_prefill(q4k, oracle, gpu):
+    m = 2048
+    wg, wu, wd = weights(40, 12288, 4096), weights(41, 12288, 4096), weights(42, 4096, 12288)
+    G, U, D = q4k.Weight(wg, 12288, 4096), q4k.Weight(wu, 12288, 4096), q4k.Weight(wd, 4096, 12288)
+    x = acts(4, m, 4096)
+    xt = _t(x, gpu)
+    gate = torch.empty((m, 12288), device=gpu)
+    q4k.mlp_gate_up(xt, G, U, m, gate, query_counts=[m])
+    out = torch.empty((m, 4096), device=gpu)
+    q4k.linear(gate, D, m, out, query_counts=[m])
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(4).choice(m, 64, replace=False)
+    g_gpu = gate.cpu().numpy()
+    assert row_rel_err(g_gpu[rows], oracle.mlp_gate_up(x[rows], wg, wu, 12288, 4096)) <= TOL
+    assert row_rel_err(out.cpu().numpy()[rows], oracle.linear(g_gpu[rows], wd, 4096, 12288)) <= TOL
+    # Linearity over every row of the full-size gate projection.
+    xa = acts(44, m, 4096)
+    xb = x - xa
+    ya, yb, yab = (torch.empty((m, 12288), device=gpu) for _ in range(3))
+    for xx, yy in ((xa, ya), (xb, yb), (x, yab)):
+        q4k.linear(_t(xx, gpu), G, m, yy, query_counts=[m])
+    torch.cuda.synchronize()
+    lin = (ya + yb).cpu().numpy()
+    assert row_rel_err(lin, yab.cpu().numpy()) <= 2 * TOL

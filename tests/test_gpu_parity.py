@@ -1,0 +1,217 @@
+"""HIP path vs the CPU oracle on identical seeded inputs (run on the GPU box).
+
+Bar: max over output rows of ||y - ref|| / ||ref|| <= 1e-3,
+ref = the oracle's fp32-accumulated Q4_K dequant-dot on the same inputs.
+The GEMV rounds activations to fp16 (row-scaled, weights exact); the GEMM
+also rounds dequantised weights to fp16 as the reference's prefill tiles do
+(quant_linear.metal:43,45).  Expected error is ~3e-4 and ~4e-4 respectively.
+"""
+import numpy as np
+import pytest
+import torch
+
+from q4k_ref import make_q4k, make_x, row_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _t(a, dev, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
+
+
+def _run(q4k, oracle, gpu, seed, m, n, k, post=0, dtype=torch.float32, counts=None, xscale=1.0):
+    rng = np.random.default_rng(seed)
+    w = make_q4k(rng, n, k)
+    x = make_x(rng, m, k, xscale)
+    aux = make_x(rng, m, n, 2.0) if post else None
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    xq = x.astype(npdt)
+    W = q4k.Weight(w, n, k)
+    xt = _t(xq, gpu, dtype)
+    y = torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+    auxt = None
+    if post:
+        y.copy_(_t(aux.astype(npdt), gpu, dtype))
+        auxt = y  # in place: the reference's residual / gate-buffer aliasing
+    q4k.linear(xt, W, m, y, auxiliary=auxt, gated=(post == 2), query_counts=counts)
+    torch.cuda.synchronize()
+    ref = oracle.linear(xq, w, n, k, aux=None if aux is None else aux.astype(npdt), post=post)
+    got = y.float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    err = row_rel_err(got, ref)
+    assert err <= TOL, f"m={m} n={n} k={k} post={post} dtype={dtype}: rel err {err:.3g}"
+    return W, err
+
+
+GEMV_SHAPES = [(1, 16, 256), (1, 4096, 4096), (2, 48, 768), (7, 64, 512), (8, 12288, 4096), (8, 4096, 12288),
+               (15, 144, 1024), (16, 1024, 4096), (17, 160, 512), (31, 96, 256), (32, 4096, 4096), (33, 48, 1280),
+               (40, 6144, 4096), (48, 32, 512)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMV_SHAPES)
+def test_gemv_store(q4k, oracle, gpu, m, n, k):
+    counts = [1] * m if m <= 8 else None
+    _run(q4k, oracle, gpu, 100 + m, m, n, k, counts=counts)
+
+
+@pytest.mark.parametrize("post", [1, 2])
+@pytest.mark.parametrize("m", [1, 8, 40])
+def test_gemv_epilogues(q4k, oracle, gpu, post, m):
+    _run(q4k, oracle, gpu, 200 + m + post, m, 512, 2048, post=post, counts=[1] * m if m <= 8 else [5] * 8)
+
+
+@pytest.mark.parametrize("m,post", [(1, 0), (8, 1), (33, 2)])
+def test_gemv_f16(q4k, oracle, gpu, m, post):
+    _run(q4k, oracle, gpu, 300 + m, m, 256, 1024, post=post, dtype=torch.float16, xscale=0.25)
+
+
+GEMM_SHAPES = [(49, 64, 256), (64, 128, 512), (65, 144, 768), (128, 256, 1024), (129, 16, 256), (300, 4096, 4096),
+               (821, 6144, 4096), (257, 4096, 12288)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_gemm_store(q4k, oracle, gpu, m, n, k):
+    _run(q4k, oracle, gpu, 400 + m, m, n, k)
+
+
+@pytest.mark.parametrize("post", [1, 2])
+def test_gemm_epilogues(q4k, oracle, gpu, post):
+    _run(q4k, oracle, gpu, 500 + post, 200, 384, 1024, post=post)
+
+
+@pytest.mark.parametrize("post", [0, 1, 2])
+def test_gemm_f16(q4k, oracle, gpu, post):
+    _run(q4k, oracle, gpu, 600 + post, 130, 256, 1024, post=post, dtype=torch.float16, xscale=0.25)
+
+
+def test_rows_beyond_fp16_range(q4k, oracle, gpu):
+    """Rows of 1e6-scale and 1e-30-scale activations and an all-zero row: the
+    per-row power-of-two staging keeps every path finite and accurate."""
+    rng = np.random.default_rng(700)
+    for m in (5, 70):
+        n, k = 256, 1024
+        w = make_q4k(rng, n, k)
+        x = make_x(rng, m, k)
+        x[0] *= 1e6
+        x[1] *= 1e-30
+        x[2] = 0
+        W = q4k.Weight(w, n, k)
+        y = torch.empty((m, n), device=gpu)
+        q4k.linear(_t(x, gpu), W, m, y)
+        torch.cuda.synchronize()
+        ref = oracle.linear(x, w, n, k)
+        got = y.cpu().numpy()
+        assert np.all(got[2] == 0)
+        assert row_rel_err(got, ref) <= TOL
+
+
+def test_gated_decode_fused(q4k, oracle, gpu):
+    for m, n, k in [(1, 512, 1024), (8, 12288, 4096), (17, 256, 512), (40, 1024, 4096)]:
+        rng = np.random.default_rng(800 + m)
+        wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+        x = make_x(rng, m, k, 0.5)
+        G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+        y = torch.empty((m, n), device=gpu)
+        counts = {1: [1], 8: [1] * 8, 17: [5, 5, 5, 2], 40: [5] * 8}[m]
+        q4k.linear(_t(x, gpu), G, m, y, auxiliary=U, gated=True, query_counts=counts)
+        torch.cuda.synchronize()
+        assert G.kernel_name(3).startswith("mlp_q4_k")
+        ref = oracle.mlp_gate_up(x, wg, wu, n, k)
+        assert row_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+def test_gated_prefill_two_pass(q4k, oracle, gpu):
+    """Prefill: gate (post 0) then up (post 2) in place over the gate buffer."""
+    for m in (9, 300):
+        rng = np.random.default_rng(900 + m)
+        n, k = 512, 1024
+        wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+        x = make_x(rng, m, k, 0.5)
+        G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+        y = torch.empty((m, n), device=gpu)
+        q4k.mlp_gate_up(_t(x, gpu), G, U, m, y, query_counts=[m])
+        torch.cuda.synchronize()
+        assert G.kernel_name(1) != "" and U.kernel_name(1) != ""
+        assert G.kernel_name(3) == ""
+        ref = oracle.mlp_gate_up(x, wg, wu, n, k)
+        assert row_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+def test_f16_gated_rounding(q4k, oracle, gpu):
+    rng = np.random.default_rng(950)
+    m, n, k = 8, 256, 1024
+    wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+    x = make_x(rng, m, k, 0.1).astype(np.float16)
+    G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+    y = torch.empty((m, n), device=gpu, dtype=torch.float16)
+    q4k.mlp_gate_up(_t(x, gpu, torch.float16), G, U, m, y, query_counts=[1] * 8)
+    torch.cuda.synchronize()
+    assert row_rel_err(y.float().cpu().numpy(), oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
+
+
+def test_selection_cache(q4k, gpu):
+    rng = np.random.default_rng(960)
+    n, k = 64, 256
+    W = q4k.Weight(make_q4k(rng, n, k), n, k)
+    assert all(W.kernel_name(p) == "" for p in range(4))
+    for counts, phase in [([1] * 8, 0), ([8], 2), ([100], 1)]:
+        m = sum(counts)
+        y = torch.empty((m, n), device=gpu)
+        q4k.linear(torch.randn(m, k, device=gpu), W, m, y, query_counts=counts)
+        assert W.kernel_name(phase) != ""
+    torch.cuda.synchronize()
+    names = [W.kernel_name(p) for p in range(3)]
+    assert "decode" in names[0] and "prefill" in names[1] and "prefill_small" in names[2]
+    W.prepare(3)
+    assert "gate_up" in W.kernel_name(3)
+
+
+def test_alias_rules(q4k, gpu):
+    n, k = 64, 256
+    W = q4k.Weight(make_q4k(np.random.default_rng(970), n, k), n, k)
+    buf = torch.zeros(8 * max(n, k), device=gpu)
+    x = buf[: 4 * k].view(4, k)
+    y = buf[k: k + 4 * n].view(4, n)
+    with pytest.raises(q4k.Q4KError) as e:
+        q4k.linear(x, W, 4, y)
+    assert e.value.code == -4
+
+
+def test_nondefault_stream(q4k, oracle, gpu):
+    rng = np.random.default_rng(980)
+    m, n, k = 8, 1024, 2048
+    w = make_q4k(rng, n, k)
+    x = make_x(rng, m, k)
+    W = q4k.Weight(w, n, k)
+    s = torch.cuda.Stream()
+    xt = _t(x, gpu)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        y = torch.empty((m, n), device=gpu)
+        q4k.linear(xt, W, m, y, stream=s)
+    s.synchronize()
+    assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k)) <= TOL
+
+
+def test_weight_from_device_bytes(q4k, oracle, gpu):
+    rng = np.random.default_rng(990)
+    m, n, k = 3, 96, 768
+    w = make_q4k(rng, n, k)
+    W = q4k.Weight(torch.from_numpy(w.reshape(-1)).to(gpu), n, k)
+    x = make_x(rng, m, k)
+    y = torch.empty((m, n), device=gpu)
+    q4k.linear(_t(x, gpu), W, m, y)
+    torch.cuda.synchronize()
+    assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k)) <= TOL
+
+
+def test_gather_rows(q4k, gpu):
+    lengths = [512, 37, 1, 1, 200, 5, 1, 64]
+    x = torch.randn(sum(lengths), 4096, device=gpu)
+    out = torch.empty(8, 4096, device=gpu)
+    rows = q4k.gather_rows(x, out, lengths, [1] * 8)
+    torch.cuda.synchronize()
+    assert rows == 8
+    last = np.cumsum(lengths) - 1
+    assert torch.equal(out, x[torch.as_tensor(last, device=gpu)])
