@@ -271,13 +271,16 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
   Workspace& ws = workspace(w->device);
   std::lock_guard<std::mutex> lock(ws.mu);
   const bool gemv = kern.kind != kGemm || m <= 16u * kGemvMaxRowTiles;
-  const size_t rows = gemv ? (size_t)((m + 15) / 16) * 16 : m;
-  int rc = ensure_workspace(ws, w->device, rows, w->k);
+  const bool split = gemv && gemv_split((int)m);
+  const int rows = split ? 2 * (int)m : (int)m;
+  const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : m;
+  int rc = ensure_workspace(ws, w->device, ws_rows, w->k);
   if (rc)
     return rc;
   {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
-    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, ws.scale, (int)m, (int)w->k, gemv), "stage_x launch");
+    const int mode = !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, ws.scale, (int)m, (int)w->k, mode), "stage_x launch");
   }
   if (gemv) {
     GemvArgs a;
@@ -292,8 +295,10 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
     a.k = (int)w->k;
     a.nb = (int)(w->k / 256);
     a.post = (int)post;
+    a.rows = rows;
+    a.split = split ? 1 : 0;
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape((int)m, (int)w->n, wu != nullptr), wu != nullptr), "gemv launch");
+    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr), wu != nullptr), "gemv launch");
   } else {
     GemmArgs a;
     a.w = w->data;

@@ -42,6 +42,8 @@ struct GemvArgs {
   void* y;
   const void* aux;
   int m, n, k, nb, post;
+  int rows;  // staged fragment rows: 2m when split (rows m.. hold the low parts), else m
+  int split;
 };
 
 struct GemmArgs {
@@ -58,18 +60,34 @@ struct GatherIndex {
   uint32_t src[64];
 };
 
+// Activation staging layouts.
+enum StageMode : int {
+  kStageRowMajor = 0,  // fp16 [m, k] (GEMM A operand)
+  kStageFrag = 1,      // fp16 in GEMV fragment order, m rows
+  kStageFragSplit = 2  // fragment order, rows [0, m) = hi, rows [m, 2m) = lo
+};
+
 // Stage x [m, k] (fp32 or fp16) as fp16 scaled by a per-row power of two
 // (so rows with |x| beyond the fp16 range stay finite); rowscale[r] receives
-// the factor that undoes the scaling.  frag selects the GEMV fragment order,
-// otherwise row-major.
-hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, bool frag);
+// the factor that undoes the scaling.  In the split mode each scaled value v
+// is carried as hi = fp16(v) plus lo = fp16(v - hi), about 22 significant bits.
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, int mode);
+
+// GEMV rows that the fragment layout holds for m activation rows: the split
+// (hi + lo) form while it fits the kernel's row tiles (2m <= 48), else m.
+inline bool gemv_split(int m) {
+  return 2 * m <= 48;
+}
 
 // Launch geometry of the GEMV: 16-row tiles of activations, 16-column tiles
 // of weights per workgroup, waves per workgroup (each takes 1/waves of K).
 struct GemvShape {
   int row_tiles = 1, tiles = 1, waves = 8;
 };
-GemvShape gemv_shape(int m, int n, bool gated);
+// rows = staged fragment rows (2m when split).  The environment variables
+// Q4K_GEMV_TILES (1 or 2) and Q4K_GEMV_WAVES (4, 8 or 16) override the
+// column tiles and waves per workgroup, for tuning.
+GemvShape gemv_shape(int rows, int n, int nb, bool gated);
 
 // GEMV for m <= 48.
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated);

@@ -11,6 +11,7 @@
 // and backend/metal/kernel/fused_kernels.metal:11-78.
 #include <float.h>
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 
 #include "q4k_internal.h"
 
@@ -91,24 +92,13 @@ __device__ __forceinline__ h8_t quant_times_scale(uint32_t wa, uint32_t wb, uint
 }
 
 // ----------------------------------------------------------------------------
-// Activation staging.
+// Activation staging.  One workgroup per row.  Rows of up to 256 * 8 * kStageRegChunks
+// elements are held in registers between the max reduction and the
+// conversion (one read of x); longer rows are read twice.
 // ----------------------------------------------------------------------------
-template <typename InT, bool FRAG>
-__global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale, int m,
-                                                      int k) {
-  const int row = blockIdx.x;
-  if (row >= m)
-    return;
-  const InT* xr = x + (size_t)row * k;
-  const int chunks = k >> 3, nb = k >> 8;
-  float mx = 0.0f;
-  for (int c = threadIdx.x; c < chunks; c += 256) {
-    float v[8];
-    load8(xr + c * 8, v);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      mx = fmaxf(mx, fabsf(v[i]));
-  }
+constexpr int kStageRegChunks = 6;
+
+__device__ __forceinline__ float block_max_256(float mx) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1)
     mx = fmaxf(mx, __shfl_xor(mx, off));
@@ -116,7 +106,65 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
   if ((threadIdx.x & 63) == 0)
     red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Element offset of (row, 8-element chunk c) in the GEMV fragment layout:
+// fragment ((row / 16) * nb + b) * 8 + s holds, for lane 16g + (row % 16),
+// elements b*256 + 64g + 32*(s/4) + 8*(s%4) + [0, 8).
+__device__ __forceinline__ size_t frag_offset(int row, int c, int nb) {
+  const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, sl = ((e >> 5) & 1) * 4 + ((e >> 3) & 3);
+  return ((((size_t)(row >> 4) * nb + b) * 8 + sl) * 64 + (g * 16 + (row & 15))) * 8;
+}
+
+template <int MODE>
+__device__ __forceinline__ void stage_store(_Float16* xo, int row, int c, int m, int k, int nb, const float* v, float up) {
+  h8_t hi, lo;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = v[i] * up;
+    hi[i] = (_Float16)t;
+    lo[i] = (_Float16)(t - (float)hi[i]);
+  }
+  if (MODE == kStageRowMajor) {
+    *reinterpret_cast<h8_t*>(xo + (size_t)row * k + (size_t)c * 8) = hi;
+  } else {
+    *reinterpret_cast<h8_t*>(xo + frag_offset(row, c, nb)) = hi;
+    if (MODE == kStageFragSplit)
+      *reinterpret_cast<h8_t*>(xo + frag_offset(m + row, c, nb)) = lo;
+  }
+}
+
+template <typename InT, int MODE>
+__global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale, int m,
+                                                      int k) {
+  const int row = blockIdx.x;
+  const InT* xr = x + (size_t)row * k;
+  const int chunks = k >> 3, nb = k >> 8;
+  const bool in_regs = chunks <= 256 * kStageRegChunks;
+  float v[kStageRegChunks][8];
+  float mx = 0.0f;
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kStageRegChunks; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < chunks) {
+        load8(xr + c * 8, v[j]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          mx = fmaxf(mx, fabsf(v[j][i]));
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+      float t[8];
+      load8(xr + c * 8, t);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        mx = fmaxf(mx, fabsf(t[i]));
+    }
+  }
+  mx = block_max_256(mx);
   // Scale the row so its largest magnitude lands in [2^14, 2^15): finite in
   // fp16 with the full 11-bit significand for every large element.
   float up = 1.0f, down = 1.0f;
@@ -129,21 +177,19 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
   }
   if (threadIdx.x == 0)
     rowscale[row] = down;
-  for (int c = threadIdx.x; c < chunks; c += 256) {
-    float v[8];
-    load8(xr + c * 8, v);
-    h8_t o;
+  if (in_regs) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      o[i] = (_Float16)(v[i] * up);
-    size_t dst;
-    if (FRAG) {
-      const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, s = ((e >> 5) & 1) * 4 + ((e >> 3) & 3);
-      dst = ((((size_t)(row >> 4) * nb + b) * 8 + s) * 64 + (g * 16 + (row & 15))) * 8;
-    } else {
-      dst = (size_t)row * k + (size_t)c * 8;
+    for (int j = 0; j < kStageRegChunks; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < chunks)
+        stage_store<MODE>(xo, row, c, m, k, nb, v[j], up);
     }
-    *reinterpret_cast<h8_t*>(xo + dst) = o;
+  } else {
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+      float t[8];
+      load8(xr + c * 8, t);
+      stage_store<MODE>(xo, row, c, m, k, nb, t, up);
+    }
   }
 }
 
@@ -203,7 +249,7 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
     h8_t xa[RT][8];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const bool live = rt * 16 + col < a.m;
+      const bool live = rt * 16 + col < a.rows;
       const h8_t* xp = reinterpret_cast<const h8_t*>(a.xf) + (size_t)(rt * nb + b) * 8 * 64 + lane;
 #pragma unroll
       for (int s = 0; s < 8; ++s)
@@ -254,54 +300,57 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
     cur = next;
   }
 
-  // Cross-wave reduction: lane-major so each wave's store is conflict free.
-  constexpr int NV = NM * T * RT;
-  __shared__ f4_t red[W][NV][64];
+  // Cross-wave reduction through LDS in [wave][matrix][tile][row][column]
+  // order (the C fragment of lane l is rows 4*(l/16)+v, column l%16).
+  constexpr int ROWS = RT * 16;
+  __shared__ float red[W][NM][T][ROWS][16];
 #pragma unroll
   for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
-        red[wave][(mi * T + t) * RT + rt][lane] = acc[mi][t][rt];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          red[wave][mi][t][rt * 16 + 4 * g + v][col] = acc[mi][t][rt][v];
   __syncthreads();
 
-  for (int item = tid; item < T * RT * 64; item += 64 * W) {
-    const int l = item & 63, tr = item >> 6, t = tr / RT, rt = tr % RT;
-    f4_t s[NM];
+  // Epilogue: one thread per output (row, column); split rows add their low half.
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  for (int item = tid; item < a.m * 16 * T; item += 64 * W) {
+    const int row = item / (16 * T), c = item % (16 * T), t = c >> 4, cc = c & 15;
+    float s[NM];
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
-      s[mi] = red[0][(mi * T + t) * RT + rt][l];
+      float v = 0.0f;
 #pragma unroll
-      for (int w = 1; w < W; ++w)
-        s[mi] += red[w][(mi * T + t) * RT + rt][l];
-    }
-    const int n = (ct0 + t) * 16 + (l & 15);
-    OutT* y = reinterpret_cast<OutT*>(a.y);
-    const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+      for (int w = 0; w < W; ++w)
+        v += red[w][mi][t][row][cc];
+      if (a.split) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = rt * 16 + 4 * (l >> 4) + v;
-      if (row >= a.m)
-        continue;
-      const float scale = a.rowscale[row];
-      const size_t o = (size_t)row * a.n + n;
-      float out;
-      if (GATED) {
-        float gv = s[0][v] * scale, uv = s[NM - 1][v] * scale;
-        if (sizeof(OutT) == 2) {
-          gv = round_half(gv);
-          uv = round_half(uv);
-        }
-        out = silu(gv) * uv;
-      } else {
-        float acc_v = s[0][v] * scale;
-        if (sizeof(OutT) == 2)
-          acc_v = round_half(acc_v);
-        out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
+        for (int w = 0; w < W; ++w)
+          v += red[w][mi][t][a.m + row][cc];
       }
-      store_elem(y, o, out);
+      s[mi] = v;
     }
+    const float scale = a.rowscale[row];
+    const size_t o = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
+    float out;
+    if (GATED) {
+      float gv = s[0] * scale, uv = s[NM - 1] * scale;
+      if (sizeof(OutT) == 2) {
+        gv = round_half(gv);
+        uv = round_half(uv);
+      }
+      out = silu(gv) * uv;
+    } else {
+      float acc_v = s[0] * scale;
+      if (sizeof(OutT) == 2)
+        acc_v = round_half(acc_v);
+      out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
+    }
+    store_elem(y, o, out);
   }
 }
 
@@ -472,57 +521,86 @@ hipError_t gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
   return hipGetLastError();
 }
 
+template <int RT, int T, bool GATED>
+hipError_t gemv_by_waves(hipStream_t s, const GemvArgs& a, int dtype, int waves) {
+  if constexpr (RT == 1) {
+    if (waves == 16)
+      return gemv_launch<RT, T, 16, GATED>(s, a, dtype);
+  }
+  if (waves >= 8)
+    return gemv_launch<RT, T, 8, GATED>(s, a, dtype);
+  return gemv_launch<RT, T, 4, GATED>(s, a, dtype);
+}
+
+// Instances kept within the register file (no spills): 16 waves only with
+// one row tile; two column tiles only with one row tile and no gate/up pair.
 template <bool GATED>
 hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape) {
-  // Instances (see gemv_shape): one row tile with (1 tile, 16 waves),
-  // (1 tile, 8 waves) or (2 tiles, 8 waves); two or three row tiles with
-  // 8 waves, two column tiles only without the gate/up pair (register budget).
   if (shape.row_tiles == 1) {
-    if (shape.tiles == 2)
-      return gemv_launch<1, 2, 8, GATED>(s, a, dtype);
-    return shape.waves == 16 ? gemv_launch<1, 1, 16, GATED>(s, a, dtype) : gemv_launch<1, 1, 8, GATED>(s, a, dtype);
+    if constexpr (!GATED) {
+      if (shape.tiles == 2)
+        return gemv_by_waves<1, 2, false>(s, a, dtype, shape.waves);
+    }
+    return gemv_by_waves<1, 1, GATED>(s, a, dtype, shape.waves);
   }
-  if constexpr (!GATED) {
-    if (shape.tiles == 2)
-      return shape.row_tiles == 2 ? gemv_launch<2, 2, 8, false>(s, a, dtype) : gemv_launch<3, 2, 8, false>(s, a, dtype);
-  }
-  return shape.row_tiles == 2 ? gemv_launch<2, 1, 8, GATED>(s, a, dtype) : gemv_launch<3, 1, 8, GATED>(s, a, dtype);
+  if (shape.row_tiles == 2)
+    return gemv_by_waves<2, 1, GATED>(s, a, dtype, shape.waves);
+  return gemv_by_waves<3, 1, GATED>(s, a, dtype, shape.waves);
+}
+
+int env_int(const char* name, int fallback) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : fallback;
 }
 
 }  // namespace
 
-hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, bool frag) {
-  if (m <= 0)
-    return hipSuccess;
+template <typename InT>
+hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, float* rowscale, int m, int k, int mode) {
   const dim3 grid((unsigned)m), block(256);
-  if (dtype == kF32) {
-    if (frag)
-      stage_x_kernel<float, true><<<grid, block, 0, s>>>(static_cast<const float*>(x), xo, rowscale, m, k);
-    else
-      stage_x_kernel<float, false><<<grid, block, 0, s>>>(static_cast<const float*>(x), xo, rowscale, m, k);
-  } else {
-    if (frag)
-      stage_x_kernel<_Float16, true><<<grid, block, 0, s>>>(static_cast<const _Float16*>(x), xo, rowscale, m, k);
-    else
-      stage_x_kernel<_Float16, false><<<grid, block, 0, s>>>(static_cast<const _Float16*>(x), xo, rowscale, m, k);
-  }
+  if (mode == kStageRowMajor)
+    stage_x_kernel<InT, kStageRowMajor><<<grid, block, 0, s>>>(x, xo, rowscale, m, k);
+  else if (mode == kStageFrag)
+    stage_x_kernel<InT, kStageFrag><<<grid, block, 0, s>>>(x, xo, rowscale, m, k);
+  else
+    stage_x_kernel<InT, kStageFragSplit><<<grid, block, 0, s>>>(x, xo, rowscale, m, k);
   return hipGetLastError();
 }
 
-GemvShape gemv_shape(int m, int n, bool gated) {
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, int mode) {
+  if (m <= 0)
+    return hipSuccess;
+  if (dtype == kF32)
+    return stage_launch(s, static_cast<const float*>(x), xo, rowscale, m, k, mode);
+  return stage_launch(s, static_cast<const _Float16*>(x), xo, rowscale, m, k, mode);
+}
+
+GemvShape gemv_shape(int rows, int n, int nb, bool gated) {
   GemvShape sh;
-  sh.row_tiles = m <= 16 ? 1 : m <= 32 ? 2 : 3;
-  // Two column tiles per workgroup once that still leaves >= 384 workgroups
-  // (1.5 per CU) and the registers allow it; otherwise one.  Grids of fewer
-  // than 1024 single-tile workgroups get 16 waves each so that enough weight
-  // bytes are in flight per CU.
-  sh.tiles = (n % 32 == 0 && n / 32 >= 384 && (sh.row_tiles == 1 || !gated)) ? 2 : 1;
-  sh.waves = (sh.row_tiles == 1 && sh.tiles == 1 && n / 16 < 1024) ? 16 : 8;
+  sh.row_tiles = rows <= 16 ? 1 : rows <= 32 ? 2 : 3;
+  // One 16-column tile per workgroup (two for very wide outputs, one row tile,
+  // no gate/up pair), and enough waves per workgroup -- each taking 1/waves
+  // of K -- for about 12-16 resident waves per CU across the grid.
+  const int ctiles = n / 16;
+  static const int env_tiles = env_int("Q4K_GEMV_TILES", 0), env_waves = env_int("Q4K_GEMV_WAVES", 0);
+  sh.tiles = (sh.row_tiles == 1 && !gated && n % 32 == 0 && ctiles >= 4096) ? 2 : 1;
+  if (env_tiles == 1 || (env_tiles == 2 && sh.row_tiles == 1 && !gated && n % 32 == 0))
+    sh.tiles = env_tiles;
+  const int groups = ctiles / sh.tiles;
+  int waves = groups >= 1024 ? 4 : groups >= 512 ? 4 : groups >= 320 ? 8 : 16;
+  if (env_waves == 4 || env_waves == 8 || env_waves == 16)
+    waves = env_waves;
+  while (waves > 4 && waves > nb)
+    waves >>= 1;
+  if (sh.row_tiles > 1 && waves > 8)
+    waves = 8;
+  sh.waves = waves;
   return sh;
 }
 
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated) {
-  if (shape.row_tiles < 1 || shape.row_tiles > kGemvMaxRowTiles || a.n % (16 * shape.tiles) != 0 || a.m > 16 * shape.row_tiles)
+  if (shape.row_tiles < 1 || shape.row_tiles > kGemvMaxRowTiles || a.n % (16 * shape.tiles) != 0 || a.rows > 16 * shape.row_tiles ||
+      a.rows != (a.split ? 2 * a.m : a.m))
     return hipErrorInvalidValue;
   return gated ? gemv_dispatch<true>(s, a, dtype, shape) : gemv_dispatch<false>(s, a, dtype, shape);
 }
