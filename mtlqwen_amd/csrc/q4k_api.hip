@@ -58,7 +58,7 @@ struct Kernel {
 // still name them.  Growth is bounded by the largest m * k staged.
 struct Workspace {
   std::mutex mu;
-  _Float16* x = nullptr;
+  _Float16* x = nullptr;  // staged activations, then the sub-block sums
   size_t x_elems = 0;
   float* scale = nullptr;
   size_t scale_elems = 0;
@@ -223,9 +223,9 @@ Workspace& workspace(int device) {
   return g_ws[device & 63];
 }
 
-// Grows the device's staging buffers to hold `rows` x `k` fp16 plus row scales.
-int ensure_workspace(Workspace& ws, int device, size_t rows, size_t k) {
-  const size_t need = rows * k, need_s = rows < 64 ? 64 : rows;
+// Grows the device's staging buffers to `halves` fp16 values plus `rows` row scales.
+int ensure_workspace(Workspace& ws, int device, size_t halves, size_t rows) {
+  const size_t need = halves, need_s = rows < 64 ? 64 : rows;
   if (ws.x_elems >= need && ws.scale_elems >= need_s)
     return Q4K_OK;
   if (ws.x_elems < need) {
@@ -274,19 +274,23 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
   const bool split = gemv && gemv_split((int)m);
   const int rows = split ? 2 * (int)m : (int)m;
   const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : m;
-  int rc = ensure_workspace(ws, w->device, ws_rows, w->k);
+  // xs is read 32 lanes at a time from its start; +128 halves of slack.
+  const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : 0;
+  int rc = ensure_workspace(ws, w->device, ws_rows * w->k + xs_halves, ws_rows);
   if (rc)
     return rc;
+  _Float16* xs = ws.x + ws_rows * w->k;
   {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
     const int mode = !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
-    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, ws.scale, (int)m, (int)w->k, mode), "stage_x launch");
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode), "stage_x launch");
   }
   if (gemv) {
     GemvArgs a;
     a.w = w->data;
     a.wu = wu ? wu->data : w->data;
     a.xf = ws.x;
+    a.xs = xs;
     a.rowscale = ws.scale;
     a.y = y;
     a.aux = aux;

@@ -38,6 +38,7 @@ struct GemvArgs {
   const uint8_t* w;       // tiled weights (gate weights when gated)
   const uint8_t* wu;      // up weights when gated, else unused
   const _Float16* xf;     // staged activations, fragment order
+  const _Float16* xs;     // staged sub-block sums / 32, min-term fragment order
   const float* rowscale;  // per-row power-of-two unscale factor
   void* y;
   const void* aux;
@@ -71,7 +72,15 @@ enum StageMode : int {
 // (so rows with |x| beyond the fp16 range stay finite); rowscale[r] receives
 // the factor that undoes the scaling.  In the split mode each scaled value v
 // is carried as hi = fp16(v) plus lo = fp16(v - hi), about 22 significant bits.
-hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, int mode);
+// The fragment modes also write xs: each 32-element sub-block's sum of the
+// scaled values, divided by 32 (so it stays within fp16), hi/lo like x.
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode);
+
+// Halves of the sub-block-sum fragments for `rows` staged rows: per 16-row
+// tile and block, 32 lanes x 4 halves.
+inline size_t gemv_xs_halves(int rows, int k) {
+  return (size_t)((rows + 15) / 16) * (k / 256) * 128;
+}
 
 // GEMV rows that the fragment layout holds for m activation rows: the split
 // (hi + lo) form while it fits the kernel's row tiles (2m <= 48), else m.

@@ -78,17 +78,70 @@ __device__ __forceinline__ void scale_min_pair(u4_t hd, int g, uint32_t& sc0, ui
   }
 }
 
+// (a & mask) | bits in one v_and_or_b32.  Written as asm because gfx9 VOP3
+// encodings cannot take the two literal constants the compiler would
+// otherwise need, so it splits the expression into v_and + v_or.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+  return r;
+}
+
+__device__ __forceinline__ h2_t as_h2(uint32_t v) {
+  return __builtin_bit_cast(h2_t, v);
+}
+
+__device__ __forceinline__ uint32_t as_u32(h2_t v) {
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Eight quants of one slab pair as exact fp16 products q * sc.
 // (w & mask) | 0x6400 is the fp16 value 1024 + q (low nibble, mask 0x000F) or
 // 1024 + 16q (high nibble, mask 0x00F0); one fused multiply-add with
 // (sc, -1024 sc) or (sc/16, -64 sc) leaves q*sc <= 945, exact in fp16.
-__device__ __forceinline__ h8_t quant_times_scale(uint32_t wa, uint32_t wb, uint32_t mask, h2_t mul, h2_t add) {
+__device__ __forceinline__ h8_t quant_times_scale(uint32_t wa, uint32_t wb, uint32_t mask, uint32_t bias, h2_t mul, h2_t add) {
   const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-  h2_t v0 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wa & mask) | 0x64006400u), mul, add);
-  h2_t v1 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wa8 & mask) | 0x64006400u), mul, add);
-  h2_t v2 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wb & mask) | 0x64006400u), mul, add);
-  h2_t v3 = __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (wb8 & mask) | 0x64006400u), mul, add);
-  return h8_t{v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+  const h2_t v0 = __builtin_elementwise_fma(as_h2(and_or(wa, mask, bias)), mul, add);
+  const h2_t v1 = __builtin_elementwise_fma(as_h2(and_or(wa8, mask, bias)), mul, add);
+  const h2_t v2 = __builtin_elementwise_fma(as_h2(and_or(wb, mask, bias)), mul, add);
+  const h2_t v3 = __builtin_elementwise_fma(as_h2(and_or(wb8, mask, bias)), mul, add);
+  return __builtin_bit_cast(h8_t, u4_t{as_u32(v0), as_u32(v1), as_u32(v2), as_u32(v3)});
+}
+
+// Per-lane constants of one tile-block header for lane group g: the fp16
+// multipliers of the low / high nibbles (sub-blocks 2g, 2g+1) and the min
+// fragment 32 * m_{4g..4g+3} (zero for g >= 2: k = 8..15 of the 16x16x16 MFMA
+// are unused).  quant_linear.metal:12-20 unpacking, two fields at a time.
+struct BlockConsts {
+  float d, dmin;
+  h2_t mul_lo, add_lo, mul_hi, add_hi;
+  h4_t bmin;
+};
+
+__device__ __forceinline__ BlockConsts block_consts(u4_t hd, int g) {
+  BlockConsts k;
+  k.d = half_bits_to_float(hd.x & 0xffffu);
+  k.dmin = half_bits_to_float(hd.x >> 16);
+  const uint32_t sh = 16u * (uint32_t)(g & 1);
+  const uint32_t a = hd.y >> sh, c = hd.w >> sh;
+  // bytes 0, 1 = sc_{2g}, sc_{2g+1}
+  const uint32_t scp = g < 2 ? (a & 0x3F3Fu) : ((c & 0x0F0Fu) | ((a >> 2) & 0x3030u));
+  const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const h2_t kneg1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  // perm(0x64646464, v, sel) interleaves bytes of v with 0x64: fp16 1024 + byte.
+  k.mul_lo = as_h2(__builtin_amdgcn_perm(0x64646464u, scp, 0x04000400u)) - k1024;
+  k.add_lo = k.mul_lo * kneg1024;
+  const h2_t p_hi = as_h2(__builtin_amdgcn_perm(0x64646464u, scp, 0x04010401u));
+  k.mul_hi = __builtin_elementwise_fma(p_hi, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-64.0f, (_Float16)-64.0f});
+  k.add_hi = k.mul_hi * kneg1024;
+  // bytes 0..3 = m_{4g}..m_{4g+3} for g < 2; zero for g >= 2 (k = 8..15 unused)
+  const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+  const uint32_t mb = g == 0 ? (hd.z & 0x3F3F3F3Fu) : g == 1 ? m47 : 0u;
+  const h2_t k32 = {(_Float16)32.0f, (_Float16)32.0f}, kneg32768 = {(_Float16)-32768.0f, (_Float16)-32768.0f};
+  const h2_t m01 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04010400u)), k32, kneg32768);
+  const h2_t m23 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04030402u)), k32, kneg32768);
+  k.bmin = h4_t{m01[0], m01[1], m23[0], m23[1]};
+  return k;
 }
 
 // ----------------------------------------------------------------------------
@@ -117,32 +170,58 @@ __device__ __forceinline__ size_t frag_offset(int row, int c, int nb) {
   return ((((size_t)(row >> 4) * nb + b) * 8 + sl) * 64 + (g * 16 + (row & 15))) * 8;
 }
 
+// Half index of (row, sub-block j of block b) in the min-term fragments: per
+// (row tile, block), lane 16 * (j / 4) + row % 16 holds j % 4 of 4 halves --
+// the A operand of v_mfma_f32_16x16x16_f16 with k = sub-block (8 of 16 used).
+__device__ __forceinline__ size_t xs_offset(int row, int b, int j, int nb) {
+  return (((size_t)(row >> 4) * nb + b) * 32 + 16 * (j >> 2) + (row & 15)) * 4 + (j & 3);
+}
+
+// Converts and stores one 8-element chunk; all 256 threads of the workgroup
+// must call it together (the sub-block sum is reduced over 4 lanes).
 template <int MODE>
-__device__ __forceinline__ void stage_store(_Float16* xo, int row, int c, int m, int k, int nb, const float* v, float up) {
+__device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row, int c, bool live, int m, int k, int nb, const float* v,
+                                            float up) {
   h8_t hi, lo;
+  float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float t = v[i] * up;
     hi[i] = (_Float16)t;
     lo[i] = (_Float16)(t - (float)hi[i]);
+    sum += t;
   }
   if (MODE == kStageRowMajor) {
-    *reinterpret_cast<h8_t*>(xo + (size_t)row * k + (size_t)c * 8) = hi;
-  } else {
+    if (live)
+      *reinterpret_cast<h8_t*>(xo + (size_t)row * k + (size_t)c * 8) = hi;
+    return;
+  }
+  if (live) {
     *reinterpret_cast<h8_t*>(xo + frag_offset(row, c, nb)) = hi;
     if (MODE == kStageFragSplit)
       *reinterpret_cast<h8_t*>(xo + frag_offset(m + row, c, nb)) = lo;
   }
+  // Chunks 4q..4q+3 (lanes 4q..4q+3) form one sub-block.
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  if (live && (c & 3) == 0) {
+    const float s32 = sum * 0.03125f;
+    const _Float16 sh = (_Float16)s32;
+    const int b = c >> 5, j = (c >> 2) & 7;
+    xs[xs_offset(row, b, j, nb)] = sh;
+    if (MODE == kStageFragSplit)
+      xs[xs_offset(m + row, b, j, nb)] = (_Float16)(s32 - (float)sh);
+  }
 }
 
 template <typename InT, int MODE>
-__global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale, int m,
-                                                      int k) {
+__global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, _Float16* __restrict__ xs,
+                                                      float* __restrict__ rowscale, int m, int k) {
   const int row = blockIdx.x;
   const InT* xr = x + (size_t)row * k;
   const int chunks = k >> 3, nb = k >> 8;
   const bool in_regs = chunks <= 256 * kStageRegChunks;
-  float v[kStageRegChunks][8];
+  float v[kStageRegChunks][8] = {};
   float mx = 0.0f;
   if (in_regs) {
 #pragma unroll
@@ -181,14 +260,16 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
 #pragma unroll
     for (int j = 0; j < kStageRegChunks; ++j) {
       const int c = threadIdx.x + 256 * j;
-      if (c < chunks)
-        stage_store<MODE>(xo, row, c, m, k, nb, v[j], up);
+      if (256 * j < chunks)  // uniform: whole groups of 4 lanes take part
+        stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, v[j], up);
     }
   } else {
-    for (int c = threadIdx.x; c < chunks; c += 256) {
-      float t[8];
-      load8(xr + c * 8, t);
-      stage_store<MODE>(xo, row, c, m, k, nb, t, up);
+    for (int c0 = 0; c0 < chunks; c0 += 256) {
+      const int c = c0 + threadIdx.x;
+      float t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (c < chunks)
+        load8(xr + c * 8, t);
+      stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, t, up);
     }
   }
 }
@@ -200,9 +281,10 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
 // are split into W contiguous ranges, one per wave, and the partial sums are
 // reduced through LDS.  Per tile-block a wave issues three fully contiguous
 // 16-byte loads per lane (two quant slabs + header) and, per 16-row tile of
-// activations, 16 MFMAs: 8 with B = q*sc (exact fp16) and 8 with B = m_j, then
-// acc += d * C_q - dmin * C_m in fp32 -- the decode form of
-// quant_linear.metal:288-302 with the integer parts on the matrix core.
+// activations, 8 MFMAs with B = q*sc (exact fp16) plus one 16x16x16 MFMA of
+// the sub-block sums against 32*m_j, then acc += d * C_q - dmin * C_m in fp32
+// -- the decode form of quant_linear.metal:288-302 with the integer parts on
+// the matrix core.
 // ----------------------------------------------------------------------------
 template <int T, int NM>
 struct TileWords {
@@ -222,7 +304,9 @@ __device__ __forceinline__ void load_tile_words(TileWords<T, NM>& tw, const Gemv
     }
 }
 
-template <int RT, int T, int W, bool GATED, typename OutT>
+// BPW > 0: every wave owns exactly BPW blocks (nb == W * BPW) and issues all of
+// their weight loads at once; BPW == 0: any split, with a one-block prefetch.
+template <int RT, int T, int W, int BPW, bool GATED, typename OutT>
 __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
   constexpr int NM = GATED ? 2 : 1;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -240,64 +324,85 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
       for (int rt = 0; rt < RT; ++rt)
         acc[mi][t][rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  TileWords<T, NM> cur, next;
-  if (b0 < b1)
-    load_tile_words(cur, a, ct0, b0, nb, lane, col);
-  for (int b = b0; b < b1; ++b) {
-    // Activations of this block first, then the next block's weights: the
-    // in-order vmcnt wait for the activations then leaves the prefetch in flight.
-    h8_t xa[RT][8];
+  // Dead activation rows (>= a.rows, inside the padded 16-row tiles) are
+  // loaded unmasked: in a matrix product a garbage A row only reaches its own
+  // C row, which the epilogue never reads.  Branch-free loads keep the vmcnt
+  // waits exact.
+  auto load_x = [&](h8_t (&xa)[RT][8], h4_t (&xsa)[RT], int b) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const bool live = rt * 16 + col < a.rows;
       const h8_t* xp = reinterpret_cast<const h8_t*>(a.xf) + (size_t)(rt * nb + b) * 8 * 64 + lane;
 #pragma unroll
       for (int s = 0; s < 8; ++s)
-        xa[rt][s] = live ? xp[s * 64] : h8_t{};
+        xa[rt][s] = xp[s * 64];
+      xsa[rt] = reinterpret_cast<const h4_t*>(a.xs)[(size_t)(rt * nb + b) * 32 + (lane & 31)];
     }
-    if (b + 1 < b1)
-      load_tile_words(next, a, ct0, b + 1, nb, lane, col);
+  };
+  auto compute = [&](const TileWords<T, NM>& cur, const h8_t (&xa)[RT][8], const h4_t (&xsa)[RT]) {
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const u4_t h = cur.hd[mi][t];
-        const float d = half_bits_to_float(h.x & 0xffffu), dmin = half_bits_to_float(h.x >> 16);
-        uint32_t sc0, m0, sc1, m1;
-        scale_min_pair(h, g, sc0, m0, sc1, m1);
-        const _Float16 fsc0 = (_Float16)(float)sc0;
-        const h2_t mul_lo = {fsc0, fsc0};
-        const h2_t add_lo = {(_Float16)(-1024.0f * (float)sc0), (_Float16)(-1024.0f * (float)sc0)};
-        const h2_t mul_hi = {(_Float16)((float)sc1 * 0.0625f), (_Float16)((float)sc1 * 0.0625f)};
-        const h2_t add_hi = {(_Float16)(-64.0f * (float)sc1), (_Float16)(-64.0f * (float)sc1)};
-        const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1;
-        const h8_t bm_lo = {fm0, fm0, fm0, fm0, fm0, fm0, fm0, fm0};
-        const h8_t bm_hi = {fm1, fm1, fm1, fm1, fm1, fm1, fm1, fm1};
-        f4_t cq[RT], cm[RT];
+        const BlockConsts kc = block_consts(cur.hd[mi][t], g);
+        f4_t cq[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
-          cq[rt] = cm[rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          cq[rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const u4_t q = u < 2 ? cur.q0[mi][t] : cur.q1[mi][t];
           const uint32_t wa = q[2 * (u & 1)], wb = q[2 * (u & 1) + 1];
-          const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, mul_lo, add_lo);
-          const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, mul_hi, add_hi);
+          const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+          const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
             cq[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][u], blo, cq[rt], 0, 0, 0);
             cq[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][4 + u], bhi, cq[rt], 0, 0, 0);
-            cm[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][u], bm_lo, cm[rt], 0, 0, 0);
-            cm[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][4 + u], bm_hi, cm[rt], 0, 0, 0);
           }
         }
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt) {
+          // min term: sum_j (xs_j / 32) * (32 m_j), k = sub-block
+          const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            acc[mi][t][rt][v] = fmaf(d, cq[rt][v], fmaf(-dmin, cm[rt][v], acc[mi][t][rt][v]));
+            acc[mi][t][rt][v] = fmaf(kc.d, cq[rt][v], fmaf(-kc.dmin, cm[v], acc[mi][t][rt][v]));
+        }
       }
-    cur = next;
+  };
+
+  if constexpr (BPW > 0) {
+    // Issue order for the in-order vmcnt counter: block 0's activations, all
+    // BPW blocks' weights, then each later block's activations just in time.
+    TileWords<T, NM> tw[BPW];
+    h8_t xa[RT][8];
+    h4_t xsa[RT];
+    load_x(xa, xsa, b0);
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+      load_tile_words(tw[j], a, ct0, b0 + j, nb, lane, col);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+      if (j > 0)
+        load_x(xa, xsa, b0 + j);
+      compute(tw[j], xa, xsa);
+    }
+  } else {
+    TileWords<T, NM> cur, next;
+    if (b0 < b1)
+      load_tile_words(cur, a, ct0, b0, nb, lane, col);
+    for (int b = b0; b < b1; ++b) {
+      h8_t xa[RT][8];
+      h4_t xsa[RT];
+      load_x(xa, xsa, b);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b + 1 < b1)
+        load_tile_words(next, a, ct0, b + 1, nb, lane, col);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(cur, xa, xsa);
+      cur = next;
+    }
   }
 
   // Cross-wave reduction through LDS in [wave][matrix][tile][row][column]
@@ -511,25 +616,51 @@ __global__ __launch_bounds__(64) void relayout_kernel(const uint8_t* __restrict_
   }
 }
 
-template <int RT, int T, int W, bool GATED>
+int env_int(const char* name, int fallback) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : fallback;
+}
+
+template <int RT, int T, int W, int BPW, bool GATED>
 hipError_t gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
   const dim3 grid((unsigned)(a.n / (16 * T))), block(64 * W);
   if (dtype == kF32)
-    q4k_gemv_kernel<RT, T, W, GATED, float><<<grid, block, 0, s>>>(a);
+    q4k_gemv_kernel<RT, T, W, BPW, GATED, float><<<grid, block, 0, s>>>(a);
   else
-    q4k_gemv_kernel<RT, T, W, GATED, _Float16><<<grid, block, 0, s>>>(a);
+    q4k_gemv_kernel<RT, T, W, BPW, GATED, _Float16><<<grid, block, 0, s>>>(a);
   return hipGetLastError();
 }
 
-template <int RT, int T, bool GATED>
-hipError_t gemv_by_waves(hipStream_t s, const GemvArgs& a, int dtype, int waves) {
-  if constexpr (RT == 1) {
-    if (waves == 16)
-      return gemv_launch<RT, T, 16, GATED>(s, a, dtype);
+// One row tile: the block count per wave is fixed at compile time when the
+// waves split nb evenly into at most 4 blocks each.
+template <int T, bool GATED>
+hipError_t gemv_one_row_tile(hipStream_t s, const GemvArgs& a, int dtype, int waves) {
+  static const bool generic = env_int("Q4K_GEMV_GENERIC", 0) != 0;
+  const int bpw = !generic && a.nb % waves == 0 ? a.nb / waves : 0;
+  if (waves == 16) {
+    if (bpw == 1)
+      return gemv_launch<1, T, 16, 1, GATED>(s, a, dtype);
+    if constexpr (T == 1 && !GATED) {  // the other BPW=3 instances spill
+      if (bpw == 3)
+        return gemv_launch<1, T, 16, 3, GATED>(s, a, dtype);
+    }
+    return gemv_launch<1, T, 16, 0, GATED>(s, a, dtype);
   }
+  if (waves == 8) {
+    if (bpw == 2)
+      return gemv_launch<1, T, 8, 2, GATED>(s, a, dtype);
+    return gemv_launch<1, T, 8, 0, GATED>(s, a, dtype);
+  }
+  if (bpw == 4)
+    return gemv_launch<1, T, 4, 4, GATED>(s, a, dtype);
+  return gemv_launch<1, T, 4, 0, GATED>(s, a, dtype);
+}
+
+template <int RT, bool GATED>
+hipError_t gemv_multi_row_tile(hipStream_t s, const GemvArgs& a, int dtype, int waves) {
   if (waves >= 8)
-    return gemv_launch<RT, T, 8, GATED>(s, a, dtype);
-  return gemv_launch<RT, T, 4, GATED>(s, a, dtype);
+    return gemv_launch<RT, 1, 8, 0, GATED>(s, a, dtype);
+  return gemv_launch<RT, 1, 4, 0, GATED>(s, a, dtype);
 }
 
 // Instances kept within the register file (no spills): 16 waves only with
@@ -539,40 +670,35 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const Gemv
   if (shape.row_tiles == 1) {
     if constexpr (!GATED) {
       if (shape.tiles == 2)
-        return gemv_by_waves<1, 2, false>(s, a, dtype, shape.waves);
+        return gemv_one_row_tile<2, false>(s, a, dtype, shape.waves);
     }
-    return gemv_by_waves<1, 1, GATED>(s, a, dtype, shape.waves);
+    return gemv_one_row_tile<1, GATED>(s, a, dtype, shape.waves);
   }
   if (shape.row_tiles == 2)
-    return gemv_by_waves<2, 1, GATED>(s, a, dtype, shape.waves);
-  return gemv_by_waves<3, 1, GATED>(s, a, dtype, shape.waves);
-}
-
-int env_int(const char* name, int fallback) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : fallback;
+    return gemv_multi_row_tile<2, GATED>(s, a, dtype, shape.waves);
+  return gemv_multi_row_tile<3, GATED>(s, a, dtype, shape.waves);
 }
 
 }  // namespace
 
 template <typename InT>
-hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, float* rowscale, int m, int k, int mode) {
+hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode) {
   const dim3 grid((unsigned)m), block(256);
   if (mode == kStageRowMajor)
-    stage_x_kernel<InT, kStageRowMajor><<<grid, block, 0, s>>>(x, xo, rowscale, m, k);
+    stage_x_kernel<InT, kStageRowMajor><<<grid, block, 0, s>>>(x, xo, xs, rowscale, m, k);
   else if (mode == kStageFrag)
-    stage_x_kernel<InT, kStageFrag><<<grid, block, 0, s>>>(x, xo, rowscale, m, k);
+    stage_x_kernel<InT, kStageFrag><<<grid, block, 0, s>>>(x, xo, xs, rowscale, m, k);
   else
-    stage_x_kernel<InT, kStageFragSplit><<<grid, block, 0, s>>>(x, xo, rowscale, m, k);
+    stage_x_kernel<InT, kStageFragSplit><<<grid, block, 0, s>>>(x, xo, xs, rowscale, m, k);
   return hipGetLastError();
 }
 
-hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, float* rowscale, int m, int k, int mode) {
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode) {
   if (m <= 0)
     return hipSuccess;
   if (dtype == kF32)
-    return stage_launch(s, static_cast<const float*>(x), xo, rowscale, m, k, mode);
-  return stage_launch(s, static_cast<const _Float16*>(x), xo, rowscale, m, k, mode);
+    return stage_launch(s, static_cast<const float*>(x), xo, xs, rowscale, m, k, mode);
+  return stage_launch(s, static_cast<const _Float16*>(x), xo, xs, rowscale, m, k, mode);
 }
 
 GemvShape gemv_shape(int rows, int n, int nb, bool gated) {
