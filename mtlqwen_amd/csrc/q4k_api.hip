@@ -254,6 +254,19 @@ bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
   return a0 < b0 + bbytes && b0 < a0 + abytes;
 }
 
+// Compute units of each device (persistent-grid sizing), cached.
+int device_cus(int device) {
+  static int cus[64] = {0};
+  int& c = cus[device & 63];
+  if (c == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || v <= 0)
+      v = 256;
+    c = v;
+  }
+  return c;
+}
+
 int set_device(int device) {
   int cur = -1;
   Q4K_TRY_HIP(hipGetDevice(&cur), "hipGetDevice");
@@ -302,7 +315,10 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
     a.rows = rows;
     a.split = split ? 1 : 0;
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr), wu != nullptr), "gemv launch");
+    if (gemv_stream_supported(rows, a.nb, a.n, wu != nullptr))
+      Q4K_TRY_HIP(launch_gemv_stream(stream, a, (int)dtype, wu != nullptr, device_cus(w->device)), "gemv stream launch");
+    else
+      Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr), wu != nullptr), "gemv launch");
   } else {
     GemmArgs a;
     a.w = w->data;

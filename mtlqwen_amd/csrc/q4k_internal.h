@@ -98,6 +98,11 @@ struct GemvShape {
 // column tiles and waves per workgroup, for tuning.
 GemvShape gemv_shape(int rows, int n, int nb, bool gated);
 
+// Streaming GEMV (LDS ring, persistent workgroups) for one row tile and the
+// block counts it is instantiated for; `cus` = compute units of the device.
+bool gemv_stream_supported(int rows, int nb, int n, bool gated);
+hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus);
+
 // GEMV for m <= 48.
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated);
 

@@ -460,6 +460,183 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// Streaming GEMV (one 16-row activation tile, nb == W * BPW).
+//
+// Persistent workgroups (at most one per CU) loop over items of T column
+// tiles.  Wave w owns blocks [w*BPW, (w+1)*BPW) of every item, so its
+// activation fragments are loaded once and stay in registers.  Its weight
+// tile-blocks ("units": block j, matrix mi, tile t) stream through a private
+// LDS ring of D+1 slots with global_load_lds_dwordx4 (16 bytes per lane, lane
+// order = slab order), D units ahead of the one being computed, so about
+// D * 2.3 KB per wave is always in flight without holding VGPRs.  Every
+// iteration issues exactly three loads (units past the end re-load the last
+// unit, an L2 hit), so a constant vmcnt(3*D) marks the current unit complete.
+// ----------------------------------------------------------------------------
+// LDS-DMA loads are issued as asm: the compiler would otherwise guard every
+// later LDS read with vmcnt(0) (it cannot tell the ring slots apart).  Their
+// completion is covered by the explicit vmcnt waits below; nothing else in
+// the streaming loop issues vector-memory loads.  No memory clobber: one
+// makes the compiler treat the asm as an outstanding store and wait vmcnt(0)
+// before every later LDS read; ordering against the LDS reads comes from the
+// scheduling barrier in issue() and the clobbering wait.  M0 is written here;
+// nothing else in this kernel uses it.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform by construction
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "m0");
+}
+
+__device__ __forceinline__ void lds_load4(const void* g, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "m0");
+}
+
+template <int T, int NM, int W, int BPW, int D, typename OutT>
+__global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int items) {
+  constexpr int U = BPW * NM * T;  // units per item per wave
+  constexpr int R = D + 1;         // ring slots per wave
+  __shared__ __attribute__((aligned(16))) uint8_t ring[W][R][kTileBlockBytes];
+  __shared__ float red[W][NM][T][16][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  const int nb = a.nb, bw = wave * BPW;
+  const int first = blockIdx.x, stride = gridDim.x;
+  const int n_items = first < items ? (items - 1 - first) / stride + 1 : 0;
+  const int S = n_items * U;
+  if (S == 0)
+    return;
+
+  // Resident activations of this wave's blocks (dead rows of the 16-row
+  // tile are loaded unmasked; they only reach unread C rows), and the row
+  // scale of the row this thread finishes in every epilogue.
+  h8_t xa[BPW][8];
+  h4_t xsa[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    const h8_t* xp = reinterpret_cast<const h8_t*>(a.xf) + (size_t)(bw + j) * 8 * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      xa[j][s] = xp[s * 64];
+    xsa[j] = reinterpret_cast<const h4_t*>(a.xs)[(size_t)(bw + j) * 32 + (lane & 31)];
+  }
+  const int erow = tid / (16 * T);
+  const float escale = erow < a.m ? a.rowscale[erow] : 0.0f;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  auto issue = [&](int s) {
+    // The DMA overwrites the slot of the unit computed just before: keep the
+    // scheduler from moving that unit's LDS reads below this point.
+    __builtin_amdgcn_sched_barrier(0);
+    const int sc = s < S ? s : S - 1;
+    const int it = sc / U, q = sc - it * U;
+    const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
+    const int ct = (first + it * stride) * T + t;
+    const uint8_t* p = (mi ? a.wu : a.w) + ((size_t)ct * nb + bw + j) * kTileBlockBytes;
+    const uint32_t slot = lds_addr(&ring[wave][s % R][0]);
+    lds_load16(p + 16 * lane, slot);
+    lds_load16(p + kSlabBytes + 16 * lane, slot + kSlabBytes);
+    lds_load4(p + kHeaderOffset + 4 * lane, slot + kHeaderOffset);
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s)
+    issue(s);
+
+  f4_t acc[NM][T];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      acc[mi][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  for (int it = 0; it < n_items; ++it) {
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int s = it * U + q;
+      issue(s + D);
+      // Three loads per iteration: vmcnt(3*D) leaves exactly the D newer units
+      // outstanding.  The memory clobber keeps the LDS reads below the wait.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * D) : "memory");
+      const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
+      const u4_t* slot = reinterpret_cast<const u4_t*>(&ring[wave][s % R][0]);
+      const u4_t q0 = slot[lane];
+      const u4_t q1 = slot[kSlabBytes / 16 + lane];
+      const u4_t hd = slot[kHeaderOffset / 16 + col];
+      const BlockConsts kc = block_consts(hd, g);
+      f4_t cq = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u4_t qq = u < 2 ? q0 : q1;
+        const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
+        const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+        const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+        cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], blo, cq, 0, 0, 0);
+        cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][4 + u], bhi, cq, 0, 0, 0);
+      }
+      const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[j], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[mi][t][v] = fmaf(kc.d, cq[v], fmaf(-kc.dmin, cm[v], acc[mi][t][v]));
+    }
+
+    // Item complete: reduce the W partial sums and run the epilogue.
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          red[wave][mi][t][4 * g + v][col] = acc[mi][t][v];
+        acc[mi][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    __syncthreads();
+    const int ct0 = (first + it * stride) * T;
+    // One output per thread: m * 16T <= 16 * 32 < 64 * W.
+    for (int o = tid; o < a.m * 16 * T; o += 64 * W) {
+      const int row = o / (16 * T), c = o % (16 * T), t = c >> 4, cc = c & 15;
+      float sm[NM];
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          v += red[w][mi][t][row][cc];
+        if (a.split) {
+#pragma unroll
+          for (int w = 0; w < W; ++w)
+            v += red[w][mi][t][a.m + row][cc];
+        }
+        sm[mi] = v;
+      }
+      const float scale = escale;  // row == erow: o < 64 * W covers all outputs
+      const size_t off = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
+      float out;
+      if (NM == 2) {
+        float gv = sm[0] * scale, uv = sm[NM - 1] * scale;
+        if (sizeof(OutT) == 2) {
+          gv = round_half(gv);
+          uv = round_half(uv);
+        }
+        out = silu(gv) * uv;
+      } else {
+        float acc_v = sm[0] * scale;
+        if (sizeof(OutT) == 2)
+          acc_v = round_half(acc_v);
+        out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+      }
+      store_elem(y, off, out);
+    }
+    __syncthreads();
+  }
+  // Drain the trailing (re-load) units before the ring is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// ----------------------------------------------------------------------------
 // GEMM (prefill).  Workgroup tile 128 x 128, 4 waves of 64 x 64, k-step 64
 // (one quarter of a Q4_K block).  Per k-step: the 128x64 fp16 activation tile
 // is copied to LDS; 256 threads dequantise the 128x64 weight tile to
@@ -679,7 +856,34 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const Gemv
   return gemv_multi_row_tile<3, GATED>(s, a, dtype, shape.waves);
 }
 
+template <int T, int NM, int W, int BPW, int D>
+hipError_t stream_launch(hipStream_t s, const GemvArgs& a, int dtype, int grid, int items) {
+  if (dtype == kF32)
+    q4k_gemv_stream_kernel<T, NM, W, BPW, D, float><<<dim3((unsigned)grid), dim3(64 * W), 0, s>>>(a, items);
+  else
+    q4k_gemv_stream_kernel<T, NM, W, BPW, D, _Float16><<<dim3((unsigned)grid), dim3(64 * W), 0, s>>>(a, items);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+bool gemv_stream_supported(int rows, int nb, int n, bool gated) {
+  (void)gated;
+  static const bool enabled = env_int("Q4K_GEMV_STREAM", 1) != 0;
+  return enabled && rows <= 16 && nb == 16 && n % 16 == 0;
+}
+
+hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus) {
+  // One row tile, K = 4096 (nb = 16): 8 waves x 2 blocks, 6 units ahead.
+  const int tiles = (!gated && a.n % 32 == 0 && a.n / 32 >= 4 * cus) ? 2 : 1;
+  const int items = a.n / (16 * tiles);
+  const int grid = items < cus ? items : cus;
+  if (gated)
+    return stream_launch<1, 2, 8, 2, 6>(s, a, dtype, grid, items);
+  if (tiles == 2)
+    return stream_launch<2, 1, 8, 2, 6>(s, a, dtype, grid, items);
+  return stream_launch<1, 1, 8, 2, 6>(s, a, dtype, grid, items);
+}
 
 template <typename InT>
 hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode) {
