@@ -474,44 +474,70 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 // ----------------------------------------------------------------------------
 // LDS-DMA loads are issued as asm: the compiler would otherwise guard every
 // later LDS read with vmcnt(0) (it cannot tell the ring slots apart).  Their
-// completion is covered by the explicit vmcnt waits below; nothing else in
-// the streaming loop issues vector-memory loads.  No memory clobber: one
-// makes the compiler treat the asm as an outstanding store and wait vmcnt(0)
-// before every later LDS read; ordering against the LDS reads comes from the
-// scheduling barrier in issue() and the clobbering wait.  M0 is written here;
-// nothing else in this kernel uses it.
+// completion is covered by the explicit vmcnt waits below.  No memory
+// clobber: one makes the compiler treat the asm as an outstanding store and
+// wait vmcnt(0) before every later LDS read; ordering against the LDS reads
+// comes from the scheduling barrier in issue() and the clobbering wait.  The
+// address is a wave-uniform SGPR base plus a fixed per-lane VGPR offset, so
+// issuing costs no vector ALU work.  M0 is written here; nothing else in this
+// kernel uses it.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-__device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
-  lds = __builtin_amdgcn_readfirstlane(lds);  // wave-uniform by construction
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "m0");
+template <int OFFSET>
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "s"(lds), "n"(OFFSET) : "m0");
 }
 
-__device__ __forceinline__ void lds_load4(const void* g, uint32_t lds) {
-  lds = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "m0");
+template <int OFFSET>
+__device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "s"(lds), "n"(OFFSET) : "m0");
 }
 
 template <int T, int NM, int W, int BPW, int D, typename OutT>
 __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int items) {
   constexpr int U = BPW * NM * T;  // units per item per wave
   constexpr int R = D + 1;         // ring slots per wave
+  constexpr int AHEAD = (D + U - 1) / U;  // items the issue pointer runs ahead
   __shared__ __attribute__((aligned(16))) uint8_t ring[W][R][kTileBlockBytes];
   __shared__ float red[W][NM][T][16][16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
   const int nb = a.nb, bw = wave * BPW;
   const int first = blockIdx.x, stride = gridDim.x;
   const int n_items = first < items ? (items - 1 - first) / stride + 1 : 0;
-  const int S = n_items * U;
-  if (S == 0)
+  if (n_items == 0)
     return;
+  const uint32_t ring0 = lds_addr(&ring[wave][0][0]);
+  const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
+  const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
 
-  // Resident activations of this wave's blocks (dead rows of the 16-row
-  // tile are loaded unmasked; they only reach unread C rows), and the row
-  // scale of the row this thread finishes in every epilogue.
+  // Base of item it's first unit for matrix mi (items past the end clamp to
+  // the last item: their loads are re-reads that only keep the count fixed).
+  auto item_base = [&](int it, int mi) -> const uint8_t* {
+    const int itc = it < n_items ? it : n_items - 1;
+    const int ct = (first + itc * stride) * T;
+    return (mi ? a.wu : a.w) + (size_t)ct * tile_bytes + (size_t)bw * kTileBlockBytes;
+  };
+  // Issue unit q of item it into ring slot `slot`.
+  auto issue = [&](int it, int q, int slot) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
+    const uint8_t* p = item_base(it, mi) + (size_t)t * tile_bytes + (size_t)j * kTileBlockBytes;
+    const uint32_t l = ring0 + (uint32_t)slot * kTileBlockBytes;
+    lds_dma16<0>(p, voff16, l);
+    lds_dma16<kSlabBytes>(p, voff16, l + kSlabBytes);
+    lds_dma4<kHeaderOffset>(p, voff4, l + kHeaderOffset);
+  };
+
+  // Prologue: the first D units, then this wave's resident activations (so
+  // both first-touch latencies overlap), and the row scale of the row this
+  // thread finishes in every epilogue.
+#pragma unroll
+  for (int s = 0; s < D; ++s)
+    issue(s / U, s % U, s);
   h8_t xa[BPW][8];
   h4_t xsa[BPW];
 #pragma unroll
@@ -524,25 +550,6 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
   }
   const int erow = tid / (16 * T);
   const float escale = erow < a.m ? a.rowscale[erow] : 0.0f;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  auto issue = [&](int s) {
-    // The DMA overwrites the slot of the unit computed just before: keep the
-    // scheduler from moving that unit's LDS reads below this point.
-    __builtin_amdgcn_sched_barrier(0);
-    const int sc = s < S ? s : S - 1;
-    const int it = sc / U, q = sc - it * U;
-    const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
-    const int ct = (first + it * stride) * T + t;
-    const uint8_t* p = (mi ? a.wu : a.w) + ((size_t)ct * nb + bw + j) * kTileBlockBytes;
-    const uint32_t slot = lds_addr(&ring[wave][s % R][0]);
-    lds_load16(p + 16 * lane, slot);
-    lds_load16(p + kSlabBytes + 16 * lane, slot + kSlabBytes);
-    lds_load4(p + kHeaderOffset + 4 * lane, slot + kHeaderOffset);
-  };
-#pragma unroll
-  for (int s = 0; s < D; ++s)
-    issue(s);
 
   f4_t acc[NM][T];
 #pragma unroll
@@ -553,19 +560,24 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
 
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  int slot = 0;  // ring slot of the unit being computed
   for (int it = 0; it < n_items; ++it) {
 #pragma unroll
     for (int q = 0; q < U; ++q) {
-      const int s = it * U + q;
-      issue(s + D);
-      // Three loads per iteration: vmcnt(3*D) leaves exactly the D newer units
+      // Unit D ahead: item it + (q + D) / U, unit (q + D) % U, slot slot - 1.
+      const int islot = slot == 0 ? R - 1 : slot - 1;
+      issue(it + (q + D) / U, (q + D) % U, islot);
+      // Three loads per unit: vmcnt(3*D) leaves exactly the D newer units
       // outstanding.  The memory clobber keeps the LDS reads below the wait.
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * D) : "memory");
+      constexpr int dummy = AHEAD;
+      (void)dummy;
       const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
-      const u4_t* slot = reinterpret_cast<const u4_t*>(&ring[wave][s % R][0]);
-      const u4_t q0 = slot[lane];
-      const u4_t q1 = slot[kSlabBytes / 16 + lane];
-      const u4_t hd = slot[kHeaderOffset / 16 + col];
+      const u4_t* sl = reinterpret_cast<const u4_t*>(&ring[wave][slot][0]);
+      const u4_t q0 = sl[lane];
+      const u4_t q1 = sl[kSlabBytes / 16 + lane];
+      const u4_t hd = sl[kHeaderOffset / 16 + col];
+      slot = slot == R - 1 ? 0 : slot + 1;
       const BlockConsts kc = block_consts(hd, g);
       f4_t cq = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -595,9 +607,9 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
       }
     __syncthreads();
     const int ct0 = (first + it * stride) * T;
-    // One output per thread: m * 16T <= 16 * 32 < 64 * W.
-    for (int o = tid; o < a.m * 16 * T; o += 64 * W) {
-      const int row = o / (16 * T), c = o % (16 * T), t = c >> 4, cc = c & 15;
+    // One output per thread: m * 16T <= 16 * 32 <= 64 * W.
+    if (tid < a.m * 16 * T) {
+      const int row = erow, c = tid % (16 * T), t = c >> 4, cc = c & 15;
       float sm[NM];
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
@@ -612,18 +624,17 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
         }
         sm[mi] = v;
       }
-      const float scale = escale;  // row == erow: o < 64 * W covers all outputs
       const size_t off = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
       float out;
       if (NM == 2) {
-        float gv = sm[0] * scale, uv = sm[NM - 1] * scale;
+        float gv = sm[0] * escale, uv = sm[NM - 1] * escale;
         if (sizeof(OutT) == 2) {
           gv = round_half(gv);
           uv = round_half(uv);
         }
         out = silu(gv) * uv;
       } else {
-        float acc_v = sm[0] * scale;
+        float acc_v = sm[0] * escale;
         if (sizeof(OutT) == 2)
           acc_v = round_half(acc_v);
         out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
@@ -874,10 +885,28 @@ bool gemv_stream_supported(int rows, int nb, int n, bool gated) {
 }
 
 hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus) {
-  // One row tile, K = 4096 (nb = 16): 8 waves x 2 blocks, 6 units ahead.
+  // One row tile, K = 4096 (nb = 16): 8 waves x 2 blocks.  Ring depth D: 6
+  // units ahead (one workgroup per CU) or 2 (two per CU); Q4K_GEMV_DEPTH
+  // overrides for tuning.
+  static const int depth = env_int("Q4K_GEMV_DEPTH", 6);
   const int tiles = (!gated && a.n % 32 == 0 && a.n / 32 >= 4 * cus) ? 2 : 1;
   const int items = a.n / (16 * tiles);
-  const int grid = items < cus ? items : cus;
+  const int per_cu = depth <= 2 ? 2 : 1;
+  const int grid = items < per_cu * cus ? items : per_cu * cus;
+  if (depth <= 2) {
+    if (gated)
+      return stream_launch<1, 2, 8, 2, 2>(s, a, dtype, grid, items);
+    if (tiles == 2)
+      return stream_launch<2, 1, 8, 2, 2>(s, a, dtype, grid, items);
+    return stream_launch<1, 1, 8, 2, 2>(s, a, dtype, grid, items);
+  }
+  if (depth <= 4) {
+    if (gated)
+      return stream_launch<1, 2, 8, 2, 4>(s, a, dtype, grid, items);
+    if (tiles == 2)
+      return stream_launch<2, 1, 8, 2, 4>(s, a, dtype, grid, items);
+    return stream_launch<1, 1, 8, 2, 4>(s, a, dtype, grid, items);
+  }
   if (gated)
     return stream_launch<1, 2, 8, 2, 6>(s, a, dtype, grid, items);
   if (tiles == 2)
