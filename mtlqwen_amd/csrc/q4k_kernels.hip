@@ -526,10 +526,11 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
     __builtin_amdgcn_sched_barrier(0);
     const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
     const uint8_t* p = item_base(it, mi) + (size_t)t * tile_bytes + (size_t)j * kTileBlockBytes;
+    // The immediate offset applies to both addresses: LDS = M0 + offset + lane * size.
     const uint32_t l = ring0 + (uint32_t)slot * kTileBlockBytes;
     lds_dma16<0>(p, voff16, l);
-    lds_dma16<kSlabBytes>(p, voff16, l + kSlabBytes);
-    lds_dma4<kHeaderOffset>(p, voff4, l + kHeaderOffset);
+    lds_dma16<kSlabBytes>(p, voff16, l);
+    lds_dma4<kHeaderOffset>(p, voff4, l);
   };
 
   // Prologue: the first D units, then this wave's resident activations (so
