@@ -124,8 +124,10 @@ __device__ __forceinline__ BlockConsts block_consts(u4_t hd, int g) {
   k.dmin = half_bits_to_float(hd.x >> 16);
   const uint32_t sh = 16u * (uint32_t)(g & 1);
   const uint32_t a = hd.y >> sh, c = hd.w >> sh;
-  // bytes 0, 1 = sc_{2g}, sc_{2g+1}
-  const uint32_t scp = g < 2 ? (a & 0x3F3Fu) : ((c & 0x0F0Fu) | ((a >> 2) & 0x3030u));
+  // bytes 0, 1 = sc_{2g}, sc_{2g+1} (both forms computed, then selected:
+  // lanes of one wave take both sides of the g < 2 split)
+  const uint32_t sc_direct = a & 0x3F3Fu, sc_packed = (c & 0x0F0Fu) | ((a >> 2) & 0x3030u);
+  const uint32_t scp = g < 2 ? sc_direct : sc_packed;
   const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
   const h2_t kneg1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
   // perm(0x64646464, v, sel) interleaves bytes of v with 0x64: fp16 1024 + byte.
@@ -135,8 +137,8 @@ __device__ __forceinline__ BlockConsts block_consts(u4_t hd, int g) {
   k.mul_hi = __builtin_elementwise_fma(p_hi, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-64.0f, (_Float16)-64.0f});
   k.add_hi = k.mul_hi * kneg1024;
   // bytes 0..3 = m_{4g}..m_{4g+3} for g < 2; zero for g >= 2 (k = 8..15 unused)
-  const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-  const uint32_t mb = g == 0 ? (hd.z & 0x3F3F3F3Fu) : g == 1 ? m47 : 0u;
+  const uint32_t m03 = hd.z & 0x3F3F3F3Fu, m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+  const uint32_t mb = g >= 2 ? 0u : (g == 0 ? m03 : m47);
   const h2_t k32 = {(_Float16)32.0f, (_Float16)32.0f}, kneg32768 = {(_Float16)-32768.0f, (_Float16)-32768.0f};
   const h2_t m01 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04010400u)), k32, kneg32768);
   const h2_t m23 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04030402u)), k32, kneg32768);
@@ -485,6 +487,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// Wave-uniform values the compiler cannot prove uniform are moved to SGPRs.
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 template <int OFFSET>
 __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "s"(lds), "n"(OFFSET) : "m0");
@@ -495,13 +505,42 @@ __device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, uint3
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "s"(lds), "n"(OFFSET) : "m0");
 }
 
+// Register loads issued as asm for the same reason: a compiler-visible load
+// makes its first use wait vmcnt(0), draining the ring.  Their results are
+// released to the compiler by hold() after an explicit wait.
+__device__ __forceinline__ u4_t asm_load16(const void* p) {
+  u4_t r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+
+__device__ __forceinline__ h4_t asm_load8(const void* p) {
+  h4_t r;
+  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+
+__device__ __forceinline__ float asm_load4(const void* p) {
+  float r;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+
+template <typename V>
+__device__ __forceinline__ void hold(V& v) {
+  asm volatile("" : "+v"(v));
+}
+
 template <int T, int NM, int W, int BPW, int D, typename OutT>
 __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int items) {
-  constexpr int U = BPW * NM * T;  // units per item per wave
+  constexpr int MT = NM * T;       // (matrix, tile) pairs of an item
+  constexpr int U = BPW * MT;      // units per item per wave, order (j, mi, t)
   constexpr int R = D + 1;         // ring slots per wave
-  constexpr int AHEAD = (D + U - 1) / U;  // items the issue pointer runs ahead
   __shared__ __attribute__((aligned(16))) uint8_t ring[W][R][kTileBlockBytes];
-  __shared__ float red[W][NM][T][16][16];
+  // Per-wave partial sums of the current item, [wave][mi*T+t][row][col]: each
+  // wave accumulates its own slot in program order (deterministic), and the
+  // epilogue sums the W slots in wave order.
+  __shared__ float red[W][MT][16][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
@@ -514,133 +553,141 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
   const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
   const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
 
-  // Base of item it's first unit for matrix mi (items past the end clamp to
-  // the last item: their loads are re-reads that only keep the count fixed).
-  auto item_base = [&](int it, int mi) -> const uint8_t* {
-    const int itc = it < n_items ? it : n_items - 1;
-    const int ct = (first + itc * stride) * T;
-    return (mi ? a.wu : a.w) + (size_t)ct * tile_bytes + (size_t)bw * kTileBlockBytes;
-  };
-  // Issue unit q of item it into ring slot `slot`.
-  auto issue = [&](int it, int q, int slot) {
+  // Issue unit s of this wave's stream into ring slot `slot`; units past the
+  // end re-load the last unit (an L2 hit) so every iteration issues exactly
+  // three loads.
+  auto issue = [&](int s, int slot) {
     __builtin_amdgcn_sched_barrier(0);
-    const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
-    const uint8_t* p = item_base(it, mi) + (size_t)t * tile_bytes + (size_t)j * kTileBlockBytes;
+    int it = s / U;
+    int q = s - it * U;
+    if (it >= n_items) {
+      it = n_items - 1;
+      q = U - 1;
+    }
+    const int j = q / MT, mt = q - j * MT, mi = mt / T, t = mt - mi * T;
+    const int ct = (first + it * stride) * T + t;
+    const uint8_t* p = uniform_ptr((mi ? a.wu : a.w) + (size_t)ct * tile_bytes + (size_t)(bw + j) * kTileBlockBytes);
     // The immediate offset applies to both addresses: LDS = M0 + offset + lane * size.
-    const uint32_t l = ring0 + (uint32_t)slot * kTileBlockBytes;
+    const uint32_t l = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)slot * kTileBlockBytes);
     lds_dma16<0>(p, voff16, l);
     lds_dma16<kSlabBytes>(p, voff16, l);
     lds_dma4<kHeaderOffset>(p, voff4, l);
   };
 
-  // Prologue: the first D units, then this wave's resident activations (so
-  // both first-touch latencies overlap), and the row scale of the row this
-  // thread finishes in every epilogue.
-#pragma unroll
-  for (int s = 0; s < D; ++s)
-    issue(s / U, s % U, s);
-  h8_t xa[BPW][8];
+  // Resident activations of this wave's blocks (dead rows of the 16-row tile
+  // are loaded unmasked; they only reach unread C rows) and the scales of the
+  // rows this thread finishes in the epilogues (clamped: always issued), then
+  // the first D units.  One wait covers the activations and unit 0.
+  u4_t xw[BPW][8];
   h4_t xsa[BPW];
 #pragma unroll
   for (int j = 0; j < BPW; ++j) {
-    const h8_t* xp = reinterpret_cast<const h8_t*>(a.xf) + (size_t)(bw + j) * 8 * 64 + lane;
+    const u4_t* xp = reinterpret_cast<const u4_t*>(a.xf) + (size_t)(bw + j) * 8 * 64 + lane;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
-      xa[j][s] = xp[s * 64];
-    xsa[j] = reinterpret_cast<const h4_t*>(a.xs)[(size_t)(bw + j) * 32 + (lane & 31)];
+      xw[j][s] = asm_load16(xp + s * 64);
+    xsa[j] = asm_load8(reinterpret_cast<const h4_t*>(a.xs) + (size_t)(bw + j) * 32 + (lane & 31));
   }
-  const int erow = tid / (16 * T);
-  const float escale = erow < a.m ? a.rowscale[erow] : 0.0f;
-
-  f4_t acc[NM][T];
+  constexpr int EPI = 16 * T;  // outputs per row of an item
+  const int r0 = tid / EPI, r1 = (tid + 64 * W) / EPI;
+  float sc0 = asm_load4(a.rowscale + (r0 < a.m ? r0 : a.m - 1));
+  float sc1 = asm_load4(a.rowscale + (r1 < a.m ? r1 : a.m - 1));
 #pragma unroll
-  for (int mi = 0; mi < NM; ++mi)
+  for (int s = 0; s < D; ++s)
+    issue(s, s);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (D - 1)) : "memory");
+  h8_t xa[BPW][8];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-      acc[mi][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < BPW; ++j) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      hold(xw[j][s]);
+      xa[j][s] = __builtin_bit_cast(h8_t, xw[j][s]);
+    }
+    hold(xsa[j]);
+  }
+  hold(sc0);
+  hold(sc1);
 
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   int slot = 0;  // ring slot of the unit being computed
+  int s = 0;     // stream index of the unit being computed
   for (int it = 0; it < n_items; ++it) {
 #pragma unroll
-    for (int q = 0; q < U; ++q) {
-      // Unit D ahead: item it + (q + D) / U, unit (q + D) % U, slot slot - 1.
-      const int islot = slot == 0 ? R - 1 : slot - 1;
-      issue(it + (q + D) / U, (q + D) % U, islot);
-      // Three loads per unit: vmcnt(3*D) leaves exactly the D newer units
-      // outstanding.  The memory clobber keeps the LDS reads below the wait.
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * D) : "memory");
-      constexpr int dummy = AHEAD;
-      (void)dummy;
-      const int j = q / (NM * T), mi = (q / T) % NM, t = q % T;
-      const u4_t* sl = reinterpret_cast<const u4_t*>(&ring[wave][slot][0]);
-      const u4_t q0 = sl[lane];
-      const u4_t q1 = sl[kSlabBytes / 16 + lane];
-      const u4_t hd = sl[kHeaderOffset / 16 + col];
-      slot = slot == R - 1 ? 0 : slot + 1;
-      const BlockConsts kc = block_consts(hd, g);
-      f4_t cq = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < BPW; ++j) {
+      for (int mt = 0; mt < MT; ++mt, ++s) {
+        issue(s + D, slot == 0 ? R - 1 : slot - 1);
+        // Three loads per unit: vmcnt(3*D) leaves exactly the D newer units
+        // outstanding.  The memory clobber keeps the LDS reads below the wait.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * D) : "memory");
+        const u4_t* sl = reinterpret_cast<const u4_t*>(&ring[wave][slot][0]);
+        const u4_t q0 = sl[lane];
+        const u4_t q1 = sl[kSlabBytes / 16 + lane];
+        const u4_t hd = sl[kHeaderOffset / 16 + col];
+        slot = slot == R - 1 ? 0 : slot + 1;
+        const BlockConsts kc = block_consts(hd, g);
+        // Two accumulation chains (low / high nibbles) keep the MFMA pipe busy.
+        f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const u4_t qq = u < 2 ? q0 : q1;
-        const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
-        const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
-        const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
-        cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], blo, cq, 0, 0, 0);
-        cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][4 + u], bhi, cq, 0, 0, 0);
+        for (int u = 0; u < 4; ++u) {
+          const u4_t qq = u < 2 ? q0 : q1;
+          const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
+          const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+          const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+          cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], blo, cl, 0, 0, 0);
+          ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][4 + u], bhi, ch, 0, 0, 0);
+        }
+        const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[j], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        float* r = &red[wave][mt][4 * g][col];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float part = fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]);
+          r[16 * v] = j == 0 ? part : r[16 * v] + part;
+        }
       }
-      const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[j], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        acc[mi][t][v] = fmaf(kc.d, cq[v], fmaf(-kc.dmin, cm[v], acc[mi][t][v]));
     }
 
-    // Item complete: reduce the W partial sums and run the epilogue.
-#pragma unroll
-    for (int mi = 0; mi < NM; ++mi)
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          red[wave][mi][t][4 * g + v][col] = acc[mi][t][v];
-        acc[mi][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      }
+    // Item complete: sum the W partial slots and run the epilogue.
     __syncthreads();
     const int ct0 = (first + it * stride) * T;
-    // One output per thread: m * 16T <= 16 * 32 <= 64 * W.
-    if (tid < a.m * 16 * T) {
-      const int row = erow, c = tid % (16 * T), t = c >> 4, cc = c & 15;
-      float sm[NM];
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi) {
-        float v = 0.0f;
+    for (int k = 0; k < 2; ++k) {
+      const int o = tid + k * 64 * W;
+      if (o < a.m * EPI) {
+        const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
+        const float escale = k == 0 ? sc0 : sc1;
+        float sm[NM];
 #pragma unroll
-        for (int w = 0; w < W; ++w)
-          v += red[w][mi][t][row][cc];
-        if (a.split) {
+        for (int mi = 0; mi < NM; ++mi) {
+          float v = 0.0f;
 #pragma unroll
           for (int w = 0; w < W; ++w)
-            v += red[w][mi][t][a.m + row][cc];
+            v += red[w][mi * T + t][row][cc];
+          if (a.split) {
+#pragma unroll
+            for (int w = 0; w < W; ++w)
+              v += red[w][mi * T + t][a.m + row][cc];
+          }
+          sm[mi] = v;
         }
-        sm[mi] = v;
-      }
-      const size_t off = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
-      float out;
-      if (NM == 2) {
-        float gv = sm[0] * escale, uv = sm[NM - 1] * escale;
-        if (sizeof(OutT) == 2) {
-          gv = round_half(gv);
-          uv = round_half(uv);
+        const size_t off = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
+        float out;
+        if (NM == 2) {
+          float gv = sm[0] * escale, uv = sm[NM - 1] * escale;
+          if (sizeof(OutT) == 2) {
+            gv = round_half(gv);
+            uv = round_half(uv);
+          }
+          out = silu(gv) * uv;
+        } else {
+          float acc_v = sm[0] * escale;
+          if (sizeof(OutT) == 2)
+            acc_v = round_half(acc_v);
+          out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
         }
-        out = silu(gv) * uv;
-      } else {
-        float acc_v = sm[0] * escale;
-        if (sizeof(OutT) == 2)
-          acc_v = round_half(acc_v);
-        out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+        store_elem(y, off, out);
       }
-      store_elem(y, off, out);
     }
     __syncthreads();
   }
@@ -886,33 +933,28 @@ bool gemv_stream_supported(int rows, int nb, int n, bool gated) {
 }
 
 hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus) {
-  // One row tile, K = 4096 (nb = 16): 8 waves x 2 blocks.  Ring depth D: 6
-  // units ahead (one workgroup per CU) or 2 (two per CU); Q4K_GEMV_DEPTH
-  // overrides for tuning.
-  static const int depth = env_int("Q4K_GEMV_DEPTH", 6);
-  const int tiles = (!gated && a.n % 32 == 0 && a.n / 32 >= 4 * cus) ? 2 : 1;
-  const int items = a.n / (16 * tiles);
-  const int per_cu = depth <= 2 ? 2 : 1;
-  const int grid = items < per_cu * cus ? items : per_cu * cus;
-  if (depth <= 2) {
-    if (gated)
-      return stream_launch<1, 2, 8, 2, 2>(s, a, dtype, grid, items);
-    if (tiles == 2)
-      return stream_launch<2, 1, 8, 2, 2>(s, a, dtype, grid, items);
-    return stream_launch<1, 1, 8, 2, 2>(s, a, dtype, grid, items);
-  }
-  if (depth <= 4) {
-    if (gated)
-      return stream_launch<1, 2, 8, 2, 4>(s, a, dtype, grid, items);
-    if (tiles == 2)
-      return stream_launch<2, 1, 8, 2, 4>(s, a, dtype, grid, items);
-    return stream_launch<1, 1, 8, 2, 4>(s, a, dtype, grid, items);
-  }
+  // One row tile, K = 4096 (nb = 16): 8 waves x 2 blocks, 4 units in flight
+  // per wave.  Items of T column tiles: T = 3 makes N = 12288 exactly one item
+  // per CU; wide outputs take T = 4; otherwise one tile per item.
+  const int ctiles = a.n / 16;
+  int tiles = 1;
+  if (ctiles % 3 == 0 && ctiles / 3 == cus)
+    tiles = 3;
+  else if (!gated && ctiles % 4 == 0 && ctiles / 4 >= 4 * cus)
+    tiles = 4;
+  else if (!gated && ctiles % 2 == 0 && ctiles / 2 >= 2 * cus)
+    tiles = 2;
+  const int items = ctiles / tiles;
+  const int grid = items < cus ? items : cus;
   if (gated)
-    return stream_launch<1, 2, 8, 2, 6>(s, a, dtype, grid, items);
+    return tiles == 3 ? stream_launch<3, 2, 8, 2, 4>(s, a, dtype, grid, items) : stream_launch<1, 2, 8, 2, 4>(s, a, dtype, grid, items);
+  if (tiles == 4)
+    return stream_launch<4, 1, 8, 2, 4>(s, a, dtype, grid, items);
+  if (tiles == 3)
+    return stream_launch<3, 1, 8, 2, 4>(s, a, dtype, grid, items);
   if (tiles == 2)
-    return stream_launch<2, 1, 8, 2, 6>(s, a, dtype, grid, items);
-  return stream_launch<1, 1, 8, 2, 6>(s, a, dtype, grid, items);
+    return stream_launch<2, 1, 8, 2, 4>(s, a, dtype, grid, items);
+  return stream_launch<1, 1, 8, 2, 4>(s, a, dtype, grid, items);
 }
 
 template <typename InT>
