@@ -86,12 +86,14 @@ struct Profiler {
 
 Profiler g_prof;
 
-// Brackets one kernel launch with events when profiling is enabled.
+thread_local DispatchEvents t_dispatch_events;
+
+// Attaches a pair of events to the kernel dispatch made in its scope when
+// profiling is enabled (see dispatch_events()).
 struct LaunchTimer {
   hipEvent_t start = nullptr, stop = nullptr;
-  hipStream_t stream;
   int family;
-  LaunchTimer(hipStream_t s, int fam) : stream(s), family(fam) {
+  LaunchTimer(hipStream_t, int fam) : family(fam) {
     std::lock_guard<std::mutex> lock(g_prof.mu);
     if (!g_prof.on)
       return;
@@ -99,18 +101,22 @@ struct LaunchTimer {
       start = stop = nullptr;
       return;
     }
-    (void)hipEventRecord(start, stream);
+    dispatch_events() = DispatchEvents{start, stop};
   }
   ~LaunchTimer() {
     if (!start)
       return;
-    (void)hipEventRecord(stop, stream);
+    dispatch_events() = DispatchEvents{};
     std::lock_guard<std::mutex> lock(g_prof.mu);
     g_prof.events[family].emplace_back(start, stop);
   }
 };
 
 }  // namespace
+
+DispatchEvents& q4k::dispatch_events() {
+  return t_dispatch_events;
+}
 
 struct q4k_weight {
   int device = 0;

@@ -1,6 +1,7 @@
 // Internal interface between the C-ABI host code (q4k_api.hip) and the
 // kernels (q4k_kernels.hip).  Not installed; the public surface is include/q4k.h.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -112,5 +113,24 @@ hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dty
 
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).
 hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
+
+// ---- dispatch --------------------------------------------------------------
+// Events attached to the calling thread's next kernel dispatches (both null
+// unless launch profiling is on).  hipExtLaunchKernel stamps them with the
+// dispatch's own begin and end times, so the measured duration is the
+// kernel's execution (as a kernel-trace profiler reports it), without the
+// host launch overhead that stream-ordered event records would include.
+struct DispatchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+DispatchEvents& dispatch_events();
+
+template <typename... P, typename... A>
+hipError_t dispatch(void (*kernel)(P...), dim3 grid, dim3 block, hipStream_t s, A... args) {
+  const DispatchEvents& e = dispatch_events();
+  hipExtLaunchKernelGGL(kernel, grid, block, 0, s, e.start, e.stop, 0, static_cast<P>(args)...);
+  return hipGetLastError();
+}
 
 }  // namespace q4k

@@ -861,9 +861,9 @@ template <int RT, int T, int W, int BPW, bool GATED>
 hipError_t gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
   const dim3 grid((unsigned)(a.n / (16 * T))), block(64 * W);
   if (dtype == kF32)
-    q4k_gemv_kernel<RT, T, W, BPW, GATED, float><<<grid, block, 0, s>>>(a);
+    (void)dispatch(q4k_gemv_kernel<RT, T, W, BPW, GATED, float>, grid, block, s, a);
   else
-    q4k_gemv_kernel<RT, T, W, BPW, GATED, _Float16><<<grid, block, 0, s>>>(a);
+    (void)dispatch(q4k_gemv_kernel<RT, T, W, BPW, GATED, _Float16>, grid, block, s, a);
   return hipGetLastError();
 }
 
@@ -918,9 +918,9 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const Gemv
 template <int T, int NM, int W, int BPW, int D>
 hipError_t stream_launch(hipStream_t s, const GemvArgs& a, int dtype, int grid, int items) {
   if (dtype == kF32)
-    q4k_gemv_stream_kernel<T, NM, W, BPW, D, float><<<dim3((unsigned)grid), dim3(64 * W), 0, s>>>(a, items);
+    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, BPW, D, float>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
   else
-    q4k_gemv_stream_kernel<T, NM, W, BPW, D, _Float16><<<dim3((unsigned)grid), dim3(64 * W), 0, s>>>(a, items);
+    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, BPW, D, _Float16>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
   return hipGetLastError();
 }
 
@@ -961,11 +961,11 @@ template <typename InT>
 hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode) {
   const dim3 grid((unsigned)m), block(256);
   if (mode == kStageRowMajor)
-    stage_x_kernel<InT, kStageRowMajor><<<grid, block, 0, s>>>(x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageRowMajor>, grid, block, s, x, xo, xs, rowscale, m, k);
   else if (mode == kStageFrag)
-    stage_x_kernel<InT, kStageFrag><<<grid, block, 0, s>>>(x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageFrag>, grid, block, s, x, xo, xs, rowscale, m, k);
   else
-    stage_x_kernel<InT, kStageFragSplit><<<grid, block, 0, s>>>(x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageFragSplit>, grid, block, s, x, xo, xs, rowscale, m, k);
   return hipGetLastError();
 }
 
@@ -1010,9 +1010,9 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvSh
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype) {
   const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + kBM - 1) / kBM)), block(256);
   if (dtype == kF32)
-    q4k_gemm_kernel<float><<<grid, block, 0, s>>>(a);
+    (void)dispatch(q4k_gemm_kernel<float>, grid, block, s, a);
   else
-    q4k_gemm_kernel<_Float16><<<grid, block, 0, s>>>(a);
+    (void)dispatch(q4k_gemm_kernel<_Float16>, grid, block, s, a);
   return hipGetLastError();
 }
 
@@ -1021,9 +1021,9 @@ hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dty
     return hipSuccess;
   const dim3 grid(idx.rows), block(256);
   if (dtype == kF32)
-    gather_rows_kernel<float><<<grid, block, 0, s>>>(static_cast<const float*>(x), static_cast<float*>(out), k, idx);
+    (void)dispatch(gather_rows_kernel<float>, grid, block, s, static_cast<const float*>(x), static_cast<float*>(out), k, idx);
   else
-    gather_rows_kernel<_Float16><<<grid, block, 0, s>>>(static_cast<const _Float16*>(x), static_cast<_Float16*>(out), k, idx);
+    (void)dispatch(gather_rows_kernel<_Float16>, grid, block, s, static_cast<const _Float16*>(x), static_cast<_Float16*>(out), k, idx);
   return hipGetLastError();
 }
 
@@ -1032,7 +1032,7 @@ hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint
   const size_t tiles = (size_t)(n / 16) * nb;
   if (tiles == 0)
     return hipSuccess;
-  relayout_kernel<<<dim3((unsigned)tiles), dim3(64), 0, s>>>(src, dst, n, nb);
+  (void)dispatch(relayout_kernel, dim3((unsigned)tiles), dim3(64), s, src, dst, n, nb);
   return hipGetLastError();
 }
 
