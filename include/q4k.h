@@ -129,7 +129,9 @@ int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const ui
 
 /* Event timing of every kernel launch (no counterpart in the reference, whose
  * method is paired A/B timing, agents/KERNELS.md:13-21).  While enabled, each
- * launch is bracketed by hipEvents recorded on the launch's stream.
+ * kernel dispatch carries a pair of hipEvents that the runtime stamps with the
+ * dispatch's own begin and end times (hipExtLaunchKernel), so durations
+ * exclude host launch overhead.  Do not enable it during graph capture.
  * q4k_profile_enable(1) clears earlier records; q4k_profile_query
  * synchronises the recorded events and reports launches and summed, minimum
  * and maximum durations in milliseconds for one kernel family. */
