@@ -62,6 +62,12 @@ struct Workspace {
   size_t x_elems = 0;
   float* scale = nullptr;
   size_t scale_elems = 0;
+  float* part = nullptr;  // split-K GEMV slice partials
+  size_t part_elems = 0;
+  int* counters = nullptr;  // split-K GEMV group counters (zero between launches)
+  size_t counter_elems = 0;
+  uint8_t* pack = nullptr;  // decode pack of x (m <= 8)
+  size_t pack_bytes = 0;
   std::vector<void*> retired;
 };
 
@@ -255,6 +261,59 @@ int ensure_workspace(Workspace& ws, int device, size_t halves, size_t rows) {
   return Q4K_OK;
 }
 
+// Split-K buffers.  Counters are zeroed once when allocated; every launch
+// leaves them zero again.
+int ensure_splitk_workspace(Workspace& ws, int device, size_t part_floats, size_t groups) {
+  if (ws.part_elems < part_floats) {
+    if (ws.part)
+      ws.retired.push_back(ws.part);
+    ws.part = nullptr;
+    ws.part_elems = 0;
+    if (hipMalloc(&ws.part, part_floats * sizeof(float)) != hipSuccess)
+      return fail(Q4K_ENOMEM, "cannot allocate %zu-byte split-K workspace on device %d", part_floats * sizeof(float), device);
+    ws.part_elems = part_floats;
+  }
+  if (ws.counter_elems < groups) {
+    const size_t n = groups < 1024 ? 1024 : groups;
+    if (ws.counters)
+      ws.retired.push_back(ws.counters);
+    ws.counters = nullptr;
+    ws.counter_elems = 0;
+    if (hipMalloc(&ws.counters, n * sizeof(int)) != hipSuccess)
+      return fail(Q4K_ENOMEM, "cannot allocate split-K counters on device %d", device);
+    Q4K_TRY_HIP(hipMemset(ws.counters, 0, n * sizeof(int)), "hipMemset");
+    ws.counter_elems = n;
+  }
+  return Q4K_OK;
+}
+
+int ensure_pack_workspace(Workspace& ws, int device, size_t bytes) {
+  if (ws.pack_bytes >= bytes)
+    return Q4K_OK;
+  if (ws.pack)
+    ws.retired.push_back(ws.pack);
+  ws.pack = nullptr;
+  ws.pack_bytes = 0;
+  if (hipMalloc(&ws.pack, bytes) != hipSuccess)
+    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte decode pack on device %d", bytes, device);
+  ws.pack_bytes = bytes;
+  return Q4K_OK;
+}
+
+// Packs x (m <= 8 rows) for the streaming and split-K GEMVs.
+int stage_pack(hipStream_t stream, Workspace& ws, int device, const void* x, uint32_t dtype, uint32_t m, uint32_t k, DecodePack* pk) {
+  const size_t nb = k / 256;
+  int rc = ensure_pack_workspace(ws, device, nb * kPackBytesPerBlock);
+  if (rc)
+    return rc;
+  pk->frag = reinterpret_cast<u4_t*>(ws.pack);
+  pk->xs = reinterpret_cast<h4_t*>(ws.pack + nb * 8 * 64 * 16);
+  pk->dsc = reinterpret_cast<float*>(ws.pack + nb * (8 * 64 * 16 + 64 * 8));
+  LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
+  Q4K_TRY_HIP(launch_stage_pack(stream, x, (int)dtype, *pk, (int)m, (int)k), "stage_pack launch");
+  return Q4K_OK;
+}
+
 bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
   const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
   return a0 < b0 + bbytes && b0 < a0 + abytes;
@@ -292,6 +351,53 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
   const bool gemv = kern.kind != kGemm || m <= 16u * kGemvMaxRowTiles;
   const bool split = gemv && gemv_split((int)m);
   const int rows = split ? 2 * (int)m : (int)m;
+  SplitkPlan plan;
+  if (gemv && gemv_splitk_plan((int)m, (int)w->n, (int)(w->k / 256), wu != nullptr, device_cus(w->device), &plan)) {
+    // Split-K GEMV: decode pack, then partials in the workspace.
+    int rc = ensure_splitk_workspace(ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
+    if (rc)
+      return rc;
+    GemvArgs a{};
+    rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);
+    if (rc)
+      return rc;
+    a.w = w->data;
+    a.wu = wu ? wu->data : w->data;
+    a.x = x;
+    a.y = y;
+    a.aux = aux;
+    a.m = (int)m;
+    a.n = (int)w->n;
+    a.k = (int)w->k;
+    a.nb = (int)(w->k / 256);
+    a.post = (int)post;
+    a.rows = 2 * (int)m;
+    a.split = 1;
+    LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
+    Q4K_TRY_HIP(launch_gemv_splitk(stream, a, (int)dtype, plan, ws.part, ws.counters), "gemv split-K launch");
+    return Q4K_OK;
+  }
+  if (gemv && split && gemv_stream_supported(rows, (int)(w->k / 256), (int)w->n, wu != nullptr, device_cus(w->device))) {
+    GemvArgs a{};
+    int rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);
+    if (rc)
+      return rc;
+    a.w = w->data;
+    a.wu = wu ? wu->data : w->data;
+    a.x = x;
+    a.y = y;
+    a.aux = aux;
+    a.m = (int)m;
+    a.n = (int)w->n;
+    a.k = (int)w->k;
+    a.nb = (int)(w->k / 256);
+    a.post = (int)post;
+    a.rows = rows;
+    a.split = 1;
+    LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
+    Q4K_TRY_HIP(launch_gemv_stream(stream, a, (int)dtype, wu != nullptr, device_cus(w->device)), "gemv stream launch");
+    return Q4K_OK;
+  }
   const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : m;
   // xs is read 32 lanes at a time from its start; +128 halves of slack.
   const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : 0;
@@ -321,10 +427,7 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
     a.rows = rows;
     a.split = split ? 1 : 0;
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    if (gemv_stream_supported(rows, a.nb, a.n, wu != nullptr))
-      Q4K_TRY_HIP(launch_gemv_stream(stream, a, (int)dtype, wu != nullptr, device_cus(w->device)), "gemv stream launch");
-    else
-      Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr), wu != nullptr), "gemv launch");
+    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr), wu != nullptr), "gemv launch");
   } else {
     GemmArgs a;
     a.w = w->data;

@@ -8,6 +8,9 @@
 
 namespace q4k {
 
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
 // ---- device weight layout --------------------------------------------------
 // GGUF stores row n as k/256 consecutive 144-byte block_q4_K records
 // (d fp16 @0, dmin fp16 @2, 12 packed 6-bit scale/min bytes @4, 128 quant
@@ -35,12 +38,23 @@ constexpr int kGemvMaxRowTiles = 3;
 
 enum Dtype : int { kF32 = 0, kF16 = 1 };
 
+// Decode pack: the MFMA operands of x (m <= 8 rows) for the streaming and
+// split-K GEMVs (layout in q4k_kernels.hip, stage_pack_kernel).
+struct DecodePack {
+  u4_t* frag = nullptr;  // [nb][8][64] x 16 B
+  h4_t* xs = nullptr;    // [nb][64] x 8 B
+  float* dsc = nullptr;  // [nb][8]
+};
+constexpr size_t kPackBytesPerBlock = 8 * 64 * 16 + 64 * 8 + 8 * 4;
+
 struct GemvArgs {
   const uint8_t* w;       // tiled weights (gate weights when gated)
   const uint8_t* wu;      // up weights when gated, else unused
   const _Float16* xf;     // staged activations, fragment order
   const _Float16* xs;     // staged sub-block sums / 32, min-term fragment order
   const float* rowscale;  // per-row power-of-two unscale factor
+  const void* x;          // caller's activations [m, k]
+  DecodePack pack;        // packed operands of x (streaming and split-K GEMVs)
   void* y;
   const void* aux;
   int m, n, k, nb, post;
@@ -76,6 +90,7 @@ enum StageMode : int {
 // The fragment modes also write xs: each 32-element sub-block's sum of the
 // scaled values, divided by 32 (so it stays within fp16), hi/lo like x.
 hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode);
+hipError_t launch_stage_pack(hipStream_t s, const void* x, int dtype, const DecodePack& pk, int m, int k);
 
 // Halves of the sub-block-sum fragments for `rows` staged rows: per 16-row
 // tile and block, 32 lanes x 4 halves.
@@ -101,8 +116,19 @@ GemvShape gemv_shape(int rows, int n, int nb, bool gated);
 
 // Streaming GEMV (LDS ring, persistent workgroups) for one row tile and the
 // block counts it is instantiated for; `cus` = compute units of the device.
-bool gemv_stream_supported(int rows, int nb, int n, bool gated);
+bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus);
 hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus);
+
+// Split-K GEMV for m <= 8 (see q4k_gemv_splitk_kernel): a plan picks an
+// instance for (n, nb); the launch needs `part` (gemv_splitk_part_floats
+// floats) and `counters` (plan.groups ints, zero before the first launch;
+// every launch leaves them zero).  Calls sharing the buffers must not overlap.
+struct SplitkPlan {
+  int inst = 0, groups = 0, ks = 0, mt = 0, grid = 0;
+};
+bool gemv_splitk_plan(int m, int n, int nb, bool gated, int cus, SplitkPlan* plan);
+size_t gemv_splitk_part_floats(const SplitkPlan& plan);
+hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const SplitkPlan& plan, float* part, int* counters);
 
 // GEMV for m <= 48.
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated);

@@ -19,11 +19,9 @@ namespace q4k {
 namespace {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef float f16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float silu(float g) {
   return g / (1.0f + expf(-g));
@@ -277,6 +275,75 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
 }
 
 // ----------------------------------------------------------------------------
+// Decode pack (m <= 8): x converted once into the MFMA operands of the
+// streaming and split-K GEMVs, per 256-element block b:
+//   frag[b][s][l]  16 B: A fragment s (v_mfma_f32_16x16x32_f16) of lane l =
+//                  16g + i: elements 64g + 32 (s / 4) + 8 (s % 4) + [0, 8)
+//                  of row i (i < 8: high fp16 parts, i >= 8: low parts of
+//                  row i - 8; zero for rows >= m);
+//   xs[b][l]       8 B: min-term A operand (v_mfma_f32_16x16x16_f16) of lane
+//                  l = 16G + i: sub-block sums / 32 of sub-blocks 4G..4G+3
+//                  (high / low parts as above; zero for G >= 2);
+//   dsc[b][r]      float: unscale factor of row r in block b.
+// Each (row, block) is scaled by a power of two that puts its largest
+// magnitude in [2^14, 2^15); hi + lo carries about 22 significant bits.
+// One 64-thread workgroup per (block, row); lane l holds elements 4l..4l+3.
+// ----------------------------------------------------------------------------
+template <typename InT>
+__global__ __launch_bounds__(64) void stage_pack_kernel(const InT* __restrict__ x, u4_t* __restrict__ frag, h4_t* __restrict__ xs,
+                                                        float* __restrict__ dsc, int m, int k) {
+  const int b = blockIdx.x >> 3, r = blockIdx.x & 7, l = threadIdx.x;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (r < m) {
+    const InT* p = x + (size_t)r * k + (size_t)b * 256 + 4 * l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = (float)p[e];
+  }
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    amax = fmaxf(amax, __shfl_xor(amax, off));
+  float up = 1.0f, down = 1.0f;
+  if (amax > 0.0f && amax <= FLT_MAX) {
+    int ex;
+    frexpf(amax, &ex);
+    ex = ex < -80 ? -80 : ex;
+    up = ldexpf(1.0f, 15 - ex);
+    down = ldexpf(1.0f, ex - 15);
+  }
+  const float t0 = v[0] * up, t1 = v[1] * up, t2 = v[2] * up, t3 = v[3] * up;
+  const h2_t h01 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(t0, t1));
+  const h2_t h23 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(t2, t3));
+  const h2_t l01 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(t0 - (float)h01[0], t1 - (float)h01[1]));
+  const h2_t l23 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(t2 - (float)h23[0], t3 - (float)h23[1]));
+  // Element e = 4l: lane group g = e / 64, fragment s = 4 ((e / 32) & 1) +
+  // (e / 8) & 3, half offset e & 7 (0 or 4).
+  const int e = 4 * l, g = e >> 6, fs = 4 * ((e >> 5) & 1) + ((e >> 3) & 3), h0 = e & 7;
+  uint2* fh = reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(frag + ((size_t)b * 8 + fs) * 64 + 16 * g + r) + h0);
+  uint2* fl = reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(frag + ((size_t)b * 8 + fs) * 64 + 16 * g + r + 8) + h0);
+  *fh = uint2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
+  *fl = uint2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
+  // Sub-block j = l / 8: eight lanes.
+  float sum = (t0 + t1) + (t2 + t3);
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  _Float16* xsh = reinterpret_cast<_Float16*>(xs + (size_t)b * 64);
+  if ((l & 7) == 0) {
+    const int j = l >> 3;
+    const float s32 = sum * 0.03125f;
+    const _Float16 sh = (_Float16)s32;
+    xsh[(16 * (j >> 2) + r) * 4 + (j & 3)] = sh;
+    xsh[(16 * (j >> 2) + r + 8) * 4 + (j & 3)] = (_Float16)(s32 - (float)sh);
+  }
+  if (r == 0 && l < 32)  // lanes 32..63 of the min-term operand
+    xs[(size_t)b * 64 + 32 + l] = h4_t{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+  if (l == 0)
+    dsc[(size_t)b * 8 + r] = down;
+}
+
+// ----------------------------------------------------------------------------
 // GEMV (decode / small prefill / gated decode).
 //
 // Workgroup = W waves over T column tiles (16T output columns); the K blocks
@@ -462,11 +529,15 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// Streaming GEMV (one 16-row activation tile, nb == W * BPW).
+// Streaming GEMV (m <= 8 rows split hi/lo into one 16-row activation tile,
+// nb == W * BPW).
 //
 // Persistent workgroups (at most one per CU) loop over items of T column
-// tiles.  Wave w owns blocks [w*BPW, (w+1)*BPW) of every item, so its
-// activation fragments are loaded once and stay in registers.  Its weight
+// tiles.  Wave w owns blocks [w*BPW, (w+1)*BPW) of every item, so it stages
+// its activation fragments once, from the caller's x, and keeps them in
+// registers (no separate staging launch).  Each wave scales its own K range
+// of a row by a power of two and unscales its partial sums, so no pass over
+// the whole row is needed.  Its weight
 // tile-blocks ("units": block j, matrix mi, tile t) stream through a private
 // LDS ring of D+1 slots with global_load_lds_dwordx4 (16 bytes per lane, lane
 // order = slab order), D units ahead of the one being computed, so about
@@ -514,6 +585,24 @@ __device__ __forceinline__ u4_t asm_load16(const void* p) {
   return r;
 }
 
+// Stores and loads that bypass every cache level (sc0 sc1: system
+// coherence), for data exchanged between workgroups on different XCDs.  The
+// loads return through vmcnt like the others: wait before use.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ float load_coherent(const float* p) {
+  float r;
+  asm volatile("global_load_dword %0, %1, off sc0 sc1" : "=v"(r) : "v"(p));
+  return r;
+}
+
+// Same, into a register that keeps its value in lanes the load skips.
+__device__ __forceinline__ void asm_load16_into(u4_t& r, const void* p) {
+  asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(r) : "v"(p));
+}
+
 __device__ __forceinline__ h4_t asm_load8(const void* p) {
   h4_t r;
   asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
@@ -531,119 +620,155 @@ __device__ __forceinline__ void hold(V& v) {
   asm volatile("" : "+v"(v));
 }
 
-template <int T, int NM, int W, int BPW, int D, typename OutT>
+template <int T, int NM, int W, int DP, typename OutT>
 __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int items) {
-  constexpr int MT = NM * T;       // (matrix, tile) pairs of an item
-  constexpr int U = BPW * MT;      // units per item per wave, order (j, mi, t)
-  constexpr int R = D + 1;         // ring slots per wave
-  __shared__ __attribute__((aligned(16))) uint8_t ring[W][R][kTileBlockBytes];
-  // Per-wave partial sums of the current item, [wave][mi*T+t][row][col]: each
-  // wave accumulates its own slot in program order (deterministic), and the
-  // epilogue sums the W slots in wave order.
-  __shared__ float red[W][MT][16][16];
+  constexpr int BPW = 2;       // blocks per wave
+  constexpr int MT = NM * T;   // (matrix, tile) pairs of an item
+  static_assert(MT % 2 == 0, "unit pairs share one block");
+  constexpr int PB = MT / 2;   // unit pairs per block per item
+  constexpr int PI = BPW * PB; // unit pairs per item
+  constexpr int R = 2 * DP;    // ring slots per wave: DP pairs in flight
+  // LDS: the per-wave rings, then the per-wave partial sums of an item,
+  // [wave][mi*T+t][row][col], summed in wave order by the epilogue.
+  constexpr int kRingBytes = W * R * kTileBlockBytes;
+  constexpr int kRedBytes = W * MT * 16 * 16 * 4;
+  static_assert(kRingBytes + kRedBytes <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kRingBytes + kRedBytes];
+  float* red = reinterpret_cast<float*>(lds + kRingBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int nb = a.nb, bw = wave * BPW;
   const int first = blockIdx.x, stride = gridDim.x;
+  // The wave -> K-range assignment rotates with the workgroup, so that the
+  // workgroups of one L2 do not all read the same part of x at once.
+  const int nb = a.nb, bw = ((wave + first) % W) * BPW;
   const int n_items = first < items ? (items - 1 - first) / stride + 1 : 0;
   if (n_items == 0)
     return;
-  const uint32_t ring0 = lds_addr(&ring[wave][0][0]);
+  uint8_t* const ring = lds + (size_t)wave * R * kTileBlockBytes;
+  const uint32_t ring0 = lds_addr(ring);
   const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
   const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
 
-  // Issue unit s of this wave's stream into ring slot `slot`; units past the
-  // end re-load the last unit (an L2 hit) so every iteration issues exactly
-  // three loads.
-  auto issue = [&](int s, int slot) {
+  // Pair p of this wave's stream: item p / PI, block j, (matrix, tile) pairs
+  // 2q and 2q + 1 of that block, into ring slots 2*ps, 2*ps + 1.  Pairs past
+  // the end re-load the last pair (L2 hits), so every pair issues six loads.
+  auto issue = [&](int p, int ps) {
     __builtin_amdgcn_sched_barrier(0);
-    int it = s / U;
-    int q = s - it * U;
+    int it = p / PI;
+    int r = p - it * PI;
     if (it >= n_items) {
       it = n_items - 1;
-      q = U - 1;
+      r = PI - 1;
     }
-    const int j = q / MT, mt = q - j * MT, mi = mt / T, t = mt - mi * T;
-    const int ct = (first + it * stride) * T + t;
-    const uint8_t* p = uniform_ptr((mi ? a.wu : a.w) + (size_t)ct * tile_bytes + (size_t)(bw + j) * kTileBlockBytes);
-    // The immediate offset applies to both addresses: LDS = M0 + offset + lane * size.
-    const uint32_t l = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)slot * kTileBlockBytes);
-    lds_dma16<0>(p, voff16, l);
-    lds_dma16<kSlabBytes>(p, voff16, l);
-    lds_dma4<kHeaderOffset>(p, voff4, l);
+    const int j = r / PB, q = r - j * PB;
+    const uint32_t l = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)(2 * ps) * kTileBlockBytes);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int mt = 2 * q + h, mi = mt / T, t = mt - mi * T;
+      const size_t ct = (size_t)(first + it * stride) * T + t;
+      const uint8_t* src = uniform_ptr((mi ? a.wu : a.w) + ct * tile_bytes + (size_t)(bw + j) * kTileBlockBytes);
+      // (The immediate offset applies to both addresses: LDS = M0 + offset + lane * size.)
+      const uint32_t lh = l + (uint32_t)h * kTileBlockBytes;
+      lds_dma16<0>(src, voff16, lh);
+      lds_dma16<kSlabBytes>(src, voff16, lh);
+      lds_dma4<kHeaderOffset>(src, voff4, lh);
+    }
   };
 
-  // Resident activations of this wave's blocks (dead rows of the 16-row tile
-  // are loaded unmasked; they only reach unread C rows) and the scales of the
-  // rows this thread finishes in the epilogues (clamped: always issued), then
-  // the first D units.  One wait covers the activations and unit 0.
-  u4_t xw[BPW][8];
+  // Resident activations: the decode pack of the wave's two blocks (A
+  // fragments, min-term operands, per-(row, block) unscale factors of this
+  // lane's four C rows 4g + v, i.e. rows (4g + v) & 7), loaded with
+  // coalesced 16-byte loads.  The vector L1 returns data in request order:
+  // one wait covers pair 0 and the activations, with the next DP - 1 pairs
+  // still outstanding.
+  // The first pair goes out before the activations so that HBM starts
+  // streaming at once; the activations then land right behind it.
+  issue(0, 0);
+  u4_t xw[BPW][8], dw[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+      xw[j][f] = asm_load16(a.pack.frag + ((size_t)(bw + j) * 8 + f) * 64 + lane);
+    dw[j] = asm_load16(a.pack.dsc + (size_t)(bw + j) * 8 + 4 * (g & 1));
+  }
   h4_t xsa[BPW];
 #pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-    const u4_t* xp = reinterpret_cast<const u4_t*>(a.xf) + (size_t)(bw + j) * 8 * 64 + lane;
+  for (int j = 0; j < BPW; ++j)
+    xsa[j] = asm_load8(a.pack.xs + (size_t)(bw + j) * 64 + lane);
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      xw[j][s] = asm_load16(xp + s * 64);
-    xsa[j] = asm_load8(reinterpret_cast<const h4_t*>(a.xs) + (size_t)(bw + j) * 32 + (lane & 31));
-  }
-  constexpr int EPI = 16 * T;  // outputs per row of an item
-  const int r0 = tid / EPI, r1 = (tid + 64 * W) / EPI;
-  float sc0 = asm_load4(a.rowscale + (r0 < a.m ? r0 : a.m - 1));
-  float sc1 = asm_load4(a.rowscale + (r1 < a.m ? r1 : a.m - 1));
-#pragma unroll
-  for (int s = 0; s < D; ++s)
-    issue(s, s);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (D - 1)) : "memory");
+  for (int p = 1; p < DP; ++p)
+    issue(p, p);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * (DP - 1)) : "memory");
   h8_t xa[BPW][8];
+  float dsc[BPW][4];
 #pragma unroll
   for (int j = 0; j < BPW; ++j) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      hold(xw[j][s]);
-      xa[j][s] = __builtin_bit_cast(h8_t, xw[j][s]);
+    for (int f = 0; f < 8; ++f) {
+      hold(xw[j][f]);
+      xa[j][f] = __builtin_bit_cast(h8_t, xw[j][f]);
     }
+    hold(dw[j]);
+    const f4_t dv = __builtin_bit_cast(f4_t, dw[j]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      dsc[j][v] = dv[v];
     hold(xsa[j]);
   }
-  hold(sc0);
-  hold(sc1);
 
+  constexpr int EPI = 16 * T;  // outputs per row of an item
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
-  int slot = 0;  // ring slot of the unit being computed
-  int s = 0;     // stream index of the unit being computed
+  int ps = 0;  // ring pair-slot of the pair being computed
+  int p = 0;   // stream index of the pair being computed
   for (int it = 0; it < n_items; ++it) {
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
-      for (int mt = 0; mt < MT; ++mt, ++s) {
-        issue(s + D, slot == 0 ? R - 1 : slot - 1);
-        // Three loads per unit: vmcnt(3*D) leaves exactly the D newer units
-        // outstanding.  The memory clobber keeps the LDS reads below the wait.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * D) : "memory");
-        const u4_t* sl = reinterpret_cast<const u4_t*>(&ring[wave][slot][0]);
-        const u4_t q0 = sl[lane];
-        const u4_t q1 = sl[kSlabBytes / 16 + lane];
-        const u4_t hd = sl[kHeaderOffset / 16 + col];
-        slot = slot == R - 1 ? 0 : slot + 1;
-        const BlockConsts kc = block_consts(hd, g);
-        // Two accumulation chains (low / high nibbles) keep the MFMA pipe busy.
-        f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const u4_t qq = u < 2 ? q0 : q1;
-          const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
-          const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
-          const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
-          cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], blo, cl, 0, 0, 0);
-          ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][4 + u], bhi, ch, 0, 0, 0);
+      for (int q = 0; q < PB; ++q, ++p) {
+        // Six loads per pair: with DP pairs outstanding, vmcnt(6*(DP-1))
+        // marks the oldest complete.  The memory clobber keeps the LDS
+        // reads below the wait.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * (DP - 1)) : "memory");
+        const u4_t* sl = reinterpret_cast<const u4_t*>(ring + (2 * ps) * kTileBlockBytes);
+        u4_t q0[2], q1[2], hd[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const u4_t* su = sl + h * (kTileBlockBytes / 16);
+          q0[h] = su[lane];
+          q1[h] = su[kSlabBytes / 16 + lane];
+          hd[h] = su[kHeaderOffset / 16 + col];
         }
-        const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[j], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        float* r = &red[wave][mt][4 * g][col];
+        // The pair is in registers once the reads are done: its slots take
+        // the pair DP ahead while this one is computed.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(p + DP, ps);
+        ps = ps == DP - 1 ? 0 : ps + 1;
+        // Two independent chains, one per (matrix, tile).
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float part = fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]);
-          r[16 * v] = j == 0 ? part : r[16 * v] + part;
+        for (int h = 0; h < 2; ++h) {
+          const BlockConsts kc = block_consts(hd[h], g);
+          f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const u4_t qq = u < 2 ? q0[h] : q1[h];
+            const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
+            const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+            const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+            cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], blo, cl, 0, 0, 0);
+            ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][4 + u], bhi, ch, 0, 0, 0);
+          }
+          const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[j], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          // This wave's partial sums of (matrix, tile) 2q + h over block j,
+          // unscaled to x's range; block 1 adds to block 0's.
+          float* r = red + ((wave * MT + 2 * q + h) * 16 + 4 * g) * 16 + col;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float part = fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * dsc[j][v];
+            r[16 * v] = j == 0 ? part : r[16 * v] + part;
+          }
         }
       }
     }
@@ -656,32 +781,29 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
       const int o = tid + k * 64 * W;
       if (o < a.m * EPI) {
         const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
-        const float escale = k == 0 ? sc0 : sc1;
         float sm[NM];
 #pragma unroll
         for (int mi = 0; mi < NM; ++mi) {
           float v = 0.0f;
 #pragma unroll
           for (int w = 0; w < W; ++w)
-            v += red[w][mi * T + t][row][cc];
-          if (a.split) {
+            v += red[((w * MT + mi * T + t) * 16 + row) * 16 + cc];
 #pragma unroll
-            for (int w = 0; w < W; ++w)
-              v += red[w][mi * T + t][a.m + row][cc];
-          }
+          for (int w = 0; w < W; ++w)
+            v += red[((w * MT + mi * T + t) * 16 + 8 + row) * 16 + cc];
           sm[mi] = v;
         }
         const size_t off = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
         float out;
         if (NM == 2) {
-          float gv = sm[0] * escale, uv = sm[NM - 1] * escale;
+          float gv = sm[0], uv = sm[NM - 1];
           if (sizeof(OutT) == 2) {
             gv = round_half(gv);
             uv = round_half(uv);
           }
           out = silu(gv) * uv;
         } else {
-          float acc_v = sm[0] * escale;
+          float acc_v = sm[0];
           if (sizeof(OutT) == 2)
             acc_v = round_half(acc_v);
           out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
@@ -693,6 +815,224 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
   }
   // Drain the trailing (re-load) units before the ring is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// ----------------------------------------------------------------------------
+// Split-K GEMV (m <= 8 rows, split hi/lo into one 16-row activation tile as
+// in the streaming GEMV).
+//
+// Each CU of a persistent launch would otherwise pull all of x from L2 (32 MB
+// across the chip for m = 8, K = 4096, fp32) before its first MFMA.  Here
+// workgroup b covers column group `grp` (T tiles of NM matrices) over one
+// K-slice `ks` of BPS blocks, so it reads only its slice of x:
+//  1. the workgroup converts its slice of x once into LDS: A fragments
+//     (fp16 high parts in rows 0..7, low parts in rows 8..15, per-(row, slice)
+//     power-of-two scale) and the min-term fragments (sub-block sums / 32);
+//  2. wave w owns (matrix, tile) pairs w, w + 8, ... (PW of them) and streams
+//     their tile-blocks of the slice through a private LDS ring with DP
+//     block-steps in flight; a block-step is PW independent MFMA chains
+//     over one set of A fragments;
+//  3. each wave writes its slice partials (hi + lo rows combined, unscaled)
+//     to the workspace; the last workgroup of the group to arrive (a device-
+//     scope counter, reset by that workgroup) sums the KS slices in slice
+//     order and runs the epilogue.  No workgroup ever waits for another.
+// Workgroups of one group are placed on one XCD (workgroup b runs on XCD
+// b % 8), so their partials meet in one L2.
+// ----------------------------------------------------------------------------
+template <int NM, int T, int KS, int BPS, int DP, typename OutT>
+__global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float* __restrict__ part, int* __restrict__ counters) {
+  constexpr int W = 8, MT = NM * T, PW = MT / W;
+  static_assert(MT % W == 0, "whole (matrix, tile) pairs per wave");
+  // LDS: the rings, then the slice's decode pack (fragments, min-term
+  // operands, unscale factors: the same layout as in global memory).
+  constexpr int kFragBytes = BPS * 8 * 64 * 16;  // [BPS][8 fragments][64 lanes] x 16 B
+  constexpr int kXsBytes = BPS * 64 * 8;         // [BPS][64 lanes] x 4 halves
+  constexpr int kDscBytes = BPS * 8 * 4;         // [BPS][8 rows]
+  constexpr int kPackChunks = (kFragBytes + kXsBytes + kDscBytes) / 16;
+  constexpr int kSlots = DP * PW;                // ring slots per wave
+  constexpr int kRingBytes = W * kSlots * kTileBlockBytes;
+  static_assert(kRingBytes + kFragBytes + kXsBytes + kDscBytes + 64 <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kRingBytes + kFragBytes + kXsBytes + kDscBytes];
+  __shared__ int s_last;
+  u4_t* const xf = reinterpret_cast<u4_t*>(lds + kRingBytes);
+  _Float16* const xs = reinterpret_cast<_Float16*>(lds + kRingBytes + kFragBytes);
+  const float* const dscl = reinterpret_cast<const float*>(lds + kRingBytes + kFragBytes + kXsBytes);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int sidx = (int)blockIdx.x >> 3;
+  const int ks = sidx % KS, grp = ((int)blockIdx.x & 7) + 8 * (sidx / KS);
+  const int nb = a.nb, kb0 = ks * BPS;
+  uint8_t* const ring = lds + (size_t)wave * kSlots * kTileBlockBytes;
+  const uint32_t ring0 = lds_addr(ring);
+  const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
+
+  // Block-step i of this wave: block kb0 + i of each of its PW pairs, into
+  // slot group i % DP.  Steps past the end re-load the last one (L2 hits),
+  // so every step issues exactly 3 * PW loads.
+  auto issue = [&](int i) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int bb = i < BPS ? i : BPS - 1;
+    const int sg = i % DP;
+#pragma unroll
+    for (int pw = 0; pw < PW; ++pw) {
+      const int mt = wave + W * pw, mi = mt / T, t = mt - mi * T;
+      const size_t ct = (size_t)grp * T + t;
+      const uint8_t* src = uniform_ptr((mi ? a.wu : a.w) + (ct * nb + kb0 + bb) * kTileBlockBytes);
+      const uint32_t l = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)(sg * PW + pw) * kTileBlockBytes);
+      lds_dma16<0>(src, voff16, l);
+      lds_dma16<kSlabBytes>(src, voff16, l);
+      lds_dma4<kHeaderOffset>(src, voff4, l);
+    }
+  };
+
+  // 1. The slice's decode pack is copied into LDS (16-byte chunks, clamped
+  // so that every thread issues the same number of loads); these loads of
+  // every wave are queued before any weight load.
+  constexpr int NCH = (kPackChunks + 64 * W - 1) / (64 * W);
+  u4_t pw_[NCH];
+  {
+    const uint8_t* fsrc = reinterpret_cast<const uint8_t*>(a.pack.frag) + (size_t)kb0 * 8 * 64 * 16;
+    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(a.pack.xs) + (size_t)kb0 * 64 * 8;
+    const uint8_t* dsrc = reinterpret_cast<const uint8_t*>(a.pack.dsc) + (size_t)kb0 * 8 * 4;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      int c = tid + i * 64 * W;
+      c = c < kPackChunks ? c : kPackChunks - 1;
+      const int cb = 16 * c;
+      const uint8_t* src = cb < kFragBytes ? fsrc + cb : cb < kFragBytes + kXsBytes ? xsrc + (cb - kFragBytes) : dsrc + (cb - kFragBytes - kXsBytes);
+      pw_[i] = asm_load16(src);
+    }
+  }
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int i = 0; i < DP; ++i)
+    issue(i);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PW * DP) : "memory");
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    hold(pw_[i]);
+    const int c = tid + i * 64 * W;
+    if (c < kPackChunks)
+      *reinterpret_cast<u4_t*>(lds + kRingBytes + 16 * c) = pw_[i];
+  }
+  __syncthreads();
+
+  // 2. Stream the slice's tile-blocks of this wave's pairs.
+  f4_t acc[PW];
+#pragma unroll
+  for (int pw = 0; pw < PW; ++pw)
+    acc[pw] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < BPS; ++i) {
+    // 3 * PW loads per step: with DP steps outstanding, this marks step i.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PW * (DP - 1)) : "memory");
+    const u4_t* sl = reinterpret_cast<const u4_t*>(ring + (size_t)(i % DP) * PW * kTileBlockBytes);
+    u4_t q0[PW], q1[PW], hd[PW];
+#pragma unroll
+    for (int pw = 0; pw < PW; ++pw) {
+      const u4_t* su = sl + pw * (kTileBlockBytes / 16);
+      q0[pw] = su[lane];
+      q1[pw] = su[kSlabBytes / 16 + lane];
+      hd[pw] = su[kHeaderOffset / 16 + col];
+    }
+    h8_t xa[8];
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+      xa[f] = __builtin_bit_cast(h8_t, xf[(i * 8 + f) * 64 + lane]);
+    const h4_t xsa = *reinterpret_cast<const h4_t*>(xs + (i * 64 + lane) * 4);
+    // Unscale factors of this lane's C rows (4g + v) & 7 in block i.
+    const f4_t dv = *reinterpret_cast<const f4_t*>(dscl + i * 8 + 4 * (g & 1));
+    // The step is in registers: its slots take the step DP ahead.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(i + DP);
+#pragma unroll
+    for (int pw = 0; pw < PW; ++pw) {
+      const BlockConsts kc = block_consts(hd[pw], g);
+      f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u4_t qq = u < 2 ? q0[pw] : q1[pw];
+        const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
+        const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+        const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+        cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], blo, cl, 0, 0, 0);
+        ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[4 + u], bhi, ch, 0, 0, 0);
+      }
+      const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa, kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[pw][v] += fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * dv[v];
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // 3. Slice partials: C row r (lanes g < 2) plus its low part r + 8 (lanes
+  // g + 2), unscaled; layout [grp][ks][mt][8 rows][16 columns].  They are
+  // written through to memory (system-coherent stores) and read back the
+  // same way, so no cache of any XCD needs flushing; the counter is a
+  // device-scope atomic.
+#pragma unroll
+  for (int pw = 0; pw < PW; ++pw) {
+    const int mt = wave + W * pw;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float tot = acc[pw][v] + __shfl_xor(acc[pw][v], 32);
+      const int row = 4 * g + v;
+      if (g < 2 && row < a.m)
+        store_coherent(part + ((((size_t)grp * KS + ks) * MT + mt) * 8 + row) * 16 + col, tot);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    s_last = atomicAdd(&counters[grp], 1) == KS - 1;
+  __syncthreads();
+  if (!s_last)
+    return;
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  constexpr int EPI = 16 * T;  // outputs per row of a group
+  for (int o = tid; o < a.m * EPI; o += 64 * W) {
+    const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
+    float pv[NM][KS];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int k2 = 0; k2 < KS; ++k2)
+        pv[mi][k2] = load_coherent(part + ((((size_t)grp * KS + k2) * MT + mi * T + t) * 8 + row) * 16 + cc);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    float sm[NM];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      float v = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < KS; ++k2) {
+        hold(pv[mi][k2]);
+        v += pv[mi][k2];
+      }
+      sm[mi] = v;
+    }
+    const size_t off = (size_t)row * a.n + ((size_t)grp * T + t) * 16 + cc;
+    float out;
+    if (NM == 2) {
+      float gv = sm[0], uv = sm[NM - 1];
+      if (sizeof(OutT) == 2) {
+        gv = round_half(gv);
+        uv = round_half(uv);
+      }
+      out = silu(gv) * uv;
+    } else {
+      float acc_v = sm[0];
+      if (sizeof(OutT) == 2)
+        acc_v = round_half(acc_v);
+      out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+    }
+    store_elem(y, off, out);
+  }
+  if (tid == 0)
+    atomicExch(&counters[grp], 0);  // ready for the next launch
 }
 
 // ----------------------------------------------------------------------------
@@ -915,46 +1255,108 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const Gemv
   return gemv_multi_row_tile<3, GATED>(s, a, dtype, shape.waves);
 }
 
-template <int T, int NM, int W, int BPW, int D>
+template <int T, int NM, int W, int DP>
 hipError_t stream_launch(hipStream_t s, const GemvArgs& a, int dtype, int grid, int items) {
   if (dtype == kF32)
-    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, BPW, D, float>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
+    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, DP, float>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
   else
-    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, BPW, D, _Float16>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
+    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, DP, _Float16>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
   return hipGetLastError();
 }
 
 }  // namespace
 
-bool gemv_stream_supported(int rows, int nb, int n, bool gated) {
-  (void)gated;
+namespace {
+
+// Split-K instances: (NM, T, KS, BPS, DP).  A group is T column tiles of NM
+// matrices; KS slices of BPS blocks each.
+struct SplitkInst {
+  int nm, t, ks, bps;
+};
+constexpr SplitkInst kSplitk[] = {
+    {1, 8, 8, 6},  // K = 12288 (nb = 48), N a multiple of 1024: 8 tiles x 8 slices of 6 blocks
+};
+
+template <int NM, int T, int KS, int BPS, int DP>
+hipError_t splitk_launch(hipStream_t s, const GemvArgs& a, int dtype, int grid, float* part, int* counters) {
+  if (dtype == kF32)
+    (void)dispatch(q4k_gemv_splitk_kernel<NM, T, KS, BPS, DP, float>, dim3((unsigned)grid), dim3(512), s, a, part, counters);
+  else
+    (void)dispatch(q4k_gemv_splitk_kernel<NM, T, KS, BPS, DP, _Float16>, dim3((unsigned)grid), dim3(512), s, a, part, counters);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_splitk_plan(int m, int n, int nb, bool gated, int cus, SplitkPlan* plan) {
+  static const int forced = env_int("Q4K_GEMV_SPLITK", -1);  // -1 auto, -2 off, else instance
+  if (forced == -2 || m < 1 || m > 8 || n % 16 != 0)
+    return false;
+  const int tiles = n / 16, nm = gated ? 2 : 1;
+  int best = -1, best_grid = 0;
+  for (int i = 0; i < (int)(sizeof(kSplitk) / sizeof(kSplitk[0])); ++i) {
+    const SplitkInst& c = kSplitk[i];
+    if (forced >= 0 && i != forced)
+      continue;
+    if (c.nm != nm || c.ks * c.bps != nb || tiles % c.t != 0 || (tiles / c.t) % 8 != 0)
+      continue;
+    const int grid = tiles / c.t * c.ks;
+    // Prefer the largest grid that fills at most one workgroup per CU, then
+    // the smallest grid above that.
+    const bool fits = grid <= cus, best_fits = best_grid <= cus;
+    if (best < 0 || (fits && (!best_fits || grid > best_grid)) || (!fits && !best_fits && grid < best_grid)) {
+      best = i;
+      best_grid = grid;
+    }
+  }
+  if (best < 0)
+    return false;
+  const SplitkInst& c = kSplitk[best];
+  plan->inst = best;
+  plan->groups = tiles / c.t;
+  plan->ks = c.ks;
+  plan->mt = c.nm * c.t;
+  plan->grid = best_grid;
+  return true;
+}
+
+size_t gemv_splitk_part_floats(const SplitkPlan& plan) {
+  return (size_t)plan.groups * plan.ks * plan.mt * 8 * 16;
+}
+
+hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const SplitkPlan& plan, float* part, int* counters) {
+  (void)plan.inst;  // one instance
+  return splitk_launch<1, 8, 8, 6, 4>(s, a, dtype, plan.grid, part, counters);
+}
+
+bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus) {
+  // Gated pairs (K = 4096) and wide outputs (4 tiles per item, at least 4
+  // items per CU); narrower plain projections measure faster on the
+  // register-buffered GEMV.
   static const bool enabled = env_int("Q4K_GEMV_STREAM", 1) != 0;
-  return enabled && rows <= 16 && nb == 16 && n % 16 == 0;
+  if (!enabled || rows > 16 || nb != 16 || n % 16 != 0)
+    return false;
+  const int ctiles = n / 16;
+  return gated || (ctiles % 4 == 0 && ctiles / 4 >= 4 * cus);
 }
 
 hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus) {
-  // One row tile, K = 4096 (nb = 16): 8 waves x 2 blocks, 4 units in flight
-  // per wave.  Items of T column tiles: T = 3 makes N = 12288 exactly one item
-  // per CU; wide outputs take T = 4; otherwise one tile per item.
+  // K = 4096 (nb = 16): 8 waves x 2 blocks.  Items of T column tiles (an
+  // even number of (matrix, tile) pairs): T = 3 makes gated N = 12288
+  // exactly one item per CU; other gated outputs take 1; wide plain outputs 4.
+  // LDS holds the rings (2 * DP slots of 2304 B per wave) next to the
+  // partial sums (W * 2T KB gated, W * T KB otherwise).
   const int ctiles = a.n / 16;
-  int tiles = 1;
-  if (ctiles % 3 == 0 && ctiles / 3 == cus)
-    tiles = 3;
-  else if (!gated && ctiles % 4 == 0 && ctiles / 4 >= 4 * cus)
+  int tiles;
+  if (gated)
+    tiles = ctiles % 3 == 0 && ctiles / 3 == cus ? 3 : 1;
+  else
     tiles = 4;
-  else if (!gated && ctiles % 2 == 0 && ctiles / 2 >= 2 * cus)
-    tiles = 2;
   const int items = ctiles / tiles;
   const int grid = items < cus ? items : cus;
   if (gated)
-    return tiles == 3 ? stream_launch<3, 2, 8, 2, 4>(s, a, dtype, grid, items) : stream_launch<1, 2, 8, 2, 4>(s, a, dtype, grid, items);
-  if (tiles == 4)
-    return stream_launch<4, 1, 8, 2, 4>(s, a, dtype, grid, items);
-  if (tiles == 3)
-    return stream_launch<3, 1, 8, 2, 4>(s, a, dtype, grid, items);
-  if (tiles == 2)
-    return stream_launch<2, 1, 8, 2, 4>(s, a, dtype, grid, items);
-  return stream_launch<1, 1, 8, 2, 4>(s, a, dtype, grid, items);
+    return tiles == 3 ? stream_launch<3, 2, 8, 3>(s, a, dtype, grid, items) : stream_launch<1, 2, 8, 3>(s, a, dtype, grid, items);
+  return stream_launch<4, 1, 8, 3>(s, a, dtype, grid, items);
 }
 
 template <typename InT>
@@ -966,6 +1368,15 @@ hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs,
     (void)dispatch(stage_x_kernel<InT, kStageFrag>, grid, block, s, x, xo, xs, rowscale, m, k);
   else
     (void)dispatch(stage_x_kernel<InT, kStageFragSplit>, grid, block, s, x, xo, xs, rowscale, m, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_stage_pack(hipStream_t s, const void* x, int dtype, const DecodePack& pk, int m, int k) {
+  const dim3 grid((unsigned)(k / 256 * 8)), block(64);
+  if (dtype == kF32)
+    (void)dispatch(stage_pack_kernel<float>, grid, block, s, static_cast<const float*>(x), pk.frag, pk.xs, pk.dsc, m, k);
+  else
+    (void)dispatch(stage_pack_kernel<_Float16>, grid, block, s, static_cast<const _Float16*>(x), pk.frag, pk.xs, pk.dsc, m, k);
   return hipGetLastError();
 }
 

@@ -1,0 +1,125 @@
+"""The decode kernels for m <= 8 rows (decode pack + streaming GEMV, decode
+pack + split-K GEMV) against the CPU oracle, over the row counts, dtypes and
+epilogues of a decode pass.  Shapes are chosen to reach each kernel:
+
+  gated, K=4096, N=12288   streaming GEMV, 3 column tiles per item
+  gated, K=4096, N=512     streaming GEMV, 1 column tile per item
+  plain, K=12288, N=1024   split-K GEMV (8 tiles x 8 K-slices of 6 blocks)
+  plain, K=4096, N=65536   streaming GEMV, 4 column tiles per item
+
+Bar: max row-relative error 1e-3 against the fp32-accumulated oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from q4k_ref import make_q4k, make_x, row_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _t(a, dev, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("n", [12288, 512])
+def test_gated_stream(q4k, oracle, gpu, m, n):
+    k = 4096
+    rng = np.random.default_rng(1000 + m + n)
+    wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+    x = make_x(rng, m, k, 0.5)
+    G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+    y = torch.full((m, n), float("nan"), device=gpu)
+    q4k.mlp_gate_up(_t(x, gpu), G, U, m, y, query_counts=[1] * m)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert row_rel_err(got, oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
+
+
+def test_gated_stream_f16(q4k, oracle, gpu):
+    m, n, k = 8, 12288, 4096
+    rng = np.random.default_rng(1100)
+    wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+    x = make_x(rng, m, k, 0.5).astype(np.float16)
+    G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+    y = torch.empty((m, n), device=gpu, dtype=torch.float16)
+    q4k.mlp_gate_up(_t(x, gpu, torch.float16), G, U, m, y, query_counts=[1] * m)
+    torch.cuda.synchronize()
+    assert row_rel_err(y.float().cpu().numpy(), oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
+
+
+@pytest.mark.parametrize("m", [1, 5, 8])
+@pytest.mark.parametrize("post", [0, 1, 2])
+def test_splitk(q4k, oracle, gpu, m, post):
+    n, k = 1024, 12288
+    rng = np.random.default_rng(1200 + 10 * m + post)
+    w = make_q4k(rng, n, k)
+    x = make_x(rng, m, k, 0.5)
+    aux = make_x(rng, m, n, 2.0)
+    W = q4k.Weight(w, n, k)
+    y = _t(aux, gpu) if post else torch.full((m, n), float("nan"), device=gpu)
+    q4k.linear(_t(x, gpu), W, m, y, auxiliary=y if post else None, gated=(post == 2), query_counts=[1] * m)
+    torch.cuda.synchronize()
+    ref = oracle.linear(x, w, n, k, aux=aux if post else None, post=post)
+    assert row_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+def test_splitk_f16_and_repeat(q4k, oracle, gpu):
+    """fp16 activations; then the same call again (the group counters must
+    have been left at zero by the first launch)."""
+    m, n, k = 8, 2048, 12288
+    rng = np.random.default_rng(1300)
+    w = make_q4k(rng, n, k)
+    x = make_x(rng, m, k, 0.5).astype(np.float16)
+    W = q4k.Weight(w, n, k)
+    ref = oracle.linear(x, w, n, k)
+    for _ in range(3):
+        y = torch.empty((m, n), device=gpu, dtype=torch.float16)
+        q4k.linear(_t(x, gpu, torch.float16), W, m, y, query_counts=[1] * m)
+        torch.cuda.synchronize()
+        assert row_rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
+def test_wide_stream(q4k, oracle, gpu):
+    m, n, k = 3, 65536, 4096
+    rng = np.random.default_rng(1400)
+    w = make_q4k(rng, n, k)
+    x = make_x(rng, m, k)
+    W = q4k.Weight(w, n, k)
+    y = torch.empty((m, n), device=gpu)
+    q4k.linear(_t(x, gpu), W, m, y, query_counts=[m])
+    torch.cuda.synchronize()
+    assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k)) <= TOL
+
+
+def test_decode_rows_of_extreme_magnitude(q4k, oracle, gpu):
+    """Rows far outside fp16 range (and a zero row) through both decode
+    kernels: the per-(row, block) power-of-two scales keep them exact to
+    the same relative precision."""
+    rng = np.random.default_rng(1500)
+    for n, k, gated in [(12288, 4096, True), (1024, 12288, False)]:
+        m = 4
+        x = make_x(rng, m, k)
+        x[0] *= 1e6
+        x[1] *= 1e-6
+        x[2] = 0.0
+        w = make_q4k(rng, n, k)
+        W = q4k.Weight(w, n, k)
+        y = torch.empty((m, n), device=gpu)
+        if gated:
+            wu = make_q4k(rng, n, k)
+            U = q4k.Weight(wu, n, k)
+            # Scale the gate/up inputs down so that SiLU stays in range.
+            x *= 1e-3
+            q4k.mlp_gate_up(_t(x, gpu), W, U, m, y, query_counts=[1] * m)
+            ref = oracle.mlp_gate_up(x, w, wu, n, k)
+        else:
+            q4k.linear(_t(x, gpu), W, m, y, query_counts=[1] * m)
+            ref = oracle.linear(x, w, n, k)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.all(got[2] == 0)
+        assert row_rel_err(got, ref) <= TOL
