@@ -135,6 +135,12 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvSh
 
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype);
 
+// Pipelined GEMM: xh holds the activations staged in fragment order
+// (kStageFrag) for gemm2_rows(m) rows; N a multiple of 256.
+bool gemm2_supported(int m, int n);
+int gemm2_rows(int m);
+hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype);
+
 hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx);
 
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).

@@ -1152,6 +1152,176 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// Pipelined GEMM (prefill, N a multiple of 256).
+//
+// Workgroup tile 128 rows x 256 columns, 4 waves; wave w owns columns
+// [64w, 64w + 64) (4 column tiles) of all 128 rows (8 row tiles), so every
+// weight element is dequantised once per workgroup and each A fragment read
+// from LDS feeds 4 column tiles.  K runs in u-steps of v_mfma_f32_16x16x32_f16
+// pairs: u-step t = 4 * block + u covers, in every row, elements
+// 64g + 8u + [0, 8) (low nibbles, fragment u) and 64g + 32 + 8u + [0, 8)
+// (high nibbles, fragment 4 + u) of the block, for lane groups g.
+//  - A: the activations, staged in fragment order (1 KB per (row tile,
+//    block, fragment)), stream through a 3-slot LDS ring shared by the 4
+//    waves (16 KB per u-step: 8 row tiles x 2 fragments), loaded with
+//    global_load_lds_dwordx4, two u-steps ahead; one barrier per u-step.
+//  - B: each wave streams the tile-blocks of its 4 column tiles through a
+//    private 2-block LDS ring (one block ahead) and dequantises in
+//    registers to h(h(d*sc) * q - h(dmin*m)) (the reference's prefill tile
+//    value, quant_linear.metal:43,45, with the two products rounded first)
+//    with packed fp16 operations.
+// Wait counts: per u-step a wave issues 4 A loads (two steps ahead), and at
+// the first u-step of a block 12 B loads (next block), so the loads issued
+// after A(t) number 4 at u = 0, 3 and 16 at u = 1, 2.
+// ----------------------------------------------------------------------------
+constexpr int kG2M = 128, kG2N = 256, kG2AS = 3;
+constexpr int kG2ASlot = 16 * 1024;                    // 8 row tiles x 2 fragments x 1 KB
+constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4 tile-blocks
+
+template <typename OutT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int nb = a.nb, steps = 4 * nb;
+  const int mt0 = blockIdx.y * (kG2M / 16);                 // first row tile
+  const int ct0 = blockIdx.x * (kG2N / 16) + 4 * wave;      // this wave's first column tile
+  const uint32_t aring = lds_addr(lds);
+  uint8_t* const bring = lds + kG2AS * kG2ASlot + wave * kG2BWave;
+  const uint32_t bring0 = lds_addr(bring);
+  const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
+  const _Float16* const xh = a.xh;
+
+  // A(t): this wave's 4 of the 16 fragments of u-step t (clamped to the last
+  // u-step past the end).
+  auto issue_a = [&](int t) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int tc = t < steps ? t : steps - 1;
+    const int b = tc >> 2, u = tc & 3;
+    const uint32_t slot = aring + (uint32_t)(t % kG2AS) * kG2ASlot;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = 4 * wave + i, rt = f >> 1, h = f & 1;
+      const _Float16* src = xh + ((((size_t)(mt0 + rt) * nb + b) * 8 + u + 4 * h) * 64) * 8;
+      const uint32_t l = __builtin_amdgcn_readfirstlane(slot + (uint32_t)f * 1024);
+      lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
+    }
+  };
+  // B(blk): the 4 tile-blocks of block blk (clamped) into ring half blk & 1.
+  auto issue_b = [&](int blk) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int bc = blk < nb ? blk : nb - 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint8_t* src = uniform_ptr(a.w + ((size_t)(ct0 + c) * nb + bc) * kTileBlockBytes);
+      const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * 4 + c) * kTileBlockBytes);
+      lds_dma16<0>(src, voff16, l);
+      lds_dma16<kSlabBytes>(src, voff16, l);
+      lds_dma4<kHeaderOffset>(src, voff4, l);
+    }
+  };
+
+  f4_t acc[8][4];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      acc[rt][c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  issue_b(0);
+  issue_a(0);
+  issue_a(1);
+  h2_t dslo[4], dmlo[4], dshi[4], dmhi[4];
+  for (int blk = 0; blk < nb; ++blk) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * blk + u;
+      if (u == 0 || u == 3)
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      __syncthreads();  // A(t) of every wave landed; u-step t - 1 fully read
+      issue_a(t + 2);
+      if (u == 0)
+        issue_b(blk + 1);
+      const uint8_t* bslot = bring + (size_t)((blk & 1) * 4) * kTileBlockBytes;
+      if (u == 0) {
+        // Block constants of the 4 column tiles: h(d * sc), h(dmin * m) of
+        // sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles).
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u4_t hd = *reinterpret_cast<const u4_t*>(bslot + c * kTileBlockBytes + kHeaderOffset + 16 * col);
+          uint32_t sc0, mn0, sc1, mn1;
+          scale_min_pair(hd, g, sc0, mn0, sc1, mn1);
+          const float d = half_bits_to_float(hd.x & 0xffffu), dmin = half_bits_to_float(hd.x >> 16);
+          const _Float16 a0 = (_Float16)(d * (float)sc0), b0 = (_Float16)(dmin * (float)mn0);
+          const _Float16 a1 = (_Float16)(d * (float)sc1), b1 = (_Float16)(dmin * (float)mn1);
+          dslo[c] = h2_t{a0, a0};
+          dmlo[c] = h2_t{-b0, -b0};
+          dshi[c] = h2_t{a1, a1};
+          dmhi[c] = h2_t{-b1, -b1};
+        }
+      }
+      // B fragments of u-step u: words 2(u & 1), 2(u & 1) + 1 of slab u / 2.
+      h8_t blo[4], bhi[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint2 wv = *reinterpret_cast<const uint2*>(bslot + c * kTileBlockBytes + (u >> 1) * kSlabBytes + 16 * lane + 8 * (u & 1));
+        const uint32_t w0 = wv.x, w1 = wv.y, w0s = w0 >> 8, w1s = w1 >> 8;
+        const uint32_t lw[4] = {w0, w0s, w1, w1s};
+        const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+        const h2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+        u4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const h2_t ql = as_h2(and_or(lw[e], 0x000F000Fu, 0x64006400u)) + k1024;
+          const h2_t qh = __builtin_elementwise_fma(as_h2(and_or(lw[e], 0x00F000F0u, 0x64006400u)), k16, k64);
+          lo[e] = as_u32(__builtin_elementwise_fma(ql, dslo[c], dmlo[c]));
+          hi[e] = as_u32(__builtin_elementwise_fma(qh, dshi[c], dmhi[c]));
+        }
+        blo[c] = __builtin_bit_cast(h8_t, lo);
+        bhi[c] = __builtin_bit_cast(h8_t, hi);
+      }
+      // A fragments of u-step t: [row tile][low, high].
+      const uint8_t* aslot = lds + (size_t)(t % kG2AS) * kG2ASlot;
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const h8_t alo = *reinterpret_cast<const h8_t*>(aslot + (2 * rt) * 1024 + 16 * lane);
+        const h8_t ahi = *reinterpret_cast<const h8_t*>(aslot + (2 * rt + 1) * 1024 + 16 * lane);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, blo[c], acc[rt][c], 0, 0, 0);
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bhi[c], acc[rt][c], 0, 0, 0);
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = (mt0 + rt) * 16 + 4 * g + v;
+      if (row >= a.m)
+        continue;
+      const float rs = a.rowscale[row];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const size_t o = (size_t)row * a.n + (size_t)(ct0 + c) * 16 + col;
+        float acc_v = acc[rt][c][v] * rs;
+        if (sizeof(OutT) == 2)
+          acc_v = round_half(acc_v);
+        const float out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
+        store_elem(y, o, out);
+      }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // Row gather and device re-layout.
 // ----------------------------------------------------------------------------
 template <typename T>
@@ -1416,6 +1586,24 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvSh
       a.rows != (a.split ? 2 * a.m : a.m))
     return hipErrorInvalidValue;
   return gated ? gemv_dispatch<true>(s, a, dtype, shape) : gemv_dispatch<false>(s, a, dtype, shape);
+}
+
+bool gemm2_supported(int m, int n) {
+  static const bool enabled = env_int("Q4K_GEMM2", 1) != 0;
+  return enabled && n % kG2N == 0 && m > 0;
+}
+
+int gemm2_rows(int m) {
+  return (m + kG2M - 1) / kG2M * kG2M;
+}
+
+hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype) {
+  const dim3 grid((unsigned)(a.n / kG2N), (unsigned)((a.m + kG2M - 1) / kG2M)), block(256);
+  if (dtype == kF32)
+    (void)dispatch(q4k_gemm2_kernel<float>, grid, block, s, a);
+  else
+    (void)dispatch(q4k_gemm2_kernel<_Float16>, grid, block, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype) {
