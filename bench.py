@@ -298,7 +298,7 @@ def main():
             "unit": "TFLOP/s",
             "ms_per_step": round(pre["ms_per_step"], 4),
             "roofline": {
-                "kernel": "q4k_gemm_kernel (M=2048, 206.16 GFLOP per launch)",
+                "kernel": "q4k_gemm2_kernel (M=2048, 206.16 GFLOP per launch)",
                 "bound": "mfma",
                 "achieved": round(pre["gemm_tflops"], 1),
                 "peak": FP16_DENSE_PEAK_TFLOPS,

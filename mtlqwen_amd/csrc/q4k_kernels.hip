@@ -23,8 +23,10 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef float f16_t __attribute__((ext_vector_type(16)));
 
+// g * sigmoid(g) with the hardware exponential and reciprocal (a few ulp;
+// 1 + exp(-g) >= 1, so the reciprocal never sees a denormal or zero).
 __device__ __forceinline__ float silu(float g) {
-  return g / (1.0f + expf(-g));
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
@@ -63,17 +65,17 @@ __device__ __forceinline__ void load8(const _Float16* p, float* v) {
 __device__ __forceinline__ void scale_min_pair(u4_t hd, int g, uint32_t& sc0, uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
   const uint32_t sh = 16u * (uint32_t)(g & 1);
   const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
-  if (g < 2) {
-    sc0 = a & 63u;
-    sc1 = (a >> 8) & 63u;
-    m0 = b & 63u;
-    m1 = (b >> 8) & 63u;
-  } else {
-    sc0 = (c & 15u) | ((a >> 2) & 0x30u);
-    sc1 = ((c >> 8) & 15u) | ((a >> 10) & 0x30u);
-    m0 = ((c >> 4) & 15u) | ((b >> 2) & 0x30u);
-    m1 = ((c >> 12) & 15u) | ((b >> 10) & 0x30u);
-  }
+  // Sub-blocks 0-3 keep 6 bits in a / b; sub-blocks 4-7 take the low 4 bits
+  // from c and the top 2 from a >> 2 / b >> 2.  Written as one formula with
+  // per-lane selects of plain values: a branch on g would split the caller's
+  // instruction schedule into divergent blocks.
+  const bool low = g < 2;
+  const uint32_t ysh = low ? 0u : 2u, xsh = low ? 0u : 4u;
+  const uint32_t xa = low ? a : c, xb = (low ? b : c) >> xsh, ya = a >> ysh, yb = b >> ysh;
+  sc0 = (xa & 15u) | (ya & 0x30u);
+  sc1 = ((xa >> 8) & 15u) | ((ya >> 8) & 0x30u);
+  m0 = (xb & 15u) | (yb & 0x30u);
+  m1 = ((xb >> 8) & 15u) | ((yb >> 8) & 0x30u);
 }
 
 // (a & mask) | bits in one v_and_or_b32.  Written as asm because gfx9 VOP3
@@ -1170,13 +1172,62 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
 //    registers to h(h(d*sc) * q - h(dmin*m)) (the reference's prefill tile
 //    value, quant_linear.metal:43,45, with the two products rounded first)
 //    with packed fp16 operations.
-// Wait counts: per u-step a wave issues 4 A loads (two steps ahead), and at
-// the first u-step of a block 12 B loads (next block), so the loads issued
-// after A(t) number 4 at u = 0, 3 and 16 at u = 1, 2.
+// Loads: per u-step a wave issues its 4 fragments of A(t + 2) and, at the
+// first u-step of a block, the 4 tile-blocks (12 loads) of the next block,
+// one fragment (and one tile-block) per column group so that the load
+// issue is spread over the step.
 // ----------------------------------------------------------------------------
 constexpr int kG2M = 128, kG2N = 256, kG2AS = 3;
 constexpr int kG2ASlot = 16 * 1024;                    // 8 row tiles x 2 fragments x 1 KB
 constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4 tile-blocks
+
+// Epilogue of a 128 x 64 wave tile.  Lane (col, g) holds rows 16 rt + 4 g + v
+// of column col of each column tile.  All loads of a row tile (row scales,
+// and aux for post 1 / 2) are issued before its stores so that their latency
+// is paid once per row tile; a tile wholly inside m (FULL) has no per-row
+// checks.
+template <typename OutT, int POST, bool FULL>
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&acc)[8][4], int mt0, int ct0, int lane) {
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  const int g = lane >> 4, col = lane & 15;
+  const int row0 = mt0 * 16 + 4 * g;
+  constexpr bool full = FULL;
+  // Row scales exist for the padded rows (the staging buffers cover whole
+  // 128-row tiles), so these 16-byte loads stay in bounds.
+  f4_t rs[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+    rs[rt] = *reinterpret_cast<const f4_t*>(a.rowscale + row0 + 16 * rt);
+  const size_t col0 = (size_t)ct0 * 16 + col;
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+    float av[4][4];
+    if (POST != 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int row = row0 + 16 * rt + v;
+          av[v][c] = (full || row < a.m) ? load_elem(aux, (size_t)row * a.n + col0 + 16 * c) : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = row0 + 16 * rt + v;
+      if (!full && row >= a.m)
+        continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float acc_v = acc[rt][c][v] * rs[rt][v];
+        if (sizeof(OutT) == 2)
+          acc_v = round_half(acc_v);
+        const float out = POST == 1 ? acc_v + av[v][c] : POST == 2 ? silu(av[v][c]) * acc_v : acc_v;
+        store_elem(y, (size_t)row * a.n + col0 + 16 * c, out);
+      }
+    }
+  }
+}
 
 template <typename OutT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a) {
@@ -1193,132 +1244,172 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
   const _Float16* const xh = a.xh;
 
-  // A(t): this wave's 4 of the 16 fragments of u-step t (clamped to the last
-  // u-step past the end).
-  auto issue_a = [&](int t) {
-    __builtin_amdgcn_sched_barrier(0);
+  // A(t, i): fragment i of this wave's 4 (of the 16) fragments of u-step t
+  // (clamped to the last u-step past the end).
+  auto issue_a = [&](int t, int i) {
     const int tc = t < steps ? t : steps - 1;
     const int b = tc >> 2, u = tc & 3;
-    const uint32_t slot = aring + (uint32_t)(t % kG2AS) * kG2ASlot;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = 4 * wave + i, rt = f >> 1, h = f & 1;
-      const _Float16* src = xh + ((((size_t)(mt0 + rt) * nb + b) * 8 + u + 4 * h) * 64) * 8;
-      const uint32_t l = __builtin_amdgcn_readfirstlane(slot + (uint32_t)f * 1024);
-      lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
-    }
+    const int f = 4 * wave + i, rt = f >> 1, h = f & 1;
+    const _Float16* src = xh + ((((size_t)(mt0 + rt) * nb + b) * 8 + u + 4 * h) * 64) * 8;
+    const uint32_t l = __builtin_amdgcn_readfirstlane(aring + (uint32_t)(t % kG2AS) * kG2ASlot + (uint32_t)f * 1024);
+    lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
   };
-  // B(blk): the 4 tile-blocks of block blk (clamped) into ring half blk & 1.
-  auto issue_b = [&](int blk) {
-    __builtin_amdgcn_sched_barrier(0);
+  // B(blk, c): tile-block c of block blk (clamped) into ring half blk & 1.
+  auto issue_b = [&](int blk, int c) {
     const int bc = blk < nb ? blk : nb - 1;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint8_t* src = uniform_ptr(a.w + ((size_t)(ct0 + c) * nb + bc) * kTileBlockBytes);
-      const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * 4 + c) * kTileBlockBytes);
-      lds_dma16<0>(src, voff16, l);
-      lds_dma16<kSlabBytes>(src, voff16, l);
-      lds_dma4<kHeaderOffset>(src, voff4, l);
-    }
+    const uint8_t* src = uniform_ptr(a.w + ((size_t)(ct0 + c) * nb + bc) * kTileBlockBytes);
+    const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * 4 + c) * kTileBlockBytes);
+    lds_dma16<0>(src, voff16, l);
+    lds_dma16<kSlabBytes>(src, voff16, l);
+    lds_dma4<kHeaderOffset>(src, voff4, l);
   };
 
+  // Block constants of the 4 column tiles: h(d * sc), -h(dmin * m) of
+  // sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles), from the 4
+  // headers (this lane's column) of one block.
+  h2_t dslo[4], dmlo[4], dshi[4], dmhi[4];
+  auto block_consts_from = [&](const u4_t* hd) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t sc0, mn0, sc1, mn1;
+      scale_min_pair(hd[c], g, sc0, mn0, sc1, mn1);
+      const float d = half_bits_to_float(hd[c].x & 0xffffu), dmin = half_bits_to_float(hd[c].x >> 16);
+      const _Float16 a0 = (_Float16)(d * (float)sc0), b0 = (_Float16)(dmin * (float)mn0);
+      const _Float16 a1 = (_Float16)(d * (float)sc1), b1 = (_Float16)(dmin * (float)mn1);
+      dslo[c] = h2_t{a0, a0};
+      dmlo[c] = h2_t{-b0, -b0};
+      dshi[c] = h2_t{a1, a1};
+      dmhi[c] = h2_t{-b1, -b1};
+    }
+  };
+  // B fragments of column tile c from its two raw words (words 2(u & 1),
+  // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants.
+  auto dequant_words = [&](int c, uint2 wv, h8_t& blo, h8_t& bhi) {
+    const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+    const uint32_t lw[4] = {wv.x, wv.x >> 8, wv.y, wv.y >> 8};
+    u4_t lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const h2_t ql = as_h2(and_or(lw[e], 0x000F000Fu, 0x64006400u)) + k1024;
+      const h2_t qh = __builtin_elementwise_fma(as_h2(and_or(lw[e], 0x00F000F0u, 0x64006400u)), k16, k64);
+      lo[e] = as_u32(__builtin_elementwise_fma(ql, dslo[c], dmlo[c]));
+      hi[e] = as_u32(__builtin_elementwise_fma(qh, dshi[c], dmhi[c]));
+    }
+    blo = __builtin_bit_cast(h8_t, lo);
+    bhi = __builtin_bit_cast(h8_t, hi);
+  };
+
+  // Accumulators: 32 MFMA tiles, zeroed and pinned to AGPRs (the loop-carried
+  // values then stay in AGPRs instead of being copied through VGPRs).
   f4_t acc[8][4];
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 4; ++c) {
       acc[rt][c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      asm volatile("" : "+a"(acc[rt][c]));
+    }
 
-  issue_b(0);
-  issue_a(0);
-  issue_a(1);
-  h2_t dslo[4], dmlo[4], dshi[4], dmhi[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    issue_b(0, c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    issue_a(0, i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    issue_a(1, i);
+  // B(0) landed: 8 A loads were issued after it.
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  h8_t bclo[4], bchi[4];  // dequantised B fragments of the current u-step
+  {
+    u4_t hd[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      hd[c] = *reinterpret_cast<const u4_t*>(bring + c * kTileBlockBytes + kHeaderOffset + 16 * col);
+    block_consts_from(hd);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      dequant_words(c, *reinterpret_cast<const uint2*>(bring + c * kTileBlockBytes + 16 * lane), bclo[c], bchi[c]);
+  }
   for (int blk = 0; blk < nb; ++blk) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * blk + u;
+      // Own loads issued after A(t) (during u-steps t - 2 and t - 1, in the
+      // order of the column groups below): 4 at u = 0 and 3, 16 at u = 1,
+      // 7 at u = 2.  At u = 3 this also covers B(blk + 1), issued before A(t).
       if (u == 0 || u == 3)
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-      else
+      else if (u == 1)
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
       __syncthreads();  // A(t) of every wave landed; u-step t - 1 fully read
-      issue_a(t + 2);
-      if (u == 0)
-        issue_b(blk + 1);
-      const uint8_t* bslot = bring + (size_t)((blk & 1) * 4) * kTileBlockBytes;
-      if (u == 0) {
-        // Block constants of the 4 column tiles: h(d * sc), h(dmin * m) of
-        // sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles).
+      __builtin_amdgcn_sched_barrier(0);
+      // LDS reads of the step: the 16 A fragments of u-step t ([row tile][low,
+      // high]), then (u = 3) the headers of the next block, then the raw B
+      // words of u-step t + 1.  At u = 3 that is the next block, whose B
+      // landed before A(t) (issued at u = 0).
+      const int bn = u == 3 ? blk + 1 : blk, un = (u + 1) & 3;
+      const uint8_t* aslot = lds + (size_t)(t % kG2AS) * kG2ASlot;
+      h8_t af[16];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u4_t hd = *reinterpret_cast<const u4_t*>(bslot + c * kTileBlockBytes + kHeaderOffset + 16 * col);
-          uint32_t sc0, mn0, sc1, mn1;
-          scale_min_pair(hd, g, sc0, mn0, sc1, mn1);
-          const float d = half_bits_to_float(hd.x & 0xffffu), dmin = half_bits_to_float(hd.x >> 16);
-          const _Float16 a0 = (_Float16)(d * (float)sc0), b0 = (_Float16)(dmin * (float)mn0);
-          const _Float16 a1 = (_Float16)(d * (float)sc1), b1 = (_Float16)(dmin * (float)mn1);
-          dslo[c] = h2_t{a0, a0};
-          dmlo[c] = h2_t{-b0, -b0};
-          dshi[c] = h2_t{a1, a1};
-          dmhi[c] = h2_t{-b1, -b1};
-        }
+      for (int i = 0; i < 16; ++i)
+        af[i] = *reinterpret_cast<const h8_t*>(aslot + i * 1024 + 16 * lane);
+      const uint8_t* bslot = bring + (size_t)((bn & 1) * 4) * kTileBlockBytes;
+      u4_t hd[4];
+      if (u == 3) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          hd[c] = *reinterpret_cast<const u4_t*>(bslot + c * kTileBlockBytes + kHeaderOffset + 16 * col);
       }
-      // B fragments of u-step u: words 2(u & 1), 2(u & 1) + 1 of slab u / 2.
-      h8_t blo[4], bhi[4];
+      uint2 wv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        wv[c] = *reinterpret_cast<const uint2*>(bslot + c * kTileBlockBytes + (un >> 1) * kSlabBytes + 16 * lane + 8 * (un & 1));
+      __builtin_amdgcn_sched_barrier(0);
+      // Column tile c: its 16 MFMAs of u-step t, then its B fragments of
+      // u-step t + 1 replace the ones just consumed.  The dequantisation of
+      // column c runs under the MFMAs of column c + 1.
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint2 wv = *reinterpret_cast<const uint2*>(bslot + c * kTileBlockBytes + (u >> 1) * kSlabBytes + 16 * lane + 8 * (u & 1));
-        const uint32_t w0 = wv.x, w1 = wv.y, w0s = w0 >> 8, w1s = w1 >> 8;
-        const uint32_t lw[4] = {w0, w0s, w1, w1s};
-        const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-        const h2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
-        u4_t lo, hi;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const h2_t ql = as_h2(and_or(lw[e], 0x000F000Fu, 0x64006400u)) + k1024;
-          const h2_t qh = __builtin_elementwise_fma(as_h2(and_or(lw[e], 0x00F000F0u, 0x64006400u)), k16, k64);
-          lo[e] = as_u32(__builtin_elementwise_fma(ql, dslo[c], dmlo[c]));
-          hi[e] = as_u32(__builtin_elementwise_fma(qh, dshi[c], dmhi[c]));
+        for (int rt = 0; rt < 8; ++rt) {
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt], bclo[c], acc[rt][c], 0, 0, 0);
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt + 1], bchi[c], acc[rt][c], 0, 0, 0);
         }
-        blo[c] = __builtin_bit_cast(h8_t, lo);
-        bhi[c] = __builtin_bit_cast(h8_t, hi);
+        if (c == 0 && u == 3)
+          block_consts_from(hd);
+        if (c > 0)
+          dequant_words(c - 1, wv[c - 1], bclo[c - 1], bchi[c - 1]);
+        // The loads of the column group, spread over the step: fragment c
+        // of A(t + 2) and, at u = 0, tile-block c of B(blk + 1).
+        issue_a(t + 2, c);
+        if (u == 0)
+          issue_b(blk + 1, c);
       }
-      // A fragments of u-step t: [row tile][low, high].
-      const uint8_t* aslot = lds + (size_t)(t % kG2AS) * kG2ASlot;
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const h8_t alo = *reinterpret_cast<const h8_t*>(aslot + (2 * rt) * 1024 + 16 * lane);
-        const h8_t ahi = *reinterpret_cast<const h8_t*>(aslot + (2 * rt + 1) * 1024 + 16 * lane);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, blo[c], acc[rt][c], 0, 0, 0);
-          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bhi[c], acc[rt][c], 0, 0, 0);
-        }
-      }
+      dequant_words(3, wv[3], bclo[3], bchi[3]);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  OutT* y = reinterpret_cast<OutT*>(a.y);
-  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  // Pin the accumulators to AGPRs at the loop exit, so that the epilogue's
+  // element reads do not pull copies of them into the loop.
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = (mt0 + rt) * 16 + 4 * g + v;
-      if (row >= a.m)
-        continue;
-      const float rs = a.rowscale[row];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const size_t o = (size_t)row * a.n + (size_t)(ct0 + c) * 16 + col;
-        float acc_v = acc[rt][c][v] * rs;
-        if (sizeof(OutT) == 2)
-          acc_v = round_half(acc_v);
-        const float out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
-        store_elem(y, o, out);
-      }
-    }
+    for (int c = 0; c < 4; ++c)
+      asm volatile("" : "+a"(acc[rt][c]));
+
+  // One straight-line epilogue per (post code, tile inside m or not).
+  const bool full = mt0 * 16 + kG2M <= a.m;
+  if (a.post == 0)
+    full ? gemm2_epilogue<OutT, 0, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 0, false>(a, acc, mt0, ct0, lane);
+  else if (a.post == 1)
+    full ? gemm2_epilogue<OutT, 1, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 1, false>(a, acc, mt0, ct0, lane);
+  else
+    full ? gemm2_epilogue<OutT, 2, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 2, false>(a, acc, mt0, ct0, lane);
 }
 
 // ----------------------------------------------------------------------------
