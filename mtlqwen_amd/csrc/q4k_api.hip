@@ -401,14 +401,14 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
   const bool gemm2 = !gemv && gemm2_supported((int)m, (int)w->n);
   const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : gemm2 ? (size_t)gemm2_rows((int)m) : m;
   // xs is read 32 lanes at a time from its start; +128 halves of slack.
-  const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : gemm2 ? gemv_xs_halves((int)ws_rows, (int)w->k) + 128 : 0;
+  const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : 0;
   int rc = ensure_workspace(ws, w->device, ws_rows * w->k + xs_halves, ws_rows);
   if (rc)
     return rc;
   _Float16* xs = ws.x + ws_rows * w->k;
   {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
-    const int mode = gemm2 ? kStageFrag : !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
+    const int mode = gemm2 ? kStageGemm : !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
     Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode), "stage_x launch");
   }
   if (gemv) {

@@ -172,6 +172,18 @@ __device__ __forceinline__ size_t frag_offset(int row, int c, int nb) {
   return ((((size_t)(row >> 4) * nb + b) * 8 + sl) * 64 + (g * 16 + (row & 15))) * 8;
 }
 
+// Element offset of (row, 8-element chunk c) in the pipelined GEMM's order:
+// per (128-row block R, 256-element block b, u-step u) one contiguous 16 KB
+// run of 16 fragments f = 2 * (row tile within R) + h, h = 0 for the low-
+// nibble half (elements 64g + 8u + [0, 8)) and 1 for the high-nibble half
+// (64g + 32 + 8u + [0, 8)); fragment lane 16g + row % 16.  One u-step of a
+// workgroup's A operand is then a single contiguous read.
+__device__ __forceinline__ size_t gemm_frag_offset(int row, int c, int nb) {
+  const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, h = (e >> 5) & 1, u = (e >> 3) & 3;
+  const int f = 2 * ((row >> 4) & 7) + h;
+  return (((((size_t)(row >> 7) * nb + b) * 4 + u) * 16 + f) * 64 + (g * 16 + (row & 15))) * 8;
+}
+
 // Half index of (row, sub-block j of block b) in the min-term fragments: per
 // (row tile, block), lane 16 * (j / 4) + row % 16 holds j % 4 of 4 halves --
 // the A operand of v_mfma_f32_16x16x16_f16 with k = sub-block (8 of 16 used).
@@ -196,6 +208,11 @@ __device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row,
   if (MODE == kStageRowMajor) {
     if (live)
       *reinterpret_cast<h8_t*>(xo + (size_t)row * k + (size_t)c * 8) = hi;
+    return;
+  }
+  if (MODE == kStageGemm) {
+    if (live)
+      *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, c, nb)) = hi;
     return;
   }
   if (live) {
@@ -1163,21 +1180,22 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
 // pairs: u-step t = 4 * block + u covers, in every row, elements
 // 64g + 8u + [0, 8) (low nibbles, fragment u) and 64g + 32 + 8u + [0, 8)
 // (high nibbles, fragment 4 + u) of the block, for lane groups g.
-//  - A: the activations, staged in fragment order (1 KB per (row tile,
-//    block, fragment)), stream through a 3-slot LDS ring shared by the 4
-//    waves (16 KB per u-step: 8 row tiles x 2 fragments), loaded with
-//    global_load_lds_dwordx4, two u-steps ahead; one barrier per u-step.
+//  - A: the activations, staged in the GEMM order (gemm_frag_offset: one
+//    contiguous 16 KB run per (row block, u-step)), stream through a
+//    5-slot LDS ring shared by the 4 waves (16 KB per u-step: 8 row tiles
+//    x 2 fragments), loaded with global_load_lds_dwordx4 four u-steps ahead;
+//    one barrier per u-step.
 //  - B: each wave streams the tile-blocks of its 4 column tiles through a
 //    private 2-block LDS ring (one block ahead) and dequantises in
 //    registers to h(h(d*sc) * q - h(dmin*m)) (the reference's prefill tile
 //    value, quant_linear.metal:43,45, with the two products rounded first)
 //    with packed fp16 operations.
-// Loads: per u-step a wave issues its 4 fragments of A(t + 2) and, at the
+// Loads: per u-step a wave issues its 4 fragments of A(t + 4) and, at the
 // first u-step of a block, the 4 tile-blocks (12 loads) of the next block,
 // one fragment (and one tile-block) per column group so that the load
 // issue is spread over the step.
 // ----------------------------------------------------------------------------
-constexpr int kG2M = 128, kG2N = 256, kG2AS = 3;
+constexpr int kG2M = 128, kG2N = 256, kG2AS = 5, kG2AD = 4;  // A ring slots, A distance
 constexpr int kG2ASlot = 16 * 1024;                    // 8 row tiles x 2 fragments x 1 KB
 constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4 tile-blocks
 
@@ -1249,8 +1267,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto issue_a = [&](int t, int i) {
     const int tc = t < steps ? t : steps - 1;
     const int b = tc >> 2, u = tc & 3;
-    const int f = 4 * wave + i, rt = f >> 1, h = f & 1;
-    const _Float16* src = xh + ((((size_t)(mt0 + rt) * nb + b) * 8 + u + 4 * h) * 64) * 8;
+    const int f = 4 * wave + i;
+    const _Float16* src = xh + ((((size_t)blockIdx.y * nb + b) * 4 + u) * 16 + f) * 512;
     const uint32_t l = __builtin_amdgcn_readfirstlane(aring + (uint32_t)(t % kG2AS) * kG2ASlot + (uint32_t)f * 1024);
     lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
   };
@@ -1315,13 +1333,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int c = 0; c < 4; ++c)
     issue_b(0, c);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    issue_a(0, i);
+  for (int t = 0; t < kG2AD; ++t)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    issue_a(1, i);
-  // B(0) landed: 8 A loads were issued after it.
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    for (int i = 0; i < 4; ++i)
+      issue_a(t, i);
+  // B(0) and A(0) landed: A(1..3) (12 loads) were issued after them.
+  asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   h8_t bclo[4], bchi[4];  // dequantised B fragments of the current u-step
   {
     u4_t hd[4];
@@ -1337,15 +1354,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * blk + u;
-      // Own loads issued after A(t) (during u-steps t - 2 and t - 1, in the
-      // order of the column groups below): 4 at u = 0 and 3, 16 at u = 1,
-      // 7 at u = 2.  At u = 3 this also covers B(blk + 1), issued before A(t).
-      if (u == 0 || u == 3)
-        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-      else if (u == 1)
-        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      // Own loads issued after A(t) (during u-steps t - 4 .. t - 1, in the
+      // order of the column groups below): 15 at u = 0 (the 3 of B tile 3
+      // that follow A(t) at u-step t - 4, then 3 x 4), 24 at u = 1, 2, 3.
+      // At u = 3 B(blk + 1), issued at u-step t - 3 after A(t), must have
+      // landed too: 8 loads follow it.  (A(0) is waited for in the prologue.)
+      if (u == 0)
+        asm volatile("s_waitcnt vmcnt(15)" ::: "memory");
+      else if (u == 3)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
       else
-        asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
       __syncthreads();  // A(t) of every wave landed; u-step t - 1 fully read
       __builtin_amdgcn_sched_barrier(0);
       // LDS reads of the step: the 16 A fragments of u-step t ([row tile][low,
@@ -1385,12 +1404,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (c > 0)
           dequant_words(c - 1, wv[c - 1], bclo[c - 1], bchi[c - 1]);
         // The loads of the column group, spread over the step: fragment c
-        // of A(t + 2) and, at u = 0, tile-block c of B(blk + 1).
-        issue_a(t + 2, c);
+        // of A(t + 4) and, at u = 0, tile-block c of B(blk + 1).
+        issue_a(t + kG2AD, c);
         if (u == 0)
           issue_b(blk + 1, c);
       }
       dequant_words(3, wv[3], bclo[3], bchi[3]);
+      // Schedule of the step: the LDS reads first, then each MFMA followed
+      // by a share of the vector work (the next step's dequantisation, and
+      // at u = 3 the next block's constants), so that no vector work is
+      // left after the last MFMA.
+      if (u == 3) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
+#pragma unroll
+        for (int i = 0; i < 64; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x100, 20, 0);
+#pragma unroll
+        for (int i = 0; i < 64; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+      }
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1627,6 +1665,8 @@ hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs,
     (void)dispatch(stage_x_kernel<InT, kStageRowMajor>, grid, block, s, x, xo, xs, rowscale, m, k);
   else if (mode == kStageFrag)
     (void)dispatch(stage_x_kernel<InT, kStageFrag>, grid, block, s, x, xo, xs, rowscale, m, k);
+  else if (mode == kStageGemm)
+    (void)dispatch(stage_x_kernel<InT, kStageGemm>, grid, block, s, x, xo, xs, rowscale, m, k);
   else
     (void)dispatch(stage_x_kernel<InT, kStageFragSplit>, grid, block, s, x, xo, xs, rowscale, m, k);
   return hipGetLastError();
