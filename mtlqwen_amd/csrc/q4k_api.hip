@@ -353,14 +353,12 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
   const int rows = split ? 2 * (int)m : (int)m;
   SplitkPlan plan;
   if (gemv && gemv_splitk_plan((int)m, (int)w->n, (int)(w->k / 256), wu != nullptr, device_cus(w->device), &plan)) {
-    // Split-K GEMV: decode pack, then partials in the workspace.
+    // Split-K GEMV: each workgroup packs its own K-slice of x; partials in
+    // the workspace.
     int rc = ensure_splitk_workspace(ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
     if (rc)
       return rc;
     GemvArgs a{};
-    rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);
-    if (rc)
-      return rc;
     a.w = w->data;
     a.wu = wu ? wu->data : w->data;
     a.x = x;

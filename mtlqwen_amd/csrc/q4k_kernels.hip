@@ -308,21 +308,41 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
 // magnitude in [2^14, 2^15); hi + lo carries about 22 significant bits.
 // One 64-thread workgroup per (block, row); lane l holds elements 4l..4l+3.
 // ----------------------------------------------------------------------------
-template <typename InT>
-__global__ __launch_bounds__(64) void stage_pack_kernel(const InT* __restrict__ x, u4_t* __restrict__ frag, h4_t* __restrict__ xs,
-                                                        float* __restrict__ dsc, int m, int k) {
-  const int b = blockIdx.x >> 3, r = blockIdx.x & 7, l = threadIdx.x;
-  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (r < m) {
-    const InT* p = x + (size_t)r * k + (size_t)b * 256 + 4 * l;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = (float)p[e];
-  }
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-    amax = fmaxf(amax, __shfl_xor(amax, off));
+// Cross-lane steps on the VALU (DPP), without the LDS crossbar's latency.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm(1, 0, 3, 2)
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm(2, 3, 0, 1)
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8 lanes
+constexpr int kDppRowMirror = 0x140;  // lane i <-> 15 - i within 16 lanes
+
+// Sum over each aligned group of 8 lanes, in every lane of the group.
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v += dpp_f<kDppQuadSwap1>(v);
+  v += dpp_f<kDppQuadSwap2>(v);
+  return v + dpp_f<kDppHalfMirror>(v);
+}
+
+// Maximum over the 64 lanes (uniform result).
+__device__ __forceinline__ float max64_lanes(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Packs the four elements v of lane l (elements 4l..4l+3 of row r of one
+// block) into the block's fragments frag_b [8][64], min-term operands xs_b
+// [64] and unscale factors dsc_b [8]; the 64 lanes of one wave call it
+// together.  The pointers may be global or LDS.
+__device__ __forceinline__ void pack_block_row(const float (&v)[4], int r, int l, u4_t* frag_b, h4_t* xs_b, float* dsc_b) {
+  const float amax = max64_lanes(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
   float up = 1.0f, down = 1.0f;
   if (amax > 0.0f && amax <= FLT_MAX) {
     int ex;
@@ -339,16 +359,13 @@ __global__ __launch_bounds__(64) void stage_pack_kernel(const InT* __restrict__ 
   // Element e = 4l: lane group g = e / 64, fragment s = 4 ((e / 32) & 1) +
   // (e / 8) & 3, half offset e & 7 (0 or 4).
   const int e = 4 * l, g = e >> 6, fs = 4 * ((e >> 5) & 1) + ((e >> 3) & 3), h0 = e & 7;
-  uint2* fh = reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(frag + ((size_t)b * 8 + fs) * 64 + 16 * g + r) + h0);
-  uint2* fl = reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(frag + ((size_t)b * 8 + fs) * 64 + 16 * g + r + 8) + h0);
+  uint2* fh = reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(frag_b + fs * 64 + 16 * g + r) + h0);
+  uint2* fl = reinterpret_cast<uint2*>(reinterpret_cast<_Float16*>(frag_b + fs * 64 + 16 * g + r + 8) + h0);
   *fh = uint2{__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
   *fl = uint2{__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)};
   // Sub-block j = l / 8: eight lanes.
-  float sum = (t0 + t1) + (t2 + t3);
-  sum += __shfl_xor(sum, 1);
-  sum += __shfl_xor(sum, 2);
-  sum += __shfl_xor(sum, 4);
-  _Float16* xsh = reinterpret_cast<_Float16*>(xs + (size_t)b * 64);
+  const float sum = sum8_lanes((t0 + t1) + (t2 + t3));
+  _Float16* xsh = reinterpret_cast<_Float16*>(xs_b);
   if ((l & 7) == 0) {
     const int j = l >> 3;
     const float s32 = sum * 0.03125f;
@@ -357,9 +374,23 @@ __global__ __launch_bounds__(64) void stage_pack_kernel(const InT* __restrict__ 
     xsh[(16 * (j >> 2) + r + 8) * 4 + (j & 3)] = (_Float16)(s32 - (float)sh);
   }
   if (r == 0 && l < 32)  // lanes 32..63 of the min-term operand
-    xs[(size_t)b * 64 + 32 + l] = h4_t{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+    xs_b[32 + l] = h4_t{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
   if (l == 0)
-    dsc[(size_t)b * 8 + r] = down;
+    dsc_b[r] = down;
+}
+
+template <typename InT>
+__global__ __launch_bounds__(64) void stage_pack_kernel(const InT* __restrict__ x, u4_t* __restrict__ frag, h4_t* __restrict__ xs,
+                                                        float* __restrict__ dsc, int m, int k) {
+  const int b = blockIdx.x >> 3, r = blockIdx.x & 7, l = threadIdx.x;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (r < m) {
+    const InT* p = x + (size_t)r * k + (size_t)b * 256 + 4 * l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = (float)p[e];
+  }
+  pack_block_row(v, r, l, frag + (size_t)b * 8 * 64, xs + (size_t)b * 64, dsc + (size_t)b * 8);
 }
 
 // ----------------------------------------------------------------------------
@@ -620,6 +651,10 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 // Same, into a register that keeps its value in lanes the load skips.
 __device__ __forceinline__ void asm_load16_into(u4_t& r, const void* p) {
   asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(r) : "v"(p));
+}
+
+__device__ __forceinline__ void asm_load8_into(h4_t& r, const void* p) {
+  asm volatile("global_load_dwordx2 %0, %1, off" : "+v"(r) : "v"(p));
 }
 
 __device__ __forceinline__ h4_t asm_load8(const void* p) {
@@ -906,35 +941,47 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
     }
   };
 
-  // 1. The slice's decode pack is copied into LDS (16-byte chunks, clamped
-  // so that every thread issues the same number of loads); these loads of
-  // every wave are queued before any weight load.
-  constexpr int NCH = (kPackChunks + 64 * W - 1) / (64 * W);
-  u4_t pw_[NCH];
-  {
-    const uint8_t* fsrc = reinterpret_cast<const uint8_t*>(a.pack.frag) + (size_t)kb0 * 8 * 64 * 16;
-    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(a.pack.xs) + (size_t)kb0 * 64 * 8;
-    const uint8_t* dsrc = reinterpret_cast<const uint8_t*>(a.pack.dsc) + (size_t)kb0 * 8 * 4;
+  // 1. The workgroup packs its slice of x into LDS (the decode pack layout,
+  // see stage_pack_kernel): wave w converts (block, row) pairs w, w + 8, ...
+  // of the slice.  Its loads of x are queued before any weight load.
+  constexpr int PPW = BPS * 8 / W;  // (block, row) pairs per wave
+  static_assert(BPS * 8 % W == 0, "whole pairs per wave");
+  const OutT* const xin = reinterpret_cast<const OutT*>(a.x);
+  // Ordinary loads: the compiler waits for them (vmcnt(0), which also covers
+  // the weight prologue issued meanwhile) before their first use.  Loads
+  // issued as asm would save that wait but leave their destinations open to
+  // register copies made before the data arrives.
+  float xv[PPW][4];
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      int c = tid + i * 64 * W;
-      c = c < kPackChunks ? c : kPackChunks - 1;
-      const int cb = 16 * c;
-      const uint8_t* src = cb < kFragBytes ? fsrc + cb : cb < kFragBytes + kXsBytes ? xsrc + (cb - kFragBytes) : dsrc + (cb - kFragBytes - kXsBytes);
-      pw_[i] = asm_load16(src);
+  for (int j = 0; j < PPW; ++j) {
+    const int pr = wave + W * j, r = pr & 7;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      xv[j][e] = 0.0f;
+    if (r < a.m) {
+      const OutT* src = xin + (size_t)r * a.k + (size_t)(kb0 + (pr >> 3)) * 256 + 4 * lane;
+      if (sizeof(OutT) == 4) {
+        const f4_t t4 = *reinterpret_cast<const f4_t*>(src);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[j][e] = t4[e];
+      } else {
+        const h4_t t4 = *reinterpret_cast<const h4_t*>(src);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[j][e] = (float)t4[e];
+      }
     }
   }
   __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int i = 0; i < DP; ++i)
     issue(i);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PW * DP) : "memory");
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    hold(pw_[i]);
-    const int c = tid + i * 64 * W;
-    if (c < kPackChunks)
-      *reinterpret_cast<u4_t*>(lds + kRingBytes + 16 * c) = pw_[i];
+  for (int j = 0; j < PPW; ++j) {
+    const int pr = wave + W * j, i = pr >> 3, r = pr & 7;
+    const float (&v)[4] = xv[j];
+    pack_block_row(v, r, lane, xf + (size_t)i * 8 * 64, reinterpret_cast<h4_t*>(xs) + (size_t)i * 64, const_cast<float*>(dscl) + (size_t)i * 8);
   }
   __syncthreads();
 
