@@ -340,14 +340,16 @@ int set_device(int device) {
   return Q4K_OK;
 }
 
-// One projection (phase already chosen) on the weight's device.
-int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m, uint32_t post, uint32_t dtype,
-               uint32_t phase) {
+// One projection (phase already chosen) on the weight's device, with the
+// device's workspace lock held.  restage == false reuses the staged x of the
+// previous call, which must have been a projection of the same x with the
+// same (m, k, n) under the same lock; the decode pack and split-K paths always
+// stage (they are not reached by such pairs).
+int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m,
+                      uint32_t post, uint32_t dtype, uint32_t phase, bool restage) {
   Kernel& kern = resolve(w, phase);
   if (wu)
     resolve(wu, phase);
-  Workspace& ws = workspace(w->device);
-  std::lock_guard<std::mutex> lock(ws.mu);
   const bool gemv = kern.kind != kGemm || m <= 16u * kGemvMaxRowTiles;
   const bool split = gemv && gemv_split((int)m);
   const int rows = split ? 2 * (int)m : (int)m;
@@ -404,7 +406,7 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
   if (rc)
     return rc;
   _Float16* xs = ws.x + ws_rows * w->k;
-  {
+  if (restage) {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
     const int mode = gemm2 ? kStageGemm : !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
     Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode), "stage_x launch");
@@ -446,6 +448,13 @@ int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x,
       Q4K_TRY_HIP(launch_gemm(stream, a, (int)dtype), "gemm launch");
   }
   return Q4K_OK;
+}
+
+int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m, uint32_t post, uint32_t dtype,
+               uint32_t phase) {
+  Workspace& ws = workspace(w->device);
+  std::lock_guard<std::mutex> lock(ws.mu);
+  return run_linear_locked(stream, ws, w, wu, x, y, aux, m, post, dtype, phase, true);
 }
 
 }  // namespace
@@ -667,11 +676,15 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
       return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
     return run_linear(s, wg, wu, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase);
   }
-  // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in place.
-  rc = run_linear(s, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase);
+  // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in
+  // place.  Both read the same x: it is staged once, under one hold of the
+  // workspace lock.
+  Workspace& ws = workspace(wg->device);
+  std::lock_guard<std::mutex> lock(ws.mu);
+  rc = run_linear_locked(s, ws, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, true);
   if (rc)
     return rc;
-  return run_linear(s, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase);
+  return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, false);
 }
 
 int q4k_profile_enable(int on) {
