@@ -379,6 +379,91 @@ __device__ __forceinline__ void pack_block_row(const float (&v)[4], int r, int l
     dsc_b[r] = down;
 }
 
+// GEMM staging (kStageGemm) with 8 rows per workgroup: thread t converts row
+// t / 32 of the workgroup's 8, chunks (8 elements) t % 32 + 32 j.  The 8
+// rows' 16-byte pieces of one fragment lane group are one 128-byte line, so
+// every line is written whole by one workgroup (row-per-workgroup staging
+// leaves 8 workgroups, on different XCDs, writing 16 bytes of each line).
+// CPT > 0: the row's K / 256 <= CPT chunks per thread stay in registers
+// between the maximum and the conversion; CPT == 0: x is read twice.
+template <typename InT, int CPT>
+__global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale, int m,
+                                                         int k) {
+  const int t = threadIdx.x, q = t & 31;
+  const int row = blockIdx.x * 8 + (t >> 5);
+  const bool live = row < m;
+  const int nb = k >> 8, cpt = k >> 8;
+  const InT* xr = x + (size_t)(live ? row : 0) * k;
+  float v[CPT > 0 ? CPT : 1][8];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < (CPT > 0 ? CPT : 1); ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[j][i] = 0.0f;
+  if (CPT > 0) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+      if (live && j < cpt)
+        load8(xr + (size_t)(q + 32 * j) * 8, v[j]);
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        mx = fmaxf(mx, fabsf(v[j][i]));
+  } else if (live) {
+    for (int j = 0; j < cpt; ++j) {
+      float w[8];
+      load8(xr + (size_t)(q + 32 * j) * 8, w);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        mx = fmaxf(mx, fabsf(w[i]));
+    }
+  }
+  // Row maximum: lanes 0..31 and 32..63 of a wave are two rows.
+  mx = fmaxf(mx, dpp_f<kDppQuadSwap1>(mx));
+  mx = fmaxf(mx, dpp_f<kDppQuadSwap2>(mx));
+  mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
+  mx = fmaxf(mx, dpp_f<kDppRowMirror>(mx));
+  {
+    const int b = __builtin_bit_cast(int, mx);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    mx = (t & 63) < 32 ? fmaxf(r0, r1) : fmaxf(r2, r3);
+  }
+  float up = 1.0f, down = 1.0f;
+  if (mx > 0.0f && mx <= FLT_MAX) {
+    int e;
+    frexpf(mx, &e);
+    e = e < -80 ? -80 : e;
+    up = ldexpf(1.0f, 15 - e);
+    down = ldexpf(1.0f, e - 15);
+  }
+  if (!live)
+    return;
+  if (q == 0)
+    rowscale[row] = down;
+  auto put = [&](int j, const float* w) {
+    h8_t h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      h[i] = (_Float16)(w[i] * up);
+    *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, q + 32 * j, nb)) = h;
+  };
+  if (CPT > 0) {
+#pragma unroll
+    for (int j = 0; j < (CPT > 0 ? CPT : 1); ++j)
+      if (j < cpt)
+        put(j, v[j]);
+  } else {
+    for (int j = 0; j < cpt; ++j) {
+      float w[8];
+      load8(xr + (size_t)(q + 32 * j) * 8, w);
+      put(j, w);
+    }
+  }
+}
+
 template <typename InT>
 __global__ __launch_bounds__(64) void stage_pack_kernel(const InT* __restrict__ x, u4_t* __restrict__ frag, h4_t* __restrict__ xs,
                                                         float* __restrict__ dsc, int m, int k) {
@@ -1712,8 +1797,12 @@ hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs,
     (void)dispatch(stage_x_kernel<InT, kStageRowMajor>, grid, block, s, x, xo, xs, rowscale, m, k);
   else if (mode == kStageFrag)
     (void)dispatch(stage_x_kernel<InT, kStageFrag>, grid, block, s, x, xo, xs, rowscale, m, k);
-  else if (mode == kStageGemm)
+  else if (mode == kStageGemm && m < 2048)  // fewer than 256 workgroups of 8 rows: one row each
     (void)dispatch(stage_x_kernel<InT, kStageGemm>, grid, block, s, x, xo, xs, rowscale, m, k);
+  else if (mode == kStageGemm && k / 256 <= 16)
+    (void)dispatch(stage_gemm_kernel<InT, 16>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k);
+  else if (mode == kStageGemm)
+    (void)dispatch(stage_gemm_kernel<InT, 0>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k);
   else
     (void)dispatch(stage_x_kernel<InT, kStageFragSplit>, grid, block, s, x, xo, xs, rowscale, m, k);
   return hipGetLastError();

@@ -242,3 +242,24 @@ def test_gather_rows(q4k, gpu):
     assert rows == 8
     last = np.cumsum(lengths) - 1
     assert torch.equal(out, x[torch.as_tensor(last, device=gpu)])
+
+
+@pytest.mark.parametrize("m,k,dtype", [(2051, 4096, torch.float16), (2050, 12288, torch.float32)])
+def test_gemm_eight_row_staging(q4k, oracle, gpu, m, k, dtype):
+    """m >= 2048 stages x eight rows per workgroup: in registers for K <= 4096,
+    in two passes over x beyond.  A ragged last workgroup (rows past m) and
+    fp16 input; rows are checked on a subset that includes the last ones."""
+    n = 256
+    rng = np.random.default_rng(2000 + k)
+    w = make_q4k(rng, n, k)
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    x = make_x(rng, m, k).astype(npdt)
+    x[5] *= 1e-3  # a row whose scale differs from its neighbours'
+    W = q4k.Weight(w, n, k)
+    y = torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+    q4k.linear(_t(x, gpu, dtype), W, m, y, query_counts=[m])
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.arange(8), np.random.default_rng(3).choice(m, 40, replace=False), np.arange(m - 8, m)])
+    got = y.float().cpu().numpy()[rows]
+    assert np.all(np.isfinite(got))
+    assert row_rel_err(got, oracle.linear(x[rows], w, n, k)) <= TOL
