@@ -137,6 +137,47 @@ def decode_bench(args, dev):
     }
 
 
+def shard_bench(args, dev):
+    """One GPU's share of the config-1 MLP if it were sharded 8 ways (gate/up
+    column-parallel over N, down row-parallel over K): the fused gate/up at
+    N = 1536 and the down projection at K = 1536, weights rotating over
+    args.sets copies, kernel times from dispatch-attached events."""
+    import numpy as np
+    import torch
+    import mtlqwen_amd as q4k
+
+    M, K, N, S = 8, 4096, 12288, 8
+    rng = np.random.default_rng(0x51A70008)
+    raw = [torch.from_numpy(make_q4k(rng, n, k)).to(dev) for n, k in ((N // S, K), (N // S, K), (K, N // S))]
+    sets = [[q4k.Weight(raw[i], *shape) for i, shape in enumerate(((N // S, K), (N // S, K), (K, N // S)))]
+            for _ in range(args.sets)]
+    x = torch.randn(M, K, device=dev) * 0.5
+    gate = torch.empty(M, N // S, device=dev)
+    part = torch.empty(M, K, device=dev)
+    counts = [1] * M
+    for i in range(2 * len(sets)):
+        G, U, D = sets[i % len(sets)]
+        q4k.mlp_gate_up(x, G, U, M, gate, query_counts=counts)
+        q4k.linear(gate, D, M, part, query_counts=counts)
+    torch.cuda.synchronize()
+    q4k.profile_enable(True)
+    for i in range(args.steps):
+        G, U, D = sets[i % len(sets)]
+        q4k.mlp_gate_up(x, G, U, M, gate, query_counts=counts)
+        q4k.linear(gate, D, M, part, query_counts=counts)
+    torch.cuda.synchronize()
+    gu_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMV_GATED)
+    dn_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMV)
+    q4k.profile_enable(False)
+    gu_bytes = 2 * q4k_bytes(N // S, K) + 4 * (M * K + M * N // S)
+    dn_bytes = q4k_bytes(K, N // S) + 4 * (M * N // S + M * K)
+    return {
+        "workload": "config1 MLP, one GPU's share of an 8-way shard: fused gate/up 4096->1536 x2, down 1536->4096 (partial sums)",
+        "gate_up_us": round(gu_ms * 1e3, 3), "gate_up_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+        "down_us": round(dn_ms * 1e3, 3), "down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
+    }
+
+
 def prefill_bench(args, dev):
     import numpy as np
     import torch
@@ -231,9 +272,38 @@ def cpu_baseline(args):
             break
     dt = (time.perf_counter() - t0) / iters
     step_bytes = 2 * q4k_bytes(N, K) + q4k_bytes(K, N) + 4 * (M * K + M * N) + 4 * (M * N + 2 * M * K)
+
+    def timed(fn, budget):
+        n, t1 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            if time.perf_counter() - t1 >= budget:
+                return (time.perf_counter() - t1) / n, n
+
+    # The other headline configs, on bounded samples (a quarter of the budget each).
+    w0 = make_q4k(rng, 4096, 4096)
+    x0 = rng.standard_normal((1, 4096)).astype(np.float32)
+    dt0, n0 = timed(lambda: oracle.linear(x0, w0, 4096, 4096, threads=threads), args.cpu_seconds / 4)
+    rows4 = 16  # config 4 (M=2048) is timed on 16 of its token rows and reported per token
+    x4 = rng.standard_normal((rows4, K)).astype(np.float32)
+
+    def mlp4():
+        g4 = oracle.mlp_gate_up(x4, wg, wu, N, K, threads=threads)
+        oracle.linear(g4, wd, K, N, threads=threads)
+
+    dt4, n4 = timed(mlp4, args.cpu_seconds / 4)
+    flop_tok = 3 * 2.0 * N * K
     return {"value": step_bytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{iters} config-1 MLP steps (M=8, gate/up 4096->12288 x2 + down 12288->4096) "
-                      f"in {dt * iters:.1f} s, {dt * 1e3:.1f} ms/step"}
+                      f"in {dt * iters:.1f} s, {dt * 1e3:.1f} ms/step",
+            "configs": {
+                "config0_gbs": round((q4k_bytes(4096, 4096) + 4 * (4096 + 4096)) / dt0 / 1e9, 3),
+                "config0_sample": f"{n0} single linears M=1 K=N=4096, {dt0 * 1e3:.2f} ms each",
+                "config4_ms_per_token": round(dt4 / rows4 * 1e3, 3),
+                "config4_tflops": round(rows4 * flop_tok / dt4 / 1e12, 4),
+                "config4_sample": f"{n4} MLP passes over {rows4} token rows (gate/up + down), {dt4 * 1e3:.1f} ms each",
+            }}
 
 
 def main():
@@ -244,12 +314,14 @@ def main():
                                    "(a column/row-parallel design is described in DESIGN.md); run with --gpus 1"}))
         sys.exit(2)
     import torch
-    import mtlqwen_amd  # noqa: F401  (fails loudly if libq4k.so is missing)
+    import mtlqwen_amd  # fails loudly if libq4k.so is missing
     dev = torch.device("cuda:0")
 
     dec = decode_bench(args, dev)
     pre = None if args.no_prefill else prefill_bench(args, dev)
+    shard = shard_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
+    mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
 
     g = dec["gated"]
@@ -288,7 +360,9 @@ def main():
             "down_gemv_gbs": round(dec["down"]["gbs"], 1),
             "stage_us": round(dec["stage_avg_us"], 3),
         },
+        "shard_1of8": shard,
         "copy_ceiling_gbs": round(copy_gbs, 1),
+        "mfma_ceiling_tflops": round(mfma_tf, 1),
         "cpu_baseline": cpu,
     }
     if pre:

@@ -138,6 +138,14 @@ int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const ui
 int q4k_profile_enable(int on);
 int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, double* min_ms, double* max_ms);
 
+/* Measured fp16 MFMA ceiling of the device (no counterpart in the reference;
+ * bench.py records it beside the published peak).  Runs a loop of the GEMM's
+ * MFMA instruction, v_mfma_f32_16x16x32_f16, on every CU (one wave per SIMD,
+ * operands in registers) for about `iters` x 32 instructions per wave, and
+ * returns the achieved dense FLOP rate in TFLOP/s.  Synchronises the stream;
+ * allocates and frees a small device buffer. */
+int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops);
+
 /* The device layout as a host transform (for tests and tooling):
  * GGUF-order block_q4_K bytes <-> the kernels' tiled order.  Both buffers are
  * n * (k / 256) * 144 bytes. */

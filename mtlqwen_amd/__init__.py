@@ -1,20 +1,20 @@
 """MI355X-native (gfx950) Q4_K quantized linear() path of MTLQwen.
 
-Hand-written HIP kernels behind a C ABI (include/q4k.h, libq4k.so): an MFMA
-GEMV for decode-shaped batches (<= 48 packed rows), an LDS-tiled MFMA GEMM
+Hand-written HIP kernels behind a C ABI (include/q4k.h, libq4k.so): MFMA
+GEMVs for decode-shaped batches (<= 48 packed rows), a pipelined MFMA GEMM
 for prefill, the fused gate/up MLP, and the reference's phase selection over
 a packed ragged batch.
 """
 from ._lib import DTYPE_F16, DTYPE_F32, GGML_TYPE_Q4_K, PHASE_DECODE, PHASE_GATED_DECODE, PHASE_PREFILL, \
     PHASE_PREFILL_SMALL, POST_ADD, POST_GATE, POST_STORE, KERNEL_STAGE, KERNEL_GEMV, KERNEL_GEMV_GATED, KERNEL_GEMM, \
     Q4KError, lib
-from .linear import (PHASE_NAMES, Weight, gather_rows, linear, mlp, mlp_gate_up, pack_queries, profile_enable,
-                     profile_query, q4k_nbytes, relayout_host, select_phase, unrelayout_host)
+from .linear import (PHASE_NAMES, Weight, gather_rows, linear, mfma_ceiling, mlp, mlp_gate_up, pack_queries,
+                     profile_enable, profile_query, q4k_nbytes, relayout_host, select_phase, unrelayout_host)
 
 __all__ = [
     "Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "relayout_host",
     "unrelayout_host", "q4k_nbytes", "Q4KError", "lib", "PHASE_NAMES", "DTYPE_F32", "DTYPE_F16", "GGML_TYPE_Q4_K",
     "POST_STORE", "POST_ADD", "POST_GATE", "PHASE_DECODE", "PHASE_PREFILL", "PHASE_PREFILL_SMALL",
     "PHASE_GATED_DECODE", "KERNEL_STAGE", "KERNEL_GEMV", "KERNEL_GEMV_GATED", "KERNEL_GEMM", "profile_enable",
-    "profile_query"
+    "profile_query", "mfma_ceiling"
 ]

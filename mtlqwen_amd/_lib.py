@@ -59,6 +59,7 @@ def _load():
         "q4k_profile_enable": (c_int, [c_int]),
         "q4k_profile_query": (c_int, [u32, pu32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_double)]),
+        "q4k_mfma_ceiling": (c_int, [p, c_int, u32, ctypes.POINTER(ctypes.c_double)]),
         "q4k_relayout_host": (c_int, [p, p, u32, u32]),
         "q4k_unrelayout_host": (c_int, [p, p, u32, u32]),
     }

@@ -695,6 +695,45 @@ int q4k_profile_enable(int on) {
   return Q4K_OK;
 }
 
+int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops) {
+  if (!tflops || iters == 0)
+    return fail(Q4K_EINVAL, "tflops must be non-NULL and iters positive");
+  int rc = set_device(device);
+  if (rc)
+    return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int blocks = device_cus(device);
+  float* out = nullptr;
+  Q4K_TRY_HIP(hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)), "hipMalloc");
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t err = hipEventCreate(&e0);
+  if (err == hipSuccess)
+    err = hipEventCreate(&e1);
+  if (err == hipSuccess)
+    err = launch_mfma_ceiling(s, out, blocks, (int)(iters < 64 ? iters : 64));  // warm-up
+  if (err == hipSuccess)
+    err = hipEventRecord(e0, s);
+  if (err == hipSuccess)
+    err = launch_mfma_ceiling(s, out, blocks, (int)iters);
+  if (err == hipSuccess)
+    err = hipEventRecord(e1, s);
+  if (err == hipSuccess)
+    err = hipEventSynchronize(e1);
+  float ms = 0.0f;
+  if (err == hipSuccess)
+    err = hipEventElapsedTime(&ms, e0, e1);
+  if (e0)
+    (void)hipEventDestroy(e0);
+  if (e1)
+    (void)hipEventDestroy(e1);
+  (void)hipFree(out);
+  if (err != hipSuccess)
+    return fail(Q4K_EHIP, "mfma ceiling: %s", hipGetErrorString(err));
+  const double flop = 2.0 * 16 * 16 * 32 * 32.0 * iters * 4.0 * blocks;
+  *tflops = ms > 0.0f ? flop / (ms * 1e-3) / 1e12 : 0.0;
+  return Q4K_OK;
+}
+
 int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, double* min_ms, double* max_ms) {
   if (kernel > 3)
     return fail(Q4K_EINVAL, "kernel family %u out of range", kernel);

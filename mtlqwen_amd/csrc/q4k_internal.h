@@ -142,6 +142,10 @@ bool gemm2_supported(int m, int n);
 int gemm2_rows(int m);
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype);
 
+// One MFMA-ceiling launch: `blocks` workgroups of 4 waves, each wave issuing
+// 32 * iters v_mfma_f32_16x16x32_f16 (16384 FLOP each); out holds blocks * 256 floats.
+hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters);
+
 hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx);
 
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).

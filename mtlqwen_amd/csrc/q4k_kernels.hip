@@ -1583,6 +1583,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // ----------------------------------------------------------------------------
+// Measured MFMA ceiling: the GEMM's instruction (v_mfma_f32_16x16x32_f16) back
+// to back, 32 independent accumulators per wave, one wave per SIMD, operands
+// in registers -- the rate a kernel of this instruction can reach on the box
+// (clock under a dense MFMA load included).  The result is stored so that
+// nothing is dead; its value is meaningless.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void mfma_ceiling_kernel(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  f4_t acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    acc[i] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    asm volatile("" : "+a"(acc[i]));
+  }
+  h8_t a0, a1, b0, b1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a0[i] = (_Float16)(0.001f * (float)(lane + i));
+    a1[i] = (_Float16)(0.002f * (float)(lane - i));
+    b0[i] = (_Float16)(0.003f * (float)(i - lane));
+    b1[i] = (_Float16)(0.004f * (float)(i + 1));
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i & 1 ? a1 : a0, i & 2 ? b1 : b0, acc[i], 0, 0, 0);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    asm volatile("" : "+a"(acc[i]));
+    sum += acc[i][0] + acc[i][3];
+  }
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = sum;
+}
+
+// ----------------------------------------------------------------------------
 // Row gather and device re-layout.
 // ----------------------------------------------------------------------------
 template <typename T>
@@ -1862,6 +1899,11 @@ bool gemm2_supported(int m, int n) {
 
 int gemm2_rows(int m) {
   return (m + kG2M - 1) / kG2M * kG2M;
+}
+
+hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters) {
+  hipLaunchKernelGGL(mfma_ceiling_kernel, dim3((unsigned)blocks), dim3(256), 0, s, out, iters);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype) {

@@ -181,6 +181,14 @@ def profile_query(kernel):
     return n.value, tot.value, lo.value, hi.value
 
 
+def mfma_ceiling(device=0, iters=20000, stream=None):
+    """Measured fp16 MFMA rate of the device in TFLOP/s (a loop of the GEMM's
+    MFMA instruction on every CU); synchronises the stream."""
+    t = ctypes.c_double()
+    check(lib.q4k_mfma_ceiling(_stream(stream), int(device), int(iters), ctypes.byref(t)))
+    return t.value
+
+
 def relayout_host(gguf, n, k):
     src = np.ascontiguousarray(gguf, dtype=np.uint8).reshape(-1)
     dst = np.empty_like(src)
@@ -196,5 +204,5 @@ def unrelayout_host(tiled, n, k):
 
 
 __all__ = ["Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "relayout_host",
-           "profile_enable", "profile_query",
+           "profile_enable", "profile_query", "mfma_ceiling",
            "unrelayout_host", "q4k_nbytes", "Q4KError", "PHASE_NAMES"]

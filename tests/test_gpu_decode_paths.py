@@ -123,3 +123,21 @@ def test_decode_rows_of_extreme_magnitude(q4k, oracle, gpu):
         got = y.cpu().numpy()
         assert np.all(got[2] == 0)
         assert row_rel_err(got, ref) <= TOL
+
+
+def test_shard_shapes(q4k, oracle, gpu):
+    """One GPU's share of the config-1 MLP sharded 8 ways: gate/up N = 1536
+    (column-parallel), down K = 1536 (row-parallel, partial sums)."""
+    m, k, n = 8, 4096, 1536
+    rng = np.random.default_rng(1600)
+    wg, wu, wd = make_q4k(rng, n, k), make_q4k(rng, n, k), make_q4k(rng, k, n)
+    x = make_x(rng, m, k, 0.5)
+    G, U, D = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k), q4k.Weight(wd, k, n)
+    g = torch.empty((m, n), device=gpu)
+    q4k.mlp_gate_up(_t(x, gpu), G, U, m, g, query_counts=[1] * m)
+    y = torch.empty((m, k), device=gpu)
+    q4k.linear(g, D, m, y, query_counts=[1] * m)
+    torch.cuda.synchronize()
+    gn = g.cpu().numpy()
+    assert row_rel_err(gn, oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
+    assert row_rel_err(y.cpu().numpy(), oracle.linear(gn, wd, k, n)) <= TOL

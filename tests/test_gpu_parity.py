@@ -263,3 +263,9 @@ def test_gemm_eight_row_staging(q4k, oracle, gpu, m, k, dtype):
     got = y.float().cpu().numpy()[rows]
     assert np.all(np.isfinite(got))
     assert row_rel_err(got, oracle.linear(x[rows], w, n, k)) <= TOL
+
+
+def test_mfma_ceiling(q4k, gpu):
+    """The measured MFMA ceiling is positive and below the published dense peak."""
+    tf = q4k.mfma_ceiling(0, iters=2000)
+    assert 100.0 < tf < 2600.0
