@@ -443,7 +443,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.post = (int)post;
     LaunchTimer timer(stream, Q4K_KERNEL_GEMM);
     if (gemm2)
-      Q4K_TRY_HIP(launch_gemm2(stream, a, (int)dtype), "gemm launch");
+      Q4K_TRY_HIP(launch_gemm2(stream, a, (int)dtype, device_cus(w->device)), "gemm launch");
     else
       Q4K_TRY_HIP(launch_gemm(stream, a, (int)dtype), "gemm launch");
   }

@@ -140,7 +140,7 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype);
 // (kStageGemm) for gemm2_rows(m) rows; N a multiple of 256.
 bool gemm2_supported(int m, int n);
 int gemm2_rows(int m);
-hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype);
+hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus);
 
 // One MFMA-ceiling launch: `blocks` workgroups of 4 waves, each wave issuing
 // 32 * iters v_mfma_f32_16x16x32_f16 (16384 FLOP each); out holds blocks * 256 floats.

@@ -1379,15 +1379,15 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
   }
 }
 
+// One 128 x 256 output tile (column block bx, row block by).
 template <typename OutT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
+__device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int bx, int by) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
   const int nb = a.nb, steps = 4 * nb;
-  const int mt0 = blockIdx.y * (kG2M / 16);                 // first row tile
-  const int ct0 = blockIdx.x * (kG2N / 16) + 4 * wave;      // this wave's first column tile
+  const int mt0 = by * (kG2M / 16);                         // first row tile
+  const int ct0 = bx * (kG2N / 16) + 4 * wave;              // this wave's first column tile
   const uint32_t aring = lds_addr(lds);
   uint8_t* const bring = lds + kG2AS * kG2ASlot + wave * kG2BWave;
   const uint32_t bring0 = lds_addr(bring);
@@ -1400,7 +1400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int tc = t < steps ? t : steps - 1;
     const int b = tc >> 2, u = tc & 3;
     const int f = 4 * wave + i;
-    const _Float16* src = xh + ((((size_t)blockIdx.y * nb + b) * 4 + u) * 16 + f) * 512;
+    const _Float16* src = xh + ((((size_t)by * nb + b) * 4 + u) * 16 + f) * 512;
     const uint32_t l = __builtin_amdgcn_readfirstlane(aring + (uint32_t)(t % kG2AS) * kG2ASlot + (uint32_t)f * 1024);
     lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
   };
@@ -1580,6 +1580,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     full ? gemm2_epilogue<OutT, 1, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 1, false>(a, acc, mt0, ct0, lane);
   else
     full ? gemm2_epilogue<OutT, 2, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 2, false>(a, acc, mt0, ct0, lane);
+}
+
+// Persistent launch: workgroup b takes tiles b, b + grid, ... in the order of
+// a (column block, row block) grid with the column block fastest, so that
+// tile t runs on XCD t % 8 as it would in a one-tile-per-workgroup launch.
+// Consecutive tiles of a workgroup reuse its LDS rings; a barrier separates
+// the last reads of one tile from the first loads of the next.
+template <typename OutT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a, int tiles_x, int tiles) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    if (tile != (int)blockIdx.x)
+      __syncthreads();
+    gemm2_tile<OutT>(a, lds, tile % tiles_x, tile / tiles_x);
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -1906,12 +1921,15 @@ hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters)
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype) {
-  const dim3 grid((unsigned)(a.n / kG2N), (unsigned)((a.m + kG2M - 1) / kG2M)), block(256);
+hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
+  const int tiles_x = a.n / kG2N, tiles = tiles_x * ((a.m + kG2M - 1) / kG2M);
+  static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);
+  const int grid = persist && tiles > cus ? cus : tiles;
+  const dim3 block(256);
   if (dtype == kF32)
-    (void)dispatch(q4k_gemm2_kernel<float>, grid, block, s, a);
+    (void)dispatch(q4k_gemm2_kernel<float>, dim3((unsigned)grid), block, s, a, tiles_x, tiles);
   else
-    (void)dispatch(q4k_gemm2_kernel<_Float16>, grid, block, s, a);
+    (void)dispatch(q4k_gemm2_kernel<_Float16>, dim3((unsigned)grid), block, s, a, tiles_x, tiles);
   return hipGetLastError();
 }
 
