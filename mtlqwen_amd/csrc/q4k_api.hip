@@ -377,6 +377,23 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     Q4K_TRY_HIP(launch_gemv_splitk(stream, a, (int)dtype, plan, ws.part, ws.counters), "gemv split-K launch");
     return Q4K_OK;
   }
+  if (gemv && wu && gemv_gate_up_supported((int)m, (int)(w->k / 256), (int)w->n)) {
+    // Fused gate/up GEMV: packs x in registers, no staging launch.
+    GemvArgs a{};
+    a.w = w->data;
+    a.wu = wu->data;
+    a.x = x;
+    a.y = y;
+    a.m = (int)m;
+    a.n = (int)w->n;
+    a.k = (int)w->k;
+    a.nb = (int)(w->k / 256);
+    a.rows = 2 * (int)m;
+    a.split = 1;
+    LaunchTimer timer(stream, Q4K_KERNEL_GEMV_GATED);
+    Q4K_TRY_HIP(launch_gemv_gate_up(stream, a, (int)dtype, device_cus(w->device)), "gemv gate/up launch");
+    return Q4K_OK;
+  }
   if (gemv && split && gemv_stream_supported(rows, (int)(w->k / 256), (int)w->n, wu != nullptr, device_cus(w->device))) {
     GemvArgs a{};
     int rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);

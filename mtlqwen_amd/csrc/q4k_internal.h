@@ -120,6 +120,11 @@ GemvShape gemv_shape(int rows, int n, int nb, bool gated);
 bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus);
 hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus);
 
+// Fused gate/up GEMV for m <= 8 rows and K = 4096 that packs x itself (no
+// staging launch); reads a.x, a.w, a.wu and writes a.y.
+bool gemv_gate_up_supported(int m, int nb, int n);
+hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus);
+
 // Split-K GEMV for m <= 8 (see q4k_gemv_splitk_kernel): a plan picks an
 // instance for (n, nb); the launch needs `part` (gemv_splitk_part_floats
 // floats) and `counters` (plan.groups ints, zero before the first launch;

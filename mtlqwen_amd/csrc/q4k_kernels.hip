@@ -957,6 +957,266 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int
 }
 
 // ----------------------------------------------------------------------------
+// Fused gate/up GEMV with in-register activation packing (m <= 8 rows, K =
+// 4096, N = 16 T x workgroups: one item of T column tiles per workgroup).
+//
+// Wave w owns K-blocks bw, bw + 1 (bw = 2 ((w + b) % 8), rotated so that the
+// workgroups of one L2 read different parts of x first) of the workgroup's T
+// column tiles of both matrices: U = 4T tile-blocks ("units").  It loads its
+// two blocks of x (one coalesced 1 KB load per (block, row)), then keeps two
+// units in flight ahead of the one it computes (per unit one header dword and
+// the two quant slabs, 16 B per lane).  No staging launch precedes it: while
+// the first units are in flight the wave turns its blocks of x into the MFMA
+// operands in registers, with the same arithmetic as the decode pack
+// (pack_block_row):
+//  - x passes through LDS so that lane 16g + i holds elements
+//    64g + 32 (i / 8) + [0, 32) of row i % 8 (rows >= m read as zero);
+//  - each (row, block) is scaled by a power of two that puts its largest
+//    magnitude in [2^14, 2^15) and split into hi = h(t), lo = h(t - hi);
+//  - lanes i and i ^ 8 (one DPP row rotation) trade halves so that lanes
+//    i < 8 hold the high parts of elements 64g + [0, 64) of row i and lanes
+//    i >= 8 the low parts: the A fragments of v_mfma_f32_16x16x32_f16, rows
+//    8..15 carrying the low parts;
+//  - each lane's 32 elements are one sub-block; their sums / 32 (hi / lo)
+//    are gathered into the min-term operand of v_mfma_f32_16x16x16_f16.
+// Per unit the header's 16 bytes of this lane's column come from the four
+// lanes that loaded them (ds_bpermute).  The partial sums of a unit are
+// unscaled and accumulated in registers; hi and lo rows are combined (lanes
+// l, l + 32) and the eight waves' sums are added in wave order through LDS
+// before the SiLU(gate) * up epilogue.
+// ----------------------------------------------------------------------------
+constexpr int kDppRowRor8 = 0x128;  // lane i <- lane (i + 8) % 16 within 16 lanes
+
+template <int BANKS>
+__device__ __forceinline__ uint32_t ror8_into(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, kDppRowRor8, 0xF, BANKS, false);
+}
+
+// Registers of one packed x block: A fragments, min-term operand and the
+// unscale factors of this lane's C rows (4g + v) & 7.
+struct XBlock {
+  h8_t frag[8];
+  h4_t xs;
+  float dv[4];
+};
+
+// Converts the 32 values t0 (elements 64g + 32 (i / 8) + [0, 32) of row i % 8,
+// lane 16g + i) of one block into the block's operands.
+__device__ __forceinline__ void pack_x_regs(const float (&xv)[32], int lane, XBlock& xb) {
+  const int g = lane >> 4, i = lane & 15, half = i >> 3;
+  // Largest magnitude of the (row, block): own 32, the partner half, the four
+  // lane groups.
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e)
+    mx = fmaxf(mx, fabsf(xv[e]));
+  mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), kDppRowRor8, 0xF, 0xF, false)));
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float up = 1.0f, down = 1.0f;
+  if (mx > 0.0f && mx <= FLT_MAX) {
+    int ex;
+    frexpf(mx, &ex);
+    ex = ex < -80 ? -80 : ex;
+    up = ldexpf(1.0f, 15 - ex);
+    down = ldexpf(1.0f, ex - 15);
+  }
+  uint32_t hw[16], lw[16];
+  float sum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const float t0 = xv[2 * v] * up, t1 = xv[2 * v + 1] * up;
+    sum += t0 + t1;
+    const h2_t h = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(t0, t1));
+    hw[v] = __builtin_bit_cast(uint32_t, h);
+    lw[v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(t0 - (float)h[0], t1 - (float)h[1]));
+  }
+  // Fragments 0..3 (elements 64g + [0, 32)): own high parts in lanes i < 8,
+  // the partner's low parts in lanes i >= 8 (banks 2, 3 take the rotation).
+  // Fragments 4..7 (64g + [32, 64)): the partner's high parts in lanes i < 8,
+  // own low parts in lanes i >= 8.
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    u4_t f0, f1;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      f0[v] = ror8_into<0xC>(hw[4 * s + v], lw[4 * s + v]);
+      f1[v] = ror8_into<0x3>(lw[4 * s + v], hw[4 * s + v]);
+    }
+    xb.frag[s] = __builtin_bit_cast(h8_t, f0);
+    xb.frag[4 + s] = __builtin_bit_cast(h8_t, f1);
+  }
+  // Sub-block sums / 32 as (hi, lo) halves; lane 16G + r (G < 2) gathers
+  // sub-blocks 4G + c (c = 0..3) of row r % 8 from lanes 16 (2G + c / 2) +
+  // r % 8 + 8 (c % 2), taking the high halves for r < 8 and the low for r >= 8.
+  const float s32 = sum * 0.03125f;
+  const _Float16 sh = (_Float16)s32;
+  const _Float16 sl = (_Float16)(s32 - (float)sh);
+  const uint32_t shl = (uint32_t)__builtin_bit_cast(uint16_t, sh) | ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
+  const int G = g & 1, r8 = i & 7;
+  uint32_t got[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    got[c] = (uint32_t)__shfl((int)shl, 16 * (2 * G + (c >> 1)) + r8 + 8 * (c & 1));
+  const uint32_t sel = half ? 0x07060302u : 0x05040100u;  // low or high halves of a pair of dwords
+  const uint32_t x01 = __builtin_amdgcn_perm(got[1], got[0], sel), x23 = __builtin_amdgcn_perm(got[3], got[2], sel);
+  xb.xs = g < 2 ? __builtin_bit_cast(h4_t, uint2{x01, x23}) : h4_t{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+  // Unscale factors of C rows 4 (g & 1) + v (the same in every lane of a row).
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float d0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, down), v));
+    const float d1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, down), 4 + v));
+    xb.dv[v] = (g & 1) ? d1 : d0;
+  }
+}
+
+template <int T, typename OutT>
+__global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
+  constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT;
+  // x of wave w, re-ordered for the register pack: [block][lane][32 + 4]
+  // floats (the 4-float pad makes the 16-byte reads of 16 lanes hit 64
+  // distinct banks).  The partial sums reuse the wave's own region at the end.
+  constexpr int kXRow = 36;
+  static_assert(MT * 8 * 16 <= BPW * 64 * kXRow, "partials fit the x region");
+  __shared__ __attribute__((aligned(16))) float xl[W][BPW * 64 * kXRow];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int item = blockIdx.x;
+  const int nb = a.nb, bw = ((wave + item) % W) * BPW;
+  const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
+
+  // x: one coalesced load per (block, row), lane l holding elements
+  // 4l..4l+3 (rows >= m read row 0 and are zeroed below).
+  float xv[BPW][8][4];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const OutT* p = reinterpret_cast<const OutT*>(a.x) + (size_t)(r < a.m ? r : 0) * a.k + (size_t)(bw + j) * 256 + 4 * lane;
+      if (sizeof(OutT) == 4) {
+        const f4_t v4 = *reinterpret_cast<const f4_t*>(p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[j][r][e] = v4[e];
+      } else {
+        const h4_t v4 = *reinterpret_cast<const h4_t*>(p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[j][r][e] = (float)v4[e];
+      }
+    }
+  // Units are loaded into registers DQ ahead of the one being computed
+  // (header dword, then the two quant slabs; the scheduling barriers keep
+  // the issue order: x first, then unit by unit).  A shallow window keeps
+  // the memory queues short, so x and each wave's next unit arrive early;
+  // issuing every unit at once measured slower (the whole item's requests
+  // queue ahead of x).
+  constexpr int DQ = 2;
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t hw[U];
+  u4_t q0[U], q1[U];
+  auto issue_unit = [&](int u) {
+    const int j = u / MT, mt = u - j * MT, mi = mt / T, t = mt - mi * T;
+    const uint8_t* src = (mi ? a.wu : a.w) + ((size_t)item * T + t) * tile_bytes + (size_t)(bw + j) * kTileBlockBytes;
+    hw[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kHeaderOffset) + lane);
+    q0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    q1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int u = 0; u < (DQ < U ? DQ : U); ++u)
+    issue_unit(u);
+
+  // Element e = 4 lane of row r goes to pack lane 16 (e / 64) + r + 8 ((e / 32) & 1),
+  // float (e & 31) of its 32.
+  float* const xw = xl[wave];
+  const int dl = 16 * (lane >> 4) + 8 * ((lane >> 3) & 1), doff = 4 * (lane & 7);
+#pragma unroll
+  for (int j = 0; j < BPW; ++j)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      f4_t v4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v4[e] = r < a.m ? xv[j][r][e] : 0.0f;
+      *reinterpret_cast<f4_t*>(xw + (j * 64 + dl + r) * kXRow + doff) = v4;
+    }
+  XBlock xb[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    float t32[32];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const f4_t v4 = *reinterpret_cast<const f4_t*>(xw + (j * 64 + lane) * kXRow + 4 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        t32[4 * c + e] = v4[e];
+    }
+    pack_x_regs(t32, lane, xb[j]);
+  }
+
+  f4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    acc[mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = u / MT, mt = u - j * MT;
+    __builtin_amdgcn_sched_barrier(0);
+    if (u + DQ < U)
+      issue_unit(u + DQ);
+    u4_t hd;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      hd[w] = (uint32_t)__shfl((int)hw[u], 4 * col + w);
+    const BlockConsts kc = block_consts(hd, g);
+    f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u4_t qq = s < 2 ? q0[u] : q1[u];
+      const uint32_t wa = qq[2 * (s & 1)], wb = qq[2 * (s & 1) + 1];
+      const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+      const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+      cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[j].frag[s], blo, cl, 0, 0, 0);
+      ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[j].frag[4 + s], bhi, ch, 0, 0, 0);
+    }
+    const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xb[j].xs, kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      acc[mt][v] += fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * xb[j].dv[v];
+  }
+
+  // C row 4g + v: lanes g < 2 add the low part held 32 lanes up; the
+  // wave's partials [mt][row][col] go to its own x region.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float tot = acc[mt][v] + __shfl_xor(acc[mt][v], 32);
+      if (g < 2)
+        xw[(mt * 8 + 4 * g + v) * 16 + col] = tot;
+    }
+  __syncthreads();
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  constexpr int EPI = 16 * T;
+  for (int o = tid; o < a.m * EPI; o += 64 * W) {
+    const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
+    float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      gv += xl[w][(t * 8 + row) * 16 + cc];
+      uv += xl[w][((T + t) * 8 + row) * 16 + cc];
+    }
+    if (sizeof(OutT) == 2) {
+      gv = round_half(gv);
+      uv = round_half(uv);
+    }
+    store_elem(y, (size_t)row * a.n + ((size_t)item * T + t) * 16 + cc, silu(gv) * uv);
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Split-K GEMV (m <= 8 rows, split hi/lo into one 16-row activation tile as
 // in the streaming GEMV).
 //
@@ -1810,6 +2070,31 @@ size_t gemv_splitk_part_floats(const SplitkPlan& plan) {
 hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const SplitkPlan& plan, float* part, int* counters) {
   (void)plan.inst;  // one instance
   return splitk_launch<1, 8, 8, 6, 4>(s, a, dtype, plan.grid, part, counters);
+}
+
+bool gemv_gate_up_supported(int m, int nb, int n) {
+  static const bool enabled = env_int("Q4K_GEMV_GATE_UP", 1) != 0;
+  return enabled && m >= 1 && m <= 8 && nb == 16 && n % 16 == 0;
+}
+
+hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+  // Three column tiles per workgroup while that still gives every CU one
+  // workgroup (N = 12288: 256); otherwise one.
+  const int ctiles = a.n / 16;
+  const bool t3 = ctiles % 3 == 0 && ctiles / 3 >= cus;
+  const dim3 grid((unsigned)(t3 ? ctiles / 3 : ctiles)), block(512);
+  if (t3) {
+    if (dtype == kF32)
+      (void)dispatch(q4k_gemv_gate_up_kernel<3, float>, grid, block, s, a);
+    else
+      (void)dispatch(q4k_gemv_gate_up_kernel<3, _Float16>, grid, block, s, a);
+  } else {
+    if (dtype == kF32)
+      (void)dispatch(q4k_gemv_gate_up_kernel<1, float>, grid, block, s, a);
+    else
+      (void)dispatch(q4k_gemv_gate_up_kernel<1, _Float16>, grid, block, s, a);
+  }
+  return hipGetLastError();
 }
 
 bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus) {

@@ -1,11 +1,12 @@
-"""The decode kernels for m <= 8 rows (decode pack + streaming GEMV, decode
-pack + split-K GEMV) against the CPU oracle, over the row counts, dtypes and
-epilogues of a decode pass.  Shapes are chosen to reach each kernel:
+"""The decode kernels for m <= 8 rows (fused gate/up GEMV packing x in
+registers, split-K GEMV packing its K-slice in LDS, decode pack + streaming
+GEMV) against the CPU oracle, over the row counts, dtypes and epilogues of a
+decode pass.  Shapes are chosen to reach each kernel:
 
-  gated, K=4096, N=12288   streaming GEMV, 3 column tiles per item
-  gated, K=4096, N=512     streaming GEMV, 1 column tile per item
+  gated, K=4096, N=12288   fused gate/up GEMV, 3 column tiles per workgroup
+  gated, K=4096, N=512     fused gate/up GEMV, 1 column tile per workgroup
   plain, K=12288, N=1024   split-K GEMV (8 tiles x 8 K-slices of 6 blocks)
-  plain, K=4096, N=65536   streaming GEMV, 4 column tiles per item
+  plain, K=4096, N=65536   decode pack + streaming GEMV, 4 column tiles per item
 
 Bar: max row-relative error 1e-3 against the fp32-accumulated oracle.
 """
@@ -49,6 +50,23 @@ def test_gated_stream_f16(q4k, oracle, gpu):
     q4k.mlp_gate_up(_t(x, gpu, torch.float16), G, U, m, y, query_counts=[1] * m)
     torch.cuda.synchronize()
     assert row_rel_err(y.float().cpu().numpy(), oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
+
+
+@pytest.mark.parametrize("m,n", [(1, 12288), (5, 12288), (5, 256), (7, 48)])
+def test_gated_register_pack_f16(q4k, oracle, gpu, m, n):
+    """fp16 activations through both column-tile widths of the fused gate/up
+    GEMV, with row counts that leave dead rows in the register pack."""
+    k = 4096
+    rng = np.random.default_rng(1150 + m + n)
+    wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+    x = make_x(rng, m, k, 0.5).astype(np.float16)
+    G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+    y = torch.full((m, n), float("nan"), device=gpu, dtype=torch.float16)
+    q4k.mlp_gate_up(_t(x, gpu, torch.float16), G, U, m, y, query_counts=[1] * m)
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert row_rel_err(got, oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
 
 
 @pytest.mark.parametrize("m", [1, 5, 8])
