@@ -2069,7 +2069,9 @@ size_t gemv_splitk_part_floats(const SplitkPlan& plan) {
 
 hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const SplitkPlan& plan, float* part, int* counters) {
   (void)plan.inst;  // one instance
-  return splitk_launch<1, 8, 8, 6, 4>(s, a, dtype, plan.grid, part, counters);
+  // Two block-steps in flight per wave: measured faster than four (shorter
+  // memory queues, as for the fused gate/up GEMV).
+  return splitk_launch<1, 8, 8, 6, 2>(s, a, dtype, plan.grid, part, counters);
 }
 
 bool gemv_gate_up_supported(int m, int nb, int n) {
