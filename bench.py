@@ -178,6 +178,60 @@ def shard_bench(args, dev):
     }
 
 
+def neighbours_bench(args, dev):
+    """The path's neighbours in a pass, each timed per launch with dispatch-
+    attached events: the Q4_K token embedding of 8 decode tokens from a full
+    248,320 x 4096 table (quant_linear.metal:572-591), the RMS norm of the 8
+    decode rows, and config 3's LM-head rms_norm_gather (8 of 821 rows).
+    All three are single round trips of a few KB to a few hundred KB, so
+    they are latency-bound; their GB/s are reported for completeness."""
+    import torch
+    import mtlqwen_amd as q4k
+
+    vocab, k = 248320, 4096
+    rb = k // 256 * BLOCK_BYTES
+    g = torch.Generator(device=dev).manual_seed(0x51A70005)
+    raw = torch.randint(0, 256, (vocab, rb), dtype=torch.uint8, device=dev, generator=g)
+    dd = (torch.rand((vocab, k // 256, 2), device=dev, generator=g) * 0.01).half().view(torch.uint8)
+    raw.view(vocab, k // 256, BLOCK_BYTES)[:, :, 0:4] = dd.view(vocab, k // 256, 4)
+    table = q4k.Weight(raw.reshape(-1), vocab, k)
+    del raw, dd
+    ids = torch.randint(0, vocab, (8,), dtype=torch.int32, device=dev, generator=g)
+    emb = torch.empty((8, k), device=dev)
+    w = torch.randn(k, device=dev, generator=g)
+    lengths = [512, 37, 1, 1, 200, 5, 1, 64]
+    hidden = torch.randn((sum(lengths), k), device=dev, generator=g)
+    normed = torch.empty((8, k), device=dev)
+    lm_rows = torch.empty((8, k), device=dev)
+
+    def run():
+        q4k.embedding(table, ids, emb)
+        q4k.rms_norm(emb, w, normed)
+        q4k.rms_norm_gather(hidden, w, lm_rows, lengths, [1] * 8)
+
+    for _ in range(10):
+        run()
+    torch.cuda.synchronize()
+    reps = 100
+    # All three share one profiling family: time each in a loop of its own.
+    out = {}
+    for name, fn, nbytes in (
+            ("embedding_8_tokens", lambda: q4k.embedding(table, ids, emb), 8 * rb + 8 * k * 4 + 8 * 4),
+            ("rms_norm_8_rows", lambda: q4k.rms_norm(emb, w, normed), 2 * 8 * k * 4 + k * 4),
+            ("rms_norm_gather_config3", lambda: q4k.rms_norm_gather(hidden, w, lm_rows, lengths, [1] * 8),
+             2 * 8 * k * 4 + k * 4)):
+        q4k.profile_enable(True)
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        n, tot, lo, _ = q4k.profile_query(q4k.KERNEL_AUX)
+        q4k.profile_enable(False)
+        avg_us = tot / n * 1e3
+        out[name] = {"avg_us": round(avg_us, 3), "min_us": round(lo * 1e3, 3), "bytes": nbytes,
+                     "gbs": round(nbytes / (avg_us * 1e-6) / 1e9, 1)}
+    return out
+
+
 def prefill_bench(args, dev):
     import numpy as np
     import torch
@@ -320,6 +374,7 @@ def main():
     dec = decode_bench(args, dev)
     pre = None if args.no_prefill else prefill_bench(args, dev)
     shard = shard_bench(args, dev)
+    neighbours = neighbours_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
@@ -362,6 +417,7 @@ def main():
             "stage_launches_per_step": dec["stage_launches"] / dec["steps"],
         },
         "shard_1of8": shard,
+        "neighbours": neighbours,
         "copy_ceiling_gbs": round(copy_gbs, 1),
         "mfma_ceiling_tflops": round(mfma_tf, 1),
         "cpu_baseline": cpu,

@@ -121,11 +121,34 @@ int q4k_pack_queries(const uint32_t* counts, const uint32_t* samples, uint32_t n
 int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const uint32_t* counts, const uint32_t* samples, uint32_t nqueries,
                     uint32_t dtype, uint32_t* rows_out);
 
+/* Token embedding (backend/metal/kernel/quant_linear.metal:572-591,
+ * embedding_q4_k; dispatched at model/qwen35/forward.cpp:125,201-202):
+ * row t of y [rows, k] is row ids[t] of the Q4_K table, dequantised as
+ * d*sc*q - dmin*m in fp32 (then rounded to half for Q4K_DTYPE_F16).  ids is
+ * a device array of rows int32 token ids; the reference derives them from its
+ * query records and drafter proposals (quant_linear.metal:577-582), which
+ * stay with the engine.  Ids outside [0, n) give a zero row.  y must not
+ * overlap ids. */
+int q4k_embedding(void* stream, const q4k_weight* table, const int32_t* ids, uint32_t rows, void* y, uint32_t dtype);
+
+/* RMS norm (native_ops.metal:6-40 rms_norm; forward.cpp:82,114):
+ * y[r] = x[r] * rsqrt(sum(x[r]^2) / k + eps) * w for m rows of k; w is a
+ * device array of k fp32 weights (the reference uses eps = 1e-6,
+ * native_ops.metal:31).  y may equal x; otherwise they must not overlap. */
+int q4k_rms_norm(void* stream, const void* x, const float* w, void* y, uint32_t m, uint32_t k, float eps, uint32_t dtype);
+
+/* rms_norm_gather (native_ops.metal:6-40 with Gather, forward.cpp:72-75): the
+ * LM-head rows that q4k_gather_rows selects, each RMS-normalised as above,
+ * written to out [sum(samples), k]. */
+int q4k_rms_norm_gather(void* stream, const void* x, const float* w, void* out, uint32_t k, const uint32_t* counts, const uint32_t* samples,
+                        uint32_t nqueries, float eps, uint32_t dtype, uint32_t* rows_out);
+
 /* Kernel families, for q4k_profile_query. */
 #define Q4K_KERNEL_STAGE 0u      /* activation staging (fp16 + row scale) */
 #define Q4K_KERNEL_GEMV 1u       /* MFMA GEMV, phases 0/2 and small prefill */
 #define Q4K_KERNEL_GEMV_GATED 2u /* fused gate/up GEMV, phase 3 */
 #define Q4K_KERNEL_GEMM 3u       /* LDS-tiled MFMA GEMM, phase 1 */
+#define Q4K_KERNEL_AUX 4u        /* token embedding, RMS norm, rms_norm_gather */
 
 /* Event timing of every kernel launch (no counterpart in the reference, whose
  * method is paired A/B timing, agents/KERNELS.md:13-21).  While enabled, each

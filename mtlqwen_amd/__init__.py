@@ -7,14 +7,15 @@ a packed ragged batch.
 """
 from ._lib import DTYPE_F16, DTYPE_F32, GGML_TYPE_Q4_K, PHASE_DECODE, PHASE_GATED_DECODE, PHASE_PREFILL, \
     PHASE_PREFILL_SMALL, POST_ADD, POST_GATE, POST_STORE, KERNEL_STAGE, KERNEL_GEMV, KERNEL_GEMV_GATED, KERNEL_GEMM, \
-    Q4KError, lib
-from .linear import (PHASE_NAMES, Weight, gather_rows, linear, mfma_ceiling, mlp, mlp_gate_up, pack_queries,
-                     profile_enable, profile_query, q4k_nbytes, relayout_host, select_phase, unrelayout_host)
+    KERNEL_AUX, Q4KError, lib
+from .linear import (PHASE_NAMES, Weight, embedding, gather_rows, linear, mfma_ceiling, mlp, mlp_gate_up, pack_queries,
+                     profile_enable, profile_query, q4k_nbytes, relayout_host, rms_norm, rms_norm_gather, select_phase,
+                     unrelayout_host)
 
 __all__ = [
     "Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "relayout_host",
     "unrelayout_host", "q4k_nbytes", "Q4KError", "lib", "PHASE_NAMES", "DTYPE_F32", "DTYPE_F16", "GGML_TYPE_Q4_K",
     "POST_STORE", "POST_ADD", "POST_GATE", "PHASE_DECODE", "PHASE_PREFILL", "PHASE_PREFILL_SMALL",
     "PHASE_GATED_DECODE", "KERNEL_STAGE", "KERNEL_GEMV", "KERNEL_GEMV_GATED", "KERNEL_GEMM", "profile_enable",
-    "profile_query", "mfma_ceiling"
+    "profile_query", "mfma_ceiling", "embedding", "rms_norm", "rms_norm_gather", "KERNEL_AUX"
 ]

@@ -24,7 +24,7 @@ DTYPE_F32 = 0
 DTYPE_F16 = 1
 POST_STORE, POST_ADD, POST_GATE = 0, 1, 2
 PHASE_DECODE, PHASE_PREFILL, PHASE_PREFILL_SMALL, PHASE_GATED_DECODE = 0, 1, 2, 3
-KERNEL_STAGE, KERNEL_GEMV, KERNEL_GEMV_GATED, KERNEL_GEMM = 0, 1, 2, 3
+KERNEL_STAGE, KERNEL_GEMV, KERNEL_GEMV_GATED, KERNEL_GEMM, KERNEL_AUX = 0, 1, 2, 3, 4
 
 
 class Q4KError(RuntimeError):
@@ -56,6 +56,9 @@ def _load():
         "q4k_select_phase": (c_int, [pu32, u32, u32, c_int, pu32]),
         "q4k_pack_queries": (c_int, [pu32, pu32, u32, pu32, pu32, pu32, pu32]),
         "q4k_gather_rows": (c_int, [p, p, p, u32, pu32, pu32, u32, u32, pu32]),
+        "q4k_embedding": (c_int, [p, p, p, u32, p, u32]),
+        "q4k_rms_norm": (c_int, [p, p, p, p, u32, u32, ctypes.c_float, u32]),
+        "q4k_rms_norm_gather": (c_int, [p, p, p, p, u32, pu32, pu32, u32, ctypes.c_float, u32, pu32]),
         "q4k_profile_enable": (c_int, [c_int]),
         "q4k_profile_query": (c_int, [u32, pu32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_double)]),

@@ -77,7 +77,7 @@ Workspace g_ws[64];
 struct Profiler {
   std::mutex mu;
   bool on = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> events[4];
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events[5];
 
   void clear() {
     for (auto& v : events) {
@@ -311,6 +311,27 @@ int stage_pack(hipStream_t stream, Workspace& ws, int device, const void* x, uin
   pk->dsc = reinterpret_cast<float*>(ws.pack + nb * (8 * 64 * 16 + 64 * 8));
   LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
   Q4K_TRY_HIP(launch_stage_pack(stream, x, (int)dtype, *pk, (int)m, (int)k), "stage_pack launch");
+  return Q4K_OK;
+}
+
+// LM-head rows of a packed batch (native_ops.metal:12-15 with batch.hpp:25-29
+// queryLogit): output row r reads input row start + count - samples +
+// (r - logit) of the first query with samples whose logit range holds r.
+// *rows receives the batch's total row count.
+int logit_rows(const uint32_t* counts, const uint32_t* samples, uint32_t nqueries, GatherIndex* idx, uint32_t* rows) {
+  uint32_t start[Q4K_MAX_QUERIES], logit[Q4K_MAX_QUERIES], nlogit = 0;
+  int rc = q4k_pack_queries(counts, samples, nqueries, start, logit, rows, &nlogit);
+  if (rc)
+    return rc;
+  if (nlogit > Q4K_MAX_LOGIT_ROWS)
+    return fail(Q4K_EINVAL, "%u sampled rows exceed %u", nlogit, Q4K_MAX_LOGIT_ROWS);
+  idx->rows = nlogit;
+  for (uint32_t r = 0; r < nlogit; ++r) {
+    uint32_t q = 0;
+    while (!samples[q] || r >= logit[q] + samples[q])
+      ++q;
+    idx->src[r] = start[q] + counts[q] - samples[q] + (r - logit[q]);
+  }
   return Q4K_OK;
 }
 
@@ -752,7 +773,7 @@ int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops) {
 }
 
 int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, double* min_ms, double* max_ms) {
-  if (kernel > 3)
+  if (kernel > Q4K_KERNEL_AUX)
     return fail(Q4K_EINVAL, "kernel family %u out of range", kernel);
   std::lock_guard<std::mutex> lock(g_prof.mu);
   double total = 0.0, lo = 0.0, hi = 0.0;
@@ -809,27 +830,76 @@ int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const ui
     return fail(Q4K_EINVAL, "bad dtype %u", dtype);
   if (k == 0)
     return fail(Q4K_ESHAPE, "k must be positive");
-  uint32_t start[Q4K_MAX_QUERIES], logit[Q4K_MAX_QUERIES], rows = 0, nlogit = 0;
-  int rc = q4k_pack_queries(counts, samples, nqueries, start, logit, &rows, &nlogit);
+  GatherIndex idx;
+  uint32_t rows = 0;
+  int rc = logit_rows(counts, samples, nqueries, &idx, &rows);
   if (rc)
     return rc;
-  if (nlogit > Q4K_MAX_LOGIT_ROWS)
-    return fail(Q4K_EINVAL, "%u sampled rows exceed %u", nlogit, Q4K_MAX_LOGIT_ROWS);
-  GatherIndex idx;
-  idx.rows = nlogit;
-  for (uint32_t r = 0; r < nlogit; ++r) {
-    // batch.hpp:25-29: first query with samples whose logit range holds r.
-    uint32_t q = 0;
-    while (!samples[q] || r >= logit[q] + samples[q])
-      ++q;
-    idx.src[r] = start[q] + counts[q] - samples[q] + (r - logit[q]);
-  }
   if (rows_out)
-    *rows_out = nlogit;
+    *rows_out = idx.rows;
   const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
-  if (overlaps(x, (size_t)rows * k * es, out, (size_t)nlogit * k * es))
+  if (overlaps(x, (size_t)rows * k * es, out, (size_t)idx.rows * k * es))
     return fail(Q4K_EALIAS, "out must not overlap x");
   Q4K_TRY_HIP(launch_gather(static_cast<hipStream_t>(stream), x, out, (int)k, (int)dtype, idx), "gather launch");
+  return Q4K_OK;
+}
+
+int q4k_embedding(void* stream, const q4k_weight* table, const int32_t* ids, uint32_t rows, void* y, uint32_t dtype) {
+  if (!table || !ids || !y)
+    return fail(Q4K_EINVAL, "null argument");
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (overlaps(ids, (size_t)rows * 4, y, (size_t)rows * table->k * es))
+    return fail(Q4K_EALIAS, "y must not overlap ids");
+  int rc = set_device(table->device);
+  if (rc)
+    return rc;
+  LaunchTimer timer(static_cast<hipStream_t>(stream), Q4K_KERNEL_AUX);
+  Q4K_TRY_HIP(launch_embedding(static_cast<hipStream_t>(stream), table->data, ids, y, (int)rows, (int)table->n, (int)table->k, (int)dtype),
+              "embedding launch");
+  return Q4K_OK;
+}
+
+int q4k_rms_norm(void* stream, const void* x, const float* w, void* y, uint32_t m, uint32_t k, float eps, uint32_t dtype) {
+  if (!x || !w || !y)
+    return fail(Q4K_EINVAL, "null argument");
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (k == 0)
+    return fail(Q4K_ESHAPE, "k must be positive");
+  if (!(eps >= 0.0f))
+    return fail(Q4K_EINVAL, "eps must be a non-negative number");
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (x != y && overlaps(x, (size_t)m * k * es, y, (size_t)m * k * es))
+    return fail(Q4K_EALIAS, "y must equal x or not overlap it");
+  LaunchTimer timer(static_cast<hipStream_t>(stream), Q4K_KERNEL_AUX);
+  Q4K_TRY_HIP(launch_rms_norm(static_cast<hipStream_t>(stream), x, w, y, (int)m, (int)k, eps, (int)dtype, nullptr), "rms_norm launch");
+  return Q4K_OK;
+}
+
+int q4k_rms_norm_gather(void* stream, const void* x, const float* w, void* out, uint32_t k, const uint32_t* counts, const uint32_t* samples,
+                        uint32_t nqueries, float eps, uint32_t dtype, uint32_t* rows_out) {
+  if (!x || !w || !out || !counts || !samples)
+    return fail(Q4K_EINVAL, "null argument");
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (k == 0)
+    return fail(Q4K_ESHAPE, "k must be positive");
+  if (!(eps >= 0.0f))
+    return fail(Q4K_EINVAL, "eps must be a non-negative number");
+  GatherIndex idx;
+  uint32_t rows = 0;
+  int rc = logit_rows(counts, samples, nqueries, &idx, &rows);
+  if (rc)
+    return rc;
+  if (rows_out)
+    *rows_out = idx.rows;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (overlaps(x, (size_t)rows * k * es, out, (size_t)idx.rows * k * es))
+    return fail(Q4K_EALIAS, "out must not overlap x");
+  LaunchTimer timer(static_cast<hipStream_t>(stream), Q4K_KERNEL_AUX);
+  Q4K_TRY_HIP(launch_rms_norm(static_cast<hipStream_t>(stream), x, w, out, (int)idx.rows, (int)k, eps, (int)dtype, &idx), "rms_norm_gather launch");
   return Q4K_OK;
 }
 

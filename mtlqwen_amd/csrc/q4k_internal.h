@@ -153,6 +153,13 @@ hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters)
 
 hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx);
 
+// Token embedding from a tiled Q4_K table (n rows of k): y[t] = row ids[t].
+hipError_t launch_embedding(hipStream_t s, const uint8_t* w, const int32_t* ids, void* y, int rows, int n, int k, int dtype);
+
+// RMS norm of `rows` rows of k (idx == nullptr: row r reads x row r;
+// otherwise x row idx->src[r]).
+hipError_t launch_rms_norm(hipStream_t s, const void* x, const float* w, void* y, int rows, int k, float eps, int dtype, const GatherIndex* idx);
+
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).
 hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
 

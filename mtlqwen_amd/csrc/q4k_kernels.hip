@@ -6,6 +6,8 @@
 //  q4k_gemm_kernel  prefill-shaped GEMM: Q4_K tiles dequantised to fp16 in LDS,
 //                   v_mfma_f32_32x32x16_f16, fp32 accumulation, post 0/1/2
 //  gather_rows_kernel, relayout_kernel
+//  embedding_kernel, rms_norm_kernel   the path's neighbours in a pass (token
+//                   embedding gather-dequant, RMS norm / LM-head rms_norm_gather)
 //
 // Reference semantics: backend/metal/kernel/quant_linear.metal (Q4_K parts)
 // and backend/metal/kernel/fused_kernels.metal:11-78.
@@ -1906,6 +1908,101 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ 
     dst[i] = src[i];
 }
 
+
+// ----------------------------------------------------------------------------
+// Token embedding (quant_linear.metal:572-591, embedding_q4_k): output row t
+// is row ids[t] of a Q4_K table kept in the tiled device layout, dequantised.
+// One 256-thread workgroup per (block, row); thread e forms element e of the
+// block from its byte (e / 64) * 32 + e % 32 (high nibble when e & 32) and
+// sub-block e / 32, as (d * sc) * q - dmin * m with each product and the
+// difference rounded once (no contraction; the CPU oracle's order).  Ids
+// outside [0, n) give a zero row.
+// ----------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restrict__ w, const int32_t* __restrict__ ids, OutT* __restrict__ y, int n,
+                                                        int nb) {
+#pragma clang fp contract(off)
+  const int b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
+  const int id = ids[t];
+  float v = 0.0f;
+  if (id >= 0 && id < n) {
+    const int i = id & 15;
+    const uint8_t* tb = w + ((size_t)(id >> 4) * nb + b) * kTileBlockBytes;
+    const uint8_t* hd = tb + kHeaderOffset + 16 * i;
+    const uint8_t* q12 = hd + 4;
+    // 6-bit scale and min of sub-block j (quant_linear.metal:12-20).
+    const int j = e >> 5;
+    uint32_t sc, mn;
+    if (j < 4) {
+      sc = q12[j] & 63u;
+      mn = q12[j + 4] & 63u;
+    } else {
+      sc = (q12[j + 4] & 15u) | ((uint32_t)(q12[j - 4] >> 6) << 4);
+      mn = (uint32_t)(q12[j + 4] >> 4) | ((uint32_t)(q12[j] >> 6) << 4);
+    }
+    // Quant byte p of the GGUF record: lane 16 (p / 32) + i of slab (p / 16) & 1,
+    // word (p / 4) & 3, with the word's two middle bytes swapped.
+    const int p = (e >> 6) * 32 + (e & 31), o = p & 31, bw = o & 3;
+    const int sbw = bw == 1 ? 2 : bw == 2 ? 1 : bw;
+    const uint8_t qb = tb[(o >> 4) * kSlabBytes + 16 * (16 * (p >> 5) + i) + (o & 12) + sbw];
+    const uint32_t q = (e & 32) ? (uint32_t)(qb >> 4) : (uint32_t)(qb & 15);
+    const float d = half_bits_to_float((uint32_t)hd[0] | ((uint32_t)hd[1] << 8));
+    const float dmin = half_bits_to_float((uint32_t)hd[2] | ((uint32_t)hd[3] << 8));
+    const float dsc = d * (float)sc;
+    const float val = dsc * (float)q;
+    const float mterm = dmin * (float)mn;
+    v = val - mterm;
+  }
+  store_elem(y, (size_t)t * nb * 256 + (size_t)b * 256 + e, v);
+}
+
+// ----------------------------------------------------------------------------
+// RMS norm (native_ops.metal:6-40): y[r] = x[s] * rsqrt(sum(x[s]^2) / k + eps)
+// * w, s = idx.src[r] for rms_norm_gather (the LM-head rows, batch.hpp:25-29)
+// or s = r.  One 256-thread workgroup per output row; fp32 sum of squares
+// (wave shuffle reduction, then across the 4 waves).  Rows of up to
+// 256 * kNormRegs elements stay in registers between the two passes (one
+// read of x); longer rows are read again.
+// ----------------------------------------------------------------------------
+constexpr int kNormRegs = 16;
+
+template <typename T>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x, const float* __restrict__ w, T* y, int k, float eps, GatherIndex idx,
+                                                       int gather) {
+  __shared__ float part[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const T* xr = x + (size_t)(gather ? idx.src[r] : (uint32_t)r) * k;
+  float v[kNormRegs];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormRegs; ++i) {
+    const int d = tid + 256 * i;
+    v[i] = d < k ? (float)xr[d] : 0.0f;
+    ss = fmaf(v[i], v[i], ss);
+  }
+  for (int d = tid + 256 * kNormRegs; d < k; d += 256) {
+    const float t = (float)xr[d];
+    ss = fmaf(t, t, ss);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    ss += __shfl_xor(ss, off);
+  if ((tid & 63) == 0)
+    part[tid >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float scale = 1.0f / sqrtf(total / (float)k + eps);
+  T* yr = y + (size_t)r * k;
+#pragma unroll
+  for (int i = 0; i < kNormRegs; ++i) {
+    const int d = tid + 256 * i;
+    if (d < k)
+      yr[d] = (T)((v[i] * scale) * w[d]);
+  }
+  for (int d = tid + 256 * kNormRegs; d < k; d += 256)
+    yr[d] = (T)(((float)xr[d] * scale) * w[d]);
+}
+
 __device__ __forceinline__ uint32_t swap_middle_bytes(uint32_t v) {
   return (v & 0xff0000ffu) | ((v & 0x0000ff00u) << 8) | ((v & 0x00ff0000u) >> 8);
 }
@@ -2237,6 +2334,32 @@ hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dty
     (void)dispatch(gather_rows_kernel<float>, grid, block, s, static_cast<const float*>(x), static_cast<float*>(out), k, idx);
   else
     (void)dispatch(gather_rows_kernel<_Float16>, grid, block, s, static_cast<const _Float16*>(x), static_cast<_Float16*>(out), k, idx);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding(hipStream_t s, const uint8_t* w, const int32_t* ids, void* y, int rows, int n, int k, int dtype) {
+  if (rows == 0)
+    return hipSuccess;
+  const dim3 grid((unsigned)(k / 256), (unsigned)rows), block(256);
+  if (dtype == kF32)
+    (void)dispatch(embedding_kernel<float>, grid, block, s, w, ids, static_cast<float*>(y), n, k / 256);
+  else
+    (void)dispatch(embedding_kernel<_Float16>, grid, block, s, w, ids, static_cast<_Float16*>(y), n, k / 256);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(hipStream_t s, const void* x, const float* w, void* y, int rows, int k, float eps, int dtype, const GatherIndex* idx) {
+  if (rows == 0)
+    return hipSuccess;
+  GatherIndex gi{};
+  if (idx)
+    gi = *idx;
+  const dim3 grid((unsigned)rows), block(256);
+  if (dtype == kF32)
+    (void)dispatch(rms_norm_kernel<float>, grid, block, s, static_cast<const float*>(x), w, static_cast<float*>(y), k, eps, gi, idx ? 1 : 0);
+  else
+    (void)dispatch(rms_norm_kernel<_Float16>, grid, block, s, static_cast<const _Float16*>(x), w, static_cast<_Float16*>(y), k, eps, gi,
+                   idx ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -168,6 +168,45 @@ def gather_rows(x, out, counts, samples, stream=None):
     return rows.value
 
 
+def embedding(table, ids, y, stream=None):
+    """Token embedding (embedding_q4_k, quant_linear.metal:572-591): row t of
+    ``y`` is row ids[t] of the Q4_K ``table`` dequantised.  ``ids`` is an
+    int32 device tensor; ids outside [0, n) give zero rows."""
+    if ids.dtype != torch.int32:
+        raise TypeError("ids must be an int32 tensor")
+    rows = ids.numel()
+    if y.shape[0] < rows or y.numel() < rows * table.k:
+        raise ValueError("y must hold len(ids) rows of table.k values")
+    check(lib.q4k_embedding(_stream(stream), table.handle, _ptr(ids), rows, _ptr(y), _dtype_code(y)))
+    return y
+
+
+def rms_norm(x, weight, y, eps=1e-6, stream=None):
+    """RMS norm of every row of ``x`` (native_ops.metal:6-40) with fp32
+    ``weight`` [k]; ``y`` may be ``x``."""
+    _check_norm_weight(weight, x.shape[-1])
+    m = x.numel() // x.shape[-1]
+    check(lib.q4k_rms_norm(_stream(stream), _ptr(x), _ptr(weight), _ptr(y), m, x.shape[-1], float(eps), _dtype_code(x)))
+    return y
+
+
+def rms_norm_gather(x, weight, out, counts, samples, eps=1e-6, stream=None):
+    """LM-head rms_norm_gather (native_ops.metal:6-40, forward.cpp:72-75):
+    the rows gather_rows selects, RMS-normalised; returns their count."""
+    _check_norm_weight(weight, x.shape[-1])
+    c, nq = u32_array(counts)
+    s, _ = u32_array(samples)
+    rows = ctypes.c_uint32()
+    check(lib.q4k_rms_norm_gather(_stream(stream), _ptr(x), _ptr(weight), _ptr(out), x.shape[-1], c, s, nq, float(eps),
+                                  _dtype_code(x), ctypes.byref(rows)))
+    return rows.value
+
+
+def _check_norm_weight(weight, k):
+    if weight.dtype != torch.float32 or weight.numel() != k:
+        raise ValueError(f"norm weight must be {k} float32 values")
+
+
 def profile_enable(on=True):
     """Bracket every kernel launch with hipEvents (clears earlier records)."""
     check(lib.q4k_profile_enable(int(bool(on))))
@@ -203,6 +242,7 @@ def unrelayout_host(tiled, n, k):
     return dst
 
 
-__all__ = ["Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "relayout_host",
+__all__ = ["Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "embedding", "rms_norm",
+           "rms_norm_gather", "relayout_host",
            "profile_enable", "profile_query", "mfma_ceiling",
            "unrelayout_host", "q4k_nbytes", "Q4KError", "PHASE_NAMES"]

@@ -386,3 +386,75 @@ int64_t q4o_gather_row(const uint32_t* start, const uint32_t* count, const uint3
       return (int64_t)start[i] + count[i] - samples[i] + (r - logit[i]);
   return -1;
 }
+
+/* ------------------------------------------------- adjacent consumers -- */
+
+/* quant_linear.metal:572-591: element r of the row's block (col >> 8) is
+ * d*sc_j*v - dmin*m_j with j = r >> 5 and v the nibble of byte
+ * (r >> 6) * 32 + (r & 31) (high nibble when r & 32). */
+static int embedding_common(float* yf, uint16_t* yh, const uint8_t* w, int n, int k, const int32_t* ids, int rows) {
+  if ((!yf && !yh) || !w || !ids || n <= 0 || k <= 0 || k % 256 != 0 || rows < 0)
+    return -1;
+  const int nb = k / 256;
+  float row[256];
+  for (int t = 0; t < rows; ++t) {
+    const int32_t id = ids[t];
+    for (int b = 0; b < nb; ++b) {
+      if (id >= 0 && id < n)
+        q4o_dequant_block(w + ((size_t)id * nb + b) * Q4O_BLOCK_BYTES, row);
+      else
+        memset(row, 0, sizeof row);
+      for (int e = 0; e < 256; ++e) {
+        const size_t o = (size_t)t * k + (size_t)b * 256 + e;
+        if (yf)
+          yf[o] = row[e];
+        else
+          yh[o] = q4o_float_to_half(row[e]);
+      }
+    }
+  }
+  return 0;
+}
+
+int q4o_embedding_f32(float* y, const uint8_t* w, int n, int k, const int32_t* ids, int rows) {
+  return embedding_common(y, NULL, w, n, k, ids, rows);
+}
+
+int q4o_embedding_f16(uint16_t* y, const uint8_t* w, int n, int k, const int32_t* ids, int rows) {
+  return embedding_common(NULL, y, w, n, k, ids, rows);
+}
+
+/* native_ops.metal:6-40 (rms_norm / rms_norm_gather). */
+static int rms_norm_common(float* yf, uint16_t* yh, const float* xf, const uint16_t* xh, const float* w, const int64_t* src, int rows, int k,
+                           float eps) {
+  if ((!yf && !yh) || (!xf && !xh) || !w || rows < 0 || k <= 0)
+    return -1;
+  for (int r = 0; r < rows; ++r) {
+    const int64_t s = src ? src[r] : r;
+    if (s < 0)
+      return -1;
+    double ss = 0.0;
+    for (int d = 0; d < k; ++d) {
+      const double v = xf ? (double)xf[(size_t)s * k + d] : (double)q4o_half_to_float(xh[(size_t)s * k + d]);
+      ss += v * v;
+    }
+    const double scale = 1.0 / sqrt(ss / (double)k + (double)eps);
+    for (int d = 0; d < k; ++d) {
+      const double v = xf ? (double)xf[(size_t)s * k + d] : (double)q4o_half_to_float(xh[(size_t)s * k + d]);
+      const float out = (float)(v * scale * (double)w[d]);
+      if (yf)
+        yf[(size_t)r * k + d] = out;
+      else
+        yh[(size_t)r * k + d] = q4o_float_to_half(out);
+    }
+  }
+  return 0;
+}
+
+int q4o_rms_norm_f32(float* y, const float* x, const float* w, const int64_t* src, int rows, int k, float eps) {
+  return rms_norm_common(y, NULL, x, NULL, w, src, rows, k, eps);
+}
+
+int q4o_rms_norm_f16(uint16_t* y, const uint16_t* x, const float* w, const int64_t* src, int rows, int k, float eps) {
+  return rms_norm_common(NULL, y, NULL, x, w, src, rows, k, eps);
+}

@@ -82,6 +82,26 @@ uint32_t q4o_pack(const uint32_t* counts, const uint32_t* samples, int nqueries,
  * query that owns logit row r.  Returns -1 if r is not owned by any query. */
 int64_t q4o_gather_row(const uint32_t* start, const uint32_t* count, const uint32_t* samples, const uint32_t* logit, int nqueries, uint32_t r);
 
+/* Token-embedding gather-dequant: row t of y (k values) is row ids[t] of the
+ * Q4_K table w (n rows of k/256 blocks), each element d*sc*q - dmin*m in fp32
+ * ((d*sc)*q first, then the min product subtracted).
+ * backend/metal/kernel/quant_linear.metal:572-591 (embedding_q4_k, the row's
+ * element addressing at :585-590); the f16 variant is its half() store.  The
+ * reference resolves ids from its query records and drafter proposals
+ * (:577-582); here they are given.  ids outside [0, n) give a zero row.
+ * Returns 0, or -1 on invalid arguments. */
+int q4o_embedding_f32(float* y, const uint8_t* w, int n, int k, const int32_t* ids, int rows);
+int q4o_embedding_f16(uint16_t* y, const uint8_t* w, int n, int k, const int32_t* ids, int rows);
+
+/* RMS norm over rows of k values (native_ops.metal:6-40):
+ * y[r][d] = x[s][d] * rsqrt(sum_d x[s][d]^2 / k + eps) * w[d] with s = src[r]
+ * (src == NULL: s = r, rms_norm; otherwise the LM-head rows of rms_norm_gather,
+ * q4o_gather_row).  The sum of squares and the scale are taken in double; the
+ * f16 variant reads and writes half (x widened exactly, y rounded once).
+ * Returns 0, or -1 on invalid arguments. */
+int q4o_rms_norm_f32(float* y, const float* x, const float* w, const int64_t* src, int rows, int k, float eps);
+int q4o_rms_norm_f16(uint16_t* y, const uint16_t* x, const float* w, const int64_t* src, int rows, int k, float eps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -121,6 +121,12 @@ def load_oracle():
     lib.q4o_pack.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 2 + [i] + [ctypes.POINTER(ctypes.c_uint32)] * 2
     lib.q4o_gather_row.restype = ctypes.c_int64
     lib.q4o_gather_row.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 4 + [i, ctypes.c_uint32]
+    for name in ("q4o_embedding_f32", "q4o_embedding_f16"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = [p, u8p, i, i, p, i]
+    for name in ("q4o_rms_norm_f32", "q4o_rms_norm_f16"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = [p, p, p, p, i, i, ctypes.c_float]
     return lib
 
 
@@ -189,6 +195,39 @@ class Oracle:
         start, logit = (ctypes.c_uint32 * n)(), (ctypes.c_uint32 * n)()
         rows = self.lib.q4o_pack(c, s, n, start, logit)
         return list(start), list(logit), rows
+
+    def embedding(self, w, n, k, ids, f16=False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        if f16:
+            y = np.empty((len(ids), k), np.float16)
+            rc = self.lib.q4o_embedding_f16(self._p(y), self._p(w), n, k, self._p(ids), len(ids))
+        else:
+            y = np.empty((len(ids), k), np.float32)
+            rc = self.lib.q4o_embedding_f32(self._p(y), self._p(w), n, k, self._p(ids), len(ids))
+        assert rc == 0
+        return y
+
+    def rms_norm(self, x, w, src=None, eps=1e-6):
+        """RMS norm of rows src (default: every row) of x [rows, k]."""
+        x = np.ascontiguousarray(x)
+        k = x.shape[-1]
+        w = np.ascontiguousarray(w, np.float32)
+        srca = None if src is None else np.ascontiguousarray(src, np.int64)
+        rows = x.shape[0] if src is None else len(srca)
+        if x.dtype == np.float16:
+            y = np.empty((rows, k), np.float16)
+            rc = self.lib.q4o_rms_norm_f16(self._p(y), self._p(x), self._p(w), self._p(srca), rows, k, eps)
+        else:
+            x = x.astype(np.float32, copy=False)
+            y = np.empty((rows, k), np.float32)
+            rc = self.lib.q4o_rms_norm_f32(self._p(y), self._p(x), self._p(w), self._p(srca), rows, k, eps)
+        assert rc == 0
+        return y
+
+    def logit_sources(self, counts, samples):
+        """Input row of every LM-head output row (q4o_gather_row over the pack)."""
+        start, logit, _ = self.pack(counts, samples)
+        return [self.gather_row(start, counts, samples, logit, r) for r in range(sum(samples))]
 
     def gather_row(self, start, count, samples, logit, r):
         n = len(start)

@@ -113,3 +113,23 @@ def test_linear_validation_before_hip(q4k):
     assert b"weight" in lib.q4k_last_error()
     assert lib.q4k_mlp_gate_up(None, None, None, None, None, 1, None, 0, 0) == -1
     assert lib.q4k_weight_destroy(None) == 0
+
+
+def test_neighbour_entry_points_validate_before_hip(q4k):
+    """Argument errors of the embedding / RMS-norm entry points are reported
+    before any HIP call (no GPU needed)."""
+    lib = q4k.lib
+    fake = ctypes.c_void_p(0x1000)
+    u32 = ctypes.c_uint32
+    assert lib.q4k_embedding(None, None, fake, 1, fake, 0) == -1
+    assert lib.q4k_rms_norm(None, None, fake, fake, 1, 16, ctypes.c_float(1e-6), 0) == -1
+    assert lib.q4k_rms_norm(None, fake, fake, fake, 1, 16, ctypes.c_float(-1.0), 0) == -1
+    assert lib.q4k_rms_norm(None, fake, fake, fake, 1, 0, ctypes.c_float(1e-6), 0) == -3
+    assert lib.q4k_rms_norm(None, fake, fake, fake, 1, 16, ctypes.c_float(1e-6), 7) == -1
+    # y partially overlapping x
+    assert lib.q4k_rms_norm(None, ctypes.c_void_p(0x1000), fake, ctypes.c_void_p(0x1004), 2, 16, ctypes.c_float(1e-6), 0) == -4
+    counts = (u32 * 2)(40, 40)
+    samples = (u32 * 2)(40, 40)  # 80 sampled rows > 64
+    assert lib.q4k_rms_norm_gather(None, fake, fake, ctypes.c_void_p(0x100000), 16, counts, samples, 2,
+                                   ctypes.c_float(1e-6), 0, None) == -1
+    assert "exceed" in lib.q4k_last_error().decode()
