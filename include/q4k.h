@@ -35,6 +35,8 @@ extern "C" {
 #define Q4K_EALIAS (-4) /* x overlaps y (aux may alias y) */
 #define Q4K_EHIP (-5)   /* HIP runtime failure */
 #define Q4K_ENOMEM (-6)
+#define Q4K_EFORMAT (-7)   /* malformed or truncated GGUF file */
+#define Q4K_ENOTFOUND (-8) /* missing file, tensor or metadata key */
 
 #define Q4K_GGML_TYPE_Q4_K 12u
 
@@ -142,6 +144,45 @@ int q4k_rms_norm(void* stream, const void* x, const float* w, void* y, uint32_t 
  * written to out [sum(samples), k]. */
 int q4k_rms_norm_gather(void* stream, const void* x, const float* w, void* out, uint32_t k, const uint32_t* counts, const uint32_t* samples,
                         uint32_t nqueries, float eps, uint32_t dtype, uint32_t* rows_out);
+
+/* ---- GGUF reader ---------------------------------------------------------
+ * Replaces the reference's ggml gguf_init_from_buffer over the mapped model
+ * file (model/qwen35/forward.cpp:12-23, loadWeights).  The file is mapped
+ * read-only; versions 2 and 3 of the GGUF container are read, every offset
+ * and length is checked against the file size, and malformed files return
+ * Q4K_EFORMAT.  A handle is read-only after open and may be shared by
+ * threads; close it after the last use of q4k_gguf_tensor_data pointers. */
+typedef struct q4k_gguf q4k_gguf;
+
+int q4k_gguf_open(const char* path, q4k_gguf** out);
+int q4k_gguf_close(q4k_gguf* g);
+
+/* Container version, tensor and metadata counts, start of the data section
+ * (gguf_get_data_offset, forward.cpp:14) and file size. */
+int q4k_gguf_info(const q4k_gguf* g, uint32_t* version, uint64_t* n_tensors, uint64_t* n_kv, uint64_t* data_offset, uint64_t* file_bytes);
+
+/* Tensor i (gguf_get_tensor_name / _type / _ne / _offset / _size,
+ * forward.cpp:18-21): name (NUL-terminated into name[name_len]), ggml type,
+ * dimensions (ne[0] fastest; unused ones are 1), absolute file offset and
+ * byte size (0 for ggml types whose block size the reader does not know). */
+int q4k_gguf_tensor(const q4k_gguf* g, uint64_t i, char* name, size_t name_len, uint32_t* ggml_type, uint32_t* n_dims, uint64_t ne[4],
+                    uint64_t* file_offset, uint64_t* bytes);
+
+/* Index of the tensor called name; Q4K_ENOTFOUND ("missing weight", the
+ * reference's lookup error, forward.cpp:37-41) if there is none. */
+int q4k_gguf_find(const q4k_gguf* g, const char* name, uint64_t* index);
+
+/* Host pointer to tensor i's bytes inside the mapping, valid until close. */
+int q4k_gguf_tensor_data(const q4k_gguf* g, uint64_t i, const void** data, uint64_t* bytes);
+
+/* Metadata value of key: any integer or bool type as int64; a string. */
+int q4k_gguf_meta_int(const q4k_gguf* g, const char* key, int64_t* value);
+int q4k_gguf_meta_str(const q4k_gguf* g, const char* key, char* buf, size_t len);
+
+/* Upload the Q4_K matrix called name to device as a weight with n = ne[1]
+ * rows of k = ne[0] (the Weight loadWeights builds, forward.cpp:18-21);
+ * Q4K_ETYPE if it is not Q4_K. */
+int q4k_weight_from_gguf(const q4k_gguf* g, const char* name, int device, q4k_weight** out);
 
 /* Kernel families, for q4k_profile_query. */
 #define Q4K_KERNEL_STAGE 0u      /* activation staging (fp16 + row scale) */

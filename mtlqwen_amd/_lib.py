@@ -18,6 +18,8 @@ ESHAPE = -3
 EALIAS = -4
 EHIP = -5
 ENOMEM = -6
+EFORMAT = -7
+ENOTFOUND = -8
 
 GGML_TYPE_Q4_K = 12
 DTYPE_F32 = 0
@@ -43,6 +45,7 @@ def _load():
     lib = ctypes.CDLL(LIB_PATH)
     u32, p, c_int, size_t = ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
     pu32 = ctypes.POINTER(ctypes.c_uint32)
+    pu64 = ctypes.POINTER(ctypes.c_uint64)
     sigs = {
         "q4k_last_error": (ctypes.c_char_p, []),
         "q4k_weight_create": (c_int, [p, size_t, u32, u32, u32, c_int, ctypes.POINTER(p)]),
@@ -64,6 +67,15 @@ def _load():
                                       ctypes.POINTER(ctypes.c_double)]),
         "q4k_mfma_ceiling": (c_int, [p, c_int, u32, ctypes.POINTER(ctypes.c_double)]),
         "q4k_relayout_host": (c_int, [p, p, u32, u32]),
+        "q4k_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(p)]),
+        "q4k_gguf_close": (c_int, [p]),
+        "q4k_gguf_info": (c_int, [p, pu32, pu64, pu64, pu64, pu64]),
+        "q4k_gguf_tensor": (c_int, [p, ctypes.c_uint64, ctypes.c_char_p, size_t, pu32, pu32, pu64, pu64, pu64]),
+        "q4k_gguf_find": (c_int, [p, ctypes.c_char_p, pu64]),
+        "q4k_gguf_tensor_data": (c_int, [p, ctypes.c_uint64, ctypes.POINTER(p), pu64]),
+        "q4k_gguf_meta_int": (c_int, [p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+        "q4k_gguf_meta_str": (c_int, [p, ctypes.c_char_p, ctypes.c_char_p, size_t]),
+        "q4k_weight_from_gguf": (c_int, [p, ctypes.c_char_p, c_int, ctypes.POINTER(p)]),
         "q4k_unrelayout_host": (c_int, [p, p, u32, u32]),
     }
     for name, (res, args) in sigs.items():

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libq4k.so")
-SOURCES = ["q4k_kernels.hip", "q4k_api.hip"]
+SOURCES = ["q4k_kernels.hip", "q4k_api.hip", "q4k_gguf.cpp"]
 ARCH = os.environ.get("Q4K_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: no v_pk_*_f32 in device code (the host pass warns that it
@@ -53,7 +53,7 @@ def build(verbose=False):
     objs = []
     cmds = []
     for src in SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as pool:

@@ -19,6 +19,8 @@
 
 using namespace q4k;
 
+int q4k_internal_fail(int code, const char* msg);
+
 namespace {
 
 thread_local std::string g_error;
@@ -32,6 +34,15 @@ int fail(int code, const char* fmt, ...) {
   g_error = buf;
   return code;
 }
+
+}  // namespace
+
+// Shared with the GGUF reader (q4k_gguf.cpp): records the thread's last error.
+int q4k_internal_fail(int code, const char* msg) {
+  return fail(code, "%s", msg);
+}
+
+namespace {
 
 int hip_fail(hipError_t e, const char* what) {
   return fail(Q4K_EHIP, "%s: %s", what, hipGetErrorString(e));

@@ -78,6 +78,14 @@ class Weight:
             raise ValueError("weight has been released")
         return self._h
 
+    @classmethod
+    def _from_handle(cls, handle, n, k, ggml_type, device):
+        """Wrap a handle the C ABI created (GGUF uploads)."""
+        obj = cls.__new__(cls)
+        obj._h = handle
+        obj.n, obj.k, obj.type, obj.device = n, k, ggml_type, device
+        return obj
+
     def kernel_name(self, phase):
         buf = ctypes.create_string_buffer(256)
         check(lib.q4k_weight_kernel_name(self.handle, phase, buf, 256))
