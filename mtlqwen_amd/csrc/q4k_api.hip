@@ -736,6 +736,37 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
   return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, false);
 }
 
+int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const void* x, void* gate, void* hidden, uint32_t m,
+            const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype) {
+  if (!wg || !wu || !wd)
+    return fail(Q4K_EINVAL, "gate, up and down weights must be non-NULL");
+  if (wg->n != wu->n || wg->k != wu->k || wg->device != wu->device)
+    return fail(Q4K_ESHAPE, "gate (%ux%u) and up (%ux%u) weights differ", wg->n, wg->k, wu->n, wu->k);
+  if (wd->k != wg->n || wd->n != wg->k || wd->device != wg->device)
+    return fail(Q4K_ESHAPE, "down weight %ux%u does not map the %u gate outputs back to %u", wd->n, wd->k, wg->n, wg->k);
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (m == 0)
+    return fail(Q4K_ESHAPE, "m must be positive");
+  if (!x || !gate || !hidden)
+    return fail(Q4K_EINVAL, "x, gate and hidden must be non-NULL");
+  int rc = check_counts(query_counts, nqueries, m);
+  if (rc)
+    return rc;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  const size_t xb = (size_t)m * wg->k * es, gb = (size_t)m * wg->n * es, hb = (size_t)m * wd->n * es;
+  if (overlaps(x, xb, gate, gb) || overlaps(gate, gb, hidden, hb))
+    return fail(Q4K_EALIAS, "the gate buffer must not overlap x or hidden");
+  if (overlaps(x, xb, hidden, hb))
+    return fail(Q4K_EALIAS, "x must not overlap hidden");
+  // forward.cpp:115-119 as two calls: gate/up into the gate buffer, then down
+  // with the residual added in place.
+  rc = q4k_mlp_gate_up(stream, wg, wu, x, gate, m, query_counts, nqueries, dtype);
+  if (rc)
+    return rc;
+  return q4k_linear(stream, wd, gate, hidden, hidden, m, query_counts, nqueries, Q4K_POST_ADD, dtype);
+}
+
 int q4k_profile_enable(int on) {
   std::lock_guard<std::mutex> lock(g_prof.mu);
   if (on)

@@ -1072,19 +1072,22 @@ __device__ __forceinline__ void pack_x_regs(const float (&xv)[32], int lane, XBl
   }
 }
 
+// x of wave w, re-ordered for the register pack: [block][lane][32 + 4]
+// floats (the 4-float pad makes the 16-byte reads of 16 lanes hit 64
+// distinct banks).  The partial sums reuse the wave's own region at the end.
+constexpr int kGuXRow = 36;
+constexpr int kGuWaveFloats = 2 * 64 * kGuXRow;
+
+// One item (T column tiles of both matrices) of the fused gate/up GEMV, by the
+// 8 waves of the workgroup, over kGuLdsBytes of LDS.
 template <int T, typename OutT>
-__global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
+__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], int item) {
   constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT;
-  // x of wave w, re-ordered for the register pack: [block][lane][32 + 4]
-  // floats (the 4-float pad makes the 16-byte reads of 16 lanes hit 64
-  // distinct banks).  The partial sums reuse the wave's own region at the end.
-  constexpr int kXRow = 36;
+  constexpr int kXRow = kGuXRow;
   static_assert(MT * 8 * 16 <= BPW * 64 * kXRow, "partials fit the x region");
-  __shared__ __attribute__((aligned(16))) float xl[W][BPW * 64 * kXRow];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int item = blockIdx.x;
   const int nb = a.nb, bw = ((wave + item) % W) * BPW;
   const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
 
@@ -1218,6 +1221,12 @@ __global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
   }
 }
 
+template <int T, typename OutT>
+__global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) float xl[8][kGuWaveFloats];
+  gate_up_item<T, OutT>(a, xl, blockIdx.x);
+}
+
 // ----------------------------------------------------------------------------
 // Split-K GEMV (m <= 8 rows, split hi/lo into one 16-row activation tile as
 // in the streaming GEMV).
@@ -1240,8 +1249,27 @@ __global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
 // Workgroups of one group are placed on one XCD (workgroup b runs on XCD
 // b % 8), so their partials meet in one L2.
 // ----------------------------------------------------------------------------
+// Count of arrivals at a counter shared by workgroups on any XCD: the atomic
+// is performed at system scope (past every XCD's L2).
+__device__ __forceinline__ int count_arrival(int* ctr) {
+  return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ void reset_counter(int* ctr) {
+  __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Bytes of LDS one split-K slice uses.
+template <int NM, int T, int BPS, int DP>
+constexpr int splitk_lds_bytes() {
+  return 8 * DP * (NM * T / 8) * kTileBlockBytes + BPS * 8 * 64 * 16 + BPS * 64 * 8 + BPS * 8 * 4;
+}
+
+// One workgroup's K-slice ks of column group grp (see above), over LDS of
+// splitk_lds_bytes().
 template <int NM, int T, int KS, int BPS, int DP, typename OutT>
-__global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float* __restrict__ part, int* __restrict__ counters) {
+__device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, int* s_last, float* __restrict__ part, int* __restrict__ counters,
+                                             int grp, int ks) {
   constexpr int W = 8, MT = NM * T, PW = MT / W;
   static_assert(MT % W == 0, "whole (matrix, tile) pairs per wave");
   // LDS: the rings, then the slice's decode pack (fragments, min-term
@@ -1252,9 +1280,7 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
   constexpr int kPackChunks = (kFragBytes + kXsBytes + kDscBytes) / 16;
   constexpr int kSlots = DP * PW;                // ring slots per wave
   constexpr int kRingBytes = W * kSlots * kTileBlockBytes;
-  static_assert(kRingBytes + kFragBytes + kXsBytes + kDscBytes + 64 <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kRingBytes + kFragBytes + kXsBytes + kDscBytes];
-  __shared__ int s_last;
+  static_assert(kRingBytes + kFragBytes + kXsBytes + kDscBytes == splitk_lds_bytes<NM, T, BPS, DP>(), "LDS layout");
   u4_t* const xf = reinterpret_cast<u4_t*>(lds + kRingBytes);
   _Float16* const xs = reinterpret_cast<_Float16*>(lds + kRingBytes + kFragBytes);
   const float* const dscl = reinterpret_cast<const float*>(lds + kRingBytes + kFragBytes + kXsBytes);
@@ -1262,8 +1288,6 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int sidx = (int)blockIdx.x >> 3;
-  const int ks = sidx % KS, grp = ((int)blockIdx.x & 7) + 8 * (sidx / KS);
   const int nb = a.nb, kb0 = ks * BPS;
   uint8_t* const ring = lds + (size_t)wave * kSlots * kTileBlockBytes;
   const uint32_t ring0 = lds_addr(ring);
@@ -1294,11 +1318,11 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
   constexpr int PPW = BPS * 8 / W;  // (block, row) pairs per wave
   static_assert(BPS * 8 % W == 0, "whole pairs per wave");
   const OutT* const xin = reinterpret_cast<const OutT*>(a.x);
-  // Ordinary loads: the compiler waits for them (vmcnt(0), which also covers
-  // the weight prologue issued meanwhile) before their first use.  Loads
-  // issued as asm would save that wait but leave their destinations open to
-  // register copies made before the data arrives.
   float xv[PPW][4];
+  // Ordinary loads: the compiler waits for them (vmcnt(0), which also
+  // covers the weight prologue issued meanwhile) before their first use.
+  // Loads issued as asm would save that wait but leave their destinations
+  // open to register copies made before the data arrives.
 #pragma unroll
   for (int j = 0; j < PPW; ++j) {
     const int pr = wave + W * j, r = pr & 7;
@@ -1400,9 +1424,9 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0)
-    s_last = atomicAdd(&counters[grp], 1) == KS - 1;
+    *s_last = count_arrival(&counters[grp]) == KS - 1;
   __syncthreads();
-  if (!s_last)
+  if (!*s_last)
     return;
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
@@ -1445,8 +1469,19 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
     store_elem(y, off, out);
   }
   if (tid == 0)
-    atomicExch(&counters[grp], 0);  // ready for the next launch
+    reset_counter(&counters[grp]);  // ready for the next launch
 }
+
+// Workgroup b: slice (b / 8) % KS of group (b % 8) + 8 ((b / 8) / KS), so the
+// KS slices of a group run on one XCD (b % 8).
+template <int NM, int T, int KS, int BPS, int DP, typename OutT>
+__global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float* __restrict__ part, int* __restrict__ counters) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[splitk_lds_bytes<NM, T, BPS, DP>()];
+  __shared__ int s_last;
+  const int sidx = (int)blockIdx.x >> 3;
+  splitk_slice<NM, T, KS, BPS, DP, OutT>(a, lds, &s_last, part, counters, ((int)blockIdx.x & 7) + 8 * (sidx / KS), sidx % KS);
+}
+
 
 // ----------------------------------------------------------------------------
 // GEMM (prefill).  Workgroup tile 128 x 128, 4 waves of 64 x 64, k-step 64

@@ -160,10 +160,14 @@ def mlp_gate_up(x, gate, up, count, output, query_counts=None, stream=None):
 
 
 def mlp(x, gate, up, down, hidden, gate_buffer, count, query_counts=None, stream=None):
-    """MLP of Ops::decoder (forward.cpp:115-119): gate/up into gate_buffer,
-    then down with the residual added in place into ``hidden``."""
-    mlp_gate_up(x, gate, up, count, gate_buffer, query_counts=query_counts, stream=stream)
-    return linear(gate_buffer, down, count, hidden, auxiliary=hidden, query_counts=query_counts, stream=stream)
+    """MLP of Ops::decoder (forward.cpp:114-119): gate/up into gate_buffer,
+    then down with the residual added in place into ``hidden`` (q4k_mlp)."""
+    dt = _dtype_code(x)
+    counts, nq = u32_array(query_counts if query_counts is not None else [count])
+    check(lib.q4k_mlp(_stream(stream), gate.handle, up.handle, down.handle, _ptr(x), _ptr(gate_buffer), _ptr(hidden), count,
+                      counts, nq, dt))
+    return hidden
+
 
 
 def gather_rows(x, out, counts, samples, stream=None):
