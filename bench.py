@@ -129,6 +129,20 @@ def decode_bench(args, dev):
     q4k.profile_enable(False)
     steps = args.steps
 
+    # The decoder's MLP block as the reference runs it (forward.cpp:114-119):
+    # x = hidden with the layer's ffn_norm, which the fused gate/up GEMV
+    # applies on the way in (no separate rms_norm launch).
+    norm_w = torch.full((K,), 0.05, device=dev)
+    h_block = torch.randn(M, K, device=dev)
+    q4k.profile_enable(True)
+    for i in range(args.steps):
+        G, U, D = sets[i % len(sets)]
+        q4k.mlp(h_block, G, U, D, h_block, gate, M, query_counts=counts, norm_weight=norm_w)
+    torch.cuda.synchronize()
+    gated_norm_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMV_GATED)
+    aux_ms, aux_n = kernel_avg_ms(q4k, q4k.KERNEL_AUX)
+    q4k.profile_enable(False)
+
     wbytes = 2 * q4k_bytes(N, K) + q4k_bytes(K, N)
     act = 4 * (M * K + M * N)  # gate/up: x in, gate buffer out
     act += 4 * (M * N + 2 * M * K)  # down: gate buffer in, residual in + out
@@ -144,6 +158,8 @@ def decode_bench(args, dev):
                   "gbs": gated_bytes / (gated_ms * 1e-3) / 1e9},
         "down": {"avg_us": down_ms * 1e3, "bytes": down_bytes, "gbs": down_bytes / (down_ms * 1e-3) / 1e9},
         "stage_launches": stage_n,
+        "gated_norm_us": gated_norm_ms * 1e3,
+        "norm_launches": aux_n,
         "weight_sets_mb": len(sets) * wbytes / 1e6,
     }
 
@@ -426,6 +442,10 @@ def main():
             "down_gemv_gbs": round(dec["down"]["gbs"], 1),
             # activation staging launches per step (none: both GEMVs pack x themselves)
             "stage_launches_per_step": dec["stage_launches"] / dec["steps"],
+            # the same gate/up launch with the layer's ffn_norm applied inside it (x = hidden);
+            # no separate RMS-norm launch runs (norm_launches_per_step)
+            "gate_up_gemv_with_ffn_norm_us": round(dec["gated_norm_us"], 3),
+            "norm_launches_per_step": dec["norm_launches"] / dec["steps"],
         },
         "shard_1of8": shard,
         "neighbours": neighbours,

@@ -108,12 +108,16 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
                     uint32_t nqueries, uint32_t dtype);
 
 /* The MLP of Ops::decoder (model/qwen35/forward.cpp:114-119):
- *   gate = silu(x.Wg^T) * (x.Wu^T)          [m, n]  (the gate buffer)
+ *   xn = norm_w ? rms_norm(x, norm_w, eps) : x    (native_ops.metal:6-40)
+ *   gate = silu(xn.Wg^T) * (xn.Wu^T)        [m, n]  (the gate buffer)
  *   hidden = hidden + gate.Wd^T              [m, k]  (post 1, in place)
- * with wg, wu n x k and wd k x n: q4k_mlp_gate_up, then q4k_linear with
- * post 1.  x, the gate buffer and hidden must not overlap. */
-int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const void* x, void* gate, void* hidden, uint32_t m,
-            const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype);
+ * with wg, wu n x k, wd k x n and norm_w k fp32 values (or NULL).  The
+ * decoder passes x = hidden with the layer's ffn_norm; for decode passes
+ * that the fused gate/up GEMV takes (m <= 8, k = 4096) the norm runs inside
+ * it, otherwise into a workspace buffer first.  The gate buffer must not
+ * overlap x or hidden; x may equal hidden. */
+int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const float* norm_w, float eps, const void* x, void* gate, void* hidden,
+            uint32_t m, const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype);
 
 /* Phase Ops::linear would use for this batch (forward.cpp:52,190). */
 int q4k_select_phase(const uint32_t* query_counts, uint32_t nqueries, uint32_t m, int gated, uint32_t* phase);

@@ -56,7 +56,7 @@ def _load():
         "q4k_weight_prepare": (c_int, [p, u32]),
         "q4k_linear": (c_int, [p, p, p, p, p, u32, pu32, u32, u32, u32]),
         "q4k_mlp_gate_up": (c_int, [p, p, p, p, p, u32, pu32, u32, u32]),
-        "q4k_mlp": (c_int, [p, p, p, p, p, p, p, u32, pu32, u32, u32]),
+        "q4k_mlp": (c_int, [p, p, p, p, p, ctypes.c_float, p, p, p, u32, pu32, u32, u32]),
         "q4k_select_phase": (c_int, [pu32, u32, u32, c_int, pu32]),
         "q4k_pack_queries": (c_int, [pu32, pu32, u32, pu32, pu32, pu32, pu32]),
         "q4k_gather_rows": (c_int, [p, p, p, u32, pu32, pu32, u32, u32, pu32]),

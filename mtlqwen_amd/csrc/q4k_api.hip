@@ -79,6 +79,8 @@ struct Workspace {
   size_t counter_elems = 0;
   uint8_t* pack = nullptr;  // decode pack of x (m <= 8)
   size_t pack_bytes = 0;
+  void* normed = nullptr;  // q4k_mlp's RMS-normalised x when the norm is not fused
+  size_t normed_bytes = 0;
   std::vector<void*> retired;
 };
 
@@ -295,6 +297,19 @@ int ensure_splitk_workspace(Workspace& ws, int device, size_t part_floats, size_
     Q4K_TRY_HIP(hipMemset(ws.counters, 0, n * sizeof(int)), "hipMemset");
     ws.counter_elems = n;
   }
+  return Q4K_OK;
+}
+
+int ensure_normed_workspace(Workspace& ws, int device, size_t bytes) {
+  if (ws.normed_bytes >= bytes)
+    return Q4K_OK;
+  if (ws.normed)
+    ws.retired.push_back(ws.normed);
+  ws.normed = nullptr;
+  ws.normed_bytes = 0;
+  if (hipMalloc(&ws.normed, bytes) != hipSuccess)
+    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte normalised-activation buffer on device %d", bytes, device);
+  ws.normed_bytes = bytes;
   return Q4K_OK;
 }
 
@@ -736,8 +751,8 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
   return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, false);
 }
 
-int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const void* x, void* gate, void* hidden, uint32_t m,
-            const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype) {
+int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const float* norm_w, float eps, const void* x, void* gate, void* hidden,
+            uint32_t m, const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype) {
   if (!wg || !wu || !wd)
     return fail(Q4K_EINVAL, "gate, up and down weights must be non-NULL");
   if (wg->n != wu->n || wg->k != wu->k || wg->device != wu->device)
@@ -750,6 +765,8 @@ int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const 
     return fail(Q4K_ESHAPE, "m must be positive");
   if (!x || !gate || !hidden)
     return fail(Q4K_EINVAL, "x, gate and hidden must be non-NULL");
+  if (norm_w && !(eps >= 0.0f))
+    return fail(Q4K_EINVAL, "eps must be a non-negative number");
   int rc = check_counts(query_counts, nqueries, m);
   if (rc)
     return rc;
@@ -757,11 +774,55 @@ int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const 
   const size_t xb = (size_t)m * wg->k * es, gb = (size_t)m * wg->n * es, hb = (size_t)m * wd->n * es;
   if (overlaps(x, xb, gate, gb) || overlaps(gate, gb, hidden, hb))
     return fail(Q4K_EALIAS, "the gate buffer must not overlap x or hidden");
-  if (overlaps(x, xb, hidden, hb))
-    return fail(Q4K_EALIAS, "x must not overlap hidden");
+  if (x != hidden && overlaps(x, xb, hidden, hb))
+    return fail(Q4K_EALIAS, "x must equal hidden or not overlap it");
+  rc = set_device(wg->device);
+  if (rc)
+    return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t phase = phase_of(query_counts, nqueries, m, true);
+  const void* xin = x;
+  if (norm_w) {
+    if (phase == Q4K_PHASE_GATED_DECODE && gemv_gate_up_supported((int)m, (int)(wg->k / 256), (int)wg->n)) {
+      // The norm runs inside the fused gate/up GEMV (forward.cpp:114-118 in one launch).
+      resolve(wg, phase);
+      resolve(wu, phase);
+      GemvArgs a{};
+      a.w = wg->data;
+      a.wu = wu->data;
+      a.x = x;
+      a.y = gate;
+      a.m = (int)m;
+      a.n = (int)wg->n;
+      a.k = (int)wg->k;
+      a.nb = (int)(wg->k / 256);
+      a.rows = 2 * (int)m;
+      a.split = 1;
+      a.norm_w = norm_w;
+      a.eps = eps;
+      {
+        LaunchTimer timer(s, Q4K_KERNEL_GEMV_GATED);
+        Q4K_TRY_HIP(launch_gemv_gate_up(s, a, (int)dtype, device_cus(wg->device)), "gemv gate/up launch");
+      }
+      return q4k_linear(stream, wd, gate, hidden, hidden, m, query_counts, nqueries, Q4K_POST_ADD, dtype);
+    }
+    // Otherwise rms_norm (forward.cpp:114) into the workspace first.
+    Workspace& ws = workspace(wg->device);
+    {
+      std::lock_guard<std::mutex> lock(ws.mu);
+      rc = ensure_normed_workspace(ws, wg->device, xb);
+    }
+    if (rc)
+      return rc;
+    rc = q4k_rms_norm(stream, x, norm_w, ws.normed, m, wg->k, eps, dtype);
+    if (rc)
+      return rc;
+    xin = ws.normed;
+  }
   // forward.cpp:115-119 as two calls: gate/up into the gate buffer, then down
-  // with the residual added in place.
-  rc = q4k_mlp_gate_up(stream, wg, wu, x, gate, m, query_counts, nqueries, dtype);
+  // with the residual added in place.  (Stream order: the gate/up kernel has
+  // read all of x before the down projection writes hidden, so x may be hidden.)
+  rc = q4k_mlp_gate_up(stream, wg, wu, xin, gate, m, query_counts, nqueries, dtype);
   if (rc)
     return rc;
   return q4k_linear(stream, wd, gate, hidden, hidden, m, query_counts, nqueries, Q4K_POST_ADD, dtype);

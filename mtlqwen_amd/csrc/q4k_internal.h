@@ -60,6 +60,10 @@ struct GemvArgs {
   int m, n, k, nb, post;
   int rows;  // staged fragment rows: 2m when split (rows m.. hold the low parts), else m
   int split;
+  // Fused gate/up GEMV only: when non-null, x is RMS-normalised first,
+  // x * rsqrt(sum(x^2) / k + eps) * norm_w (native_ops.metal:6-40).
+  const float* norm_w = nullptr;
+  float eps = 0.0f;
 };
 
 struct GemmArgs {
@@ -121,7 +125,7 @@ bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus);
 hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus);
 
 // Fused gate/up GEMV for m <= 8 rows and K = 4096 that packs x itself (no
-// staging launch); reads a.x, a.w, a.wu and writes a.y.
+// staging launch); reads a.x, a.w, a.wu (and a.norm_w when set) and writes a.y.
 bool gemv_gate_up_supported(int m, int nb, int n);
 hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus);
 

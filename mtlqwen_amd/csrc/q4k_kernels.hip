@@ -1079,9 +1079,13 @@ constexpr int kGuXRow = 36;
 constexpr int kGuWaveFloats = 2 * 64 * kGuXRow;
 
 // One item (T column tiles of both matrices) of the fused gate/up GEMV, by the
-// 8 waves of the workgroup, over kGuLdsBytes of LDS.
-template <int T, typename OutT>
-__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], int item) {
+// 8 waves of the workgroup.  NORM: x is RMS-normalised on the way in
+// (native_ops.metal:6-40, the norm forward.cpp:114 applies before the MLP):
+// the 8 waves hold all of x between them, so each row's sum of squares is
+// their partial sums (ssq [wave][row]) added after one barrier, and every
+// element becomes (x * rsqrt(sum / k + eps)) * w before the pack.
+template <int T, typename OutT, bool NORM>
+__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int item) {
   constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT;
   constexpr int kXRow = kGuXRow;
   static_assert(MT * 8 * 16 <= BPW * 64 * kXRow, "partials fit the x region");
@@ -1111,6 +1115,12 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
           xv[j][r][e] = (float)v4[e];
       }
     }
+  f4_t nw[BPW];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+      nw[j] = *reinterpret_cast<const f4_t*>(a.norm_w + (size_t)(bw + j) * 256 + 4 * lane);
+  }
   // Units are loaded into registers DQ ahead of the one being computed
   // (header dword, then the two quant slabs; the scheduling barriers keep
   // the issue order: x first, then unit by unit).  A shallow window keeps
@@ -1133,6 +1143,42 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
   for (int u = 0; u < (DQ < U ? DQ : U); ++u)
     issue_unit(u);
 
+  if constexpr (NORM) {
+    float ss[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      ss[r] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < BPW; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ss[r] = fmaf(xv[j][r][e], xv[j][r][e], ss[r]);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1)
+        ss[r] += __shfl_xor(ss[r], off);
+    }
+    if (lane < 8) {
+      float v = ss[0];
+#pragma unroll
+      for (int r = 1; r < 8; ++r)
+        v = lane == r ? ss[r] : v;
+      ssq[wave][lane] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        tot += ssq[w][r];
+      const float scale = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+#pragma unroll
+      for (int j = 0; j < BPW; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xv[j][r][e] = (xv[j][r][e] * scale) * nw[j][e];
+    }
+  }
   // Element e = 4 lane of row r goes to pack lane 16 (e / 64) + r + 8 ((e / 32) & 1),
   // float (e & 31) of its 32.
   float* const xw = xl[wave];
@@ -1221,10 +1267,11 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
   }
 }
 
-template <int T, typename OutT>
+template <int T, typename OutT, bool NORM>
 __global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
   __shared__ __attribute__((aligned(16))) float xl[8][kGuWaveFloats];
-  gate_up_item<T, OutT>(a, xl, blockIdx.x);
+  __shared__ float ssq[8][8];
+  gate_up_item<T, OutT, NORM>(a, xl, ssq, blockIdx.x);
 }
 
 // ----------------------------------------------------------------------------
@@ -2211,24 +2258,24 @@ bool gemv_gate_up_supported(int m, int nb, int n) {
   return enabled && m >= 1 && m <= 8 && nb == 16 && n % 16 == 0;
 }
 
+template <int T, bool NORM>
+hipError_t gate_up_launch(hipStream_t s, const GemvArgs& a, int dtype, unsigned grid) {
+  if (dtype == kF32)
+    (void)dispatch(q4k_gemv_gate_up_kernel<T, float, NORM>, dim3(grid), dim3(512), s, a);
+  else
+    (void)dispatch(q4k_gemv_gate_up_kernel<T, _Float16, NORM>, dim3(grid), dim3(512), s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
   // Three column tiles per workgroup while that still gives every CU one
   // workgroup (N = 12288: 256); otherwise one.
   const int ctiles = a.n / 16;
   const bool t3 = ctiles % 3 == 0 && ctiles / 3 >= cus;
-  const dim3 grid((unsigned)(t3 ? ctiles / 3 : ctiles)), block(512);
-  if (t3) {
-    if (dtype == kF32)
-      (void)dispatch(q4k_gemv_gate_up_kernel<3, float>, grid, block, s, a);
-    else
-      (void)dispatch(q4k_gemv_gate_up_kernel<3, _Float16>, grid, block, s, a);
-  } else {
-    if (dtype == kF32)
-      (void)dispatch(q4k_gemv_gate_up_kernel<1, float>, grid, block, s, a);
-    else
-      (void)dispatch(q4k_gemv_gate_up_kernel<1, _Float16>, grid, block, s, a);
-  }
-  return hipGetLastError();
+  const unsigned grid = (unsigned)(t3 ? ctiles / 3 : ctiles);
+  if (a.norm_w)
+    return t3 ? gate_up_launch<3, true>(s, a, dtype, grid) : gate_up_launch<1, true>(s, a, dtype, grid);
+  return t3 ? gate_up_launch<3, false>(s, a, dtype, grid) : gate_up_launch<1, false>(s, a, dtype, grid);
 }
 
 bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus) {

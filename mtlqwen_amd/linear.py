@@ -159,15 +159,19 @@ def mlp_gate_up(x, gate, up, count, output, query_counts=None, stream=None):
     return output
 
 
-def mlp(x, gate, up, down, hidden, gate_buffer, count, query_counts=None, stream=None):
-    """MLP of Ops::decoder (forward.cpp:114-119): gate/up into gate_buffer,
-    then down with the residual added in place into ``hidden`` (q4k_mlp)."""
+def mlp(x, gate, up, down, hidden, gate_buffer, count, query_counts=None, stream=None, norm_weight=None, eps=1e-6):
+    """MLP of Ops::decoder (forward.cpp:114-119): optionally the RMS norm of
+    ``x`` with ``norm_weight`` (fp32 [k]), then gate/up into gate_buffer,
+    then down with the residual added in place into ``hidden`` (q4k_mlp).
+    ``x`` may be ``hidden`` (the decoder passes the residual stream and
+    the layer's ffn_norm)."""
     dt = _dtype_code(x)
     counts, nq = u32_array(query_counts if query_counts is not None else [count])
-    check(lib.q4k_mlp(_stream(stream), gate.handle, up.handle, down.handle, _ptr(x), _ptr(gate_buffer), _ptr(hidden), count,
-                      counts, nq, dt))
+    if norm_weight is not None:
+        _check_norm_weight(norm_weight, x.shape[-1])
+    check(lib.q4k_mlp(_stream(stream), gate.handle, up.handle, down.handle, _ptr(norm_weight), float(eps), _ptr(x),
+                      _ptr(gate_buffer), _ptr(hidden), count, counts, nq, dt))
     return hidden
-
 
 
 def gather_rows(x, out, counts, samples, stream=None):

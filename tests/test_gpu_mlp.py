@@ -112,3 +112,31 @@ def test_prefill_phase_pass(q4k, oracle, gpu, mlp_weights):
     q4k.mlp(torch.from_numpy(x).to(gpu), G, U, D, hidden, gate, m, query_counts=[6, 6])
     torch.cuda.synchronize()
     _check(oracle, x, h0, gate, hidden, w)
+
+
+@pytest.mark.parametrize("m,counts,dtype", [(8, [1] * 8, torch.float32), (3, [1, 1, 1], torch.float32),
+                                            (12, [6, 6], torch.float32), (4, [1] * 4, torch.float16)])
+def test_mlp_block_with_ffn_norm(q4k, oracle, gpu, mlp_weights, m, counts, dtype):
+    """The decoder's MLP block as the reference runs it (forward.cpp:114-119):
+    x = hidden, the layer's ffn_norm applied first -- inside the fused
+    gate/up GEMV for decode passes, as a separate RMS norm otherwise."""
+    (wg, wu, wd), (G, U, D) = mlp_weights
+    rng = np.random.default_rng(1000 + m)
+    h0 = make_x(rng, m, K, 3.0)
+    h0[0] *= 50.0
+    # ffn_norm weights of a size that keeps SiLU(gate) * up and the down
+    # projection's outputs within fp16 range for these synthetic weights.
+    scale = 0.005 if dtype == torch.float16 else 0.05
+    norm = (scale * (1.0 + 0.2 * rng.standard_normal(K))).astype(np.float32)
+    if dtype == torch.float16:
+        h0 = h0.astype(np.float16)
+    hidden = torch.from_numpy(h0).to(gpu)
+    gate = torch.empty((m, N), device=gpu, dtype=dtype)
+    q4k.mlp(hidden, G, U, D, hidden, gate, m, query_counts=counts, norm_weight=torch.from_numpy(norm).to(gpu))
+    torch.cuda.synchronize()
+    xn = oracle.rms_norm(h0, norm)
+    g_ref = oracle.mlp_gate_up(xn, wg, wu, N, K)
+    g_gpu = gate.cpu().numpy()
+    assert row_rel_err(g_gpu.astype(np.float32), g_ref.astype(np.float32)) <= TOL
+    ref = oracle.linear(g_gpu, wd, K, N, aux=h0, post=1)
+    assert row_rel_err(hidden.cpu().numpy().astype(np.float32), ref.astype(np.float32)) <= TOL
