@@ -30,7 +30,7 @@ extern "C" {
 
 #define Q4K_OK 0
 #define Q4K_EINVAL (-1) /* null pointer, bad post code, bad dtype, bad count table */
-#define Q4K_ETYPE (-2)  /* ggml type other than Q4_K */
+#define Q4K_ETYPE (-2)  /* ggml type other than Q4_K / Q6_K (or not Q4_K where only Q4_K is served) */
 #define Q4K_ESHAPE (-3) /* k % 256 != 0, n % 16 != 0, m out of range, byte count mismatch */
 #define Q4K_EALIAS (-4) /* x overlaps y (aux may alias y) */
 #define Q4K_EHIP (-5)   /* HIP runtime failure */
@@ -39,6 +39,7 @@ extern "C" {
 #define Q4K_ENOTFOUND (-8) /* missing file, tensor or metadata key */
 
 #define Q4K_GGML_TYPE_Q4_K 12u
+#define Q4K_GGML_TYPE_Q6_K 14u /* the Q6_K LM head / mixed-type files (quant_linear.metal:69-86,437-497) */
 
 #define Q4K_DTYPE_F32 0u
 #define Q4K_DTYPE_F16 1u
@@ -66,10 +67,13 @@ typedef struct q4k_weight q4k_weight;
 const char* q4k_last_error(void);
 
 /* Upload one GGUF tensor of type Q4_K (n rows of k/256 block_q4_K records,
- * 144 B each; ggml ne[0] = k, ne[1] = n) to device `device`.  The bytes are
- * re-laid out for the kernels during the upload; the caller's buffer is not
- * retained.  Replaces the zero-copy Weight view built by loadWeights
- * (model/qwen35/forward.cpp:12-23, qwen35.hpp:34-37). */
+ * 144 B each) or Q6_K (block_q6_K, 210 B each); ggml ne[0] = k, ne[1] = n.
+ * The bytes are re-laid out for the kernels during the upload; the caller's
+ * buffer is not retained.  Replaces the zero-copy Weight view built by
+ * loadWeights (model/qwen35/forward.cpp:12-23, qwen35.hpp:34-37), whose
+ * Weight keys its kernels on the type (forward.cpp:55-57).  Q6_K weights
+ * serve q4k_linear and the two-call form of the gated projection; the fused
+ * gate/up kernel and q4k_embedding take Q4_K only (Q4K_ETYPE otherwise). */
 int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device, q4k_weight** out);
 
 /* Same, from bytes already in device memory of `device` (GGUF order). */
@@ -227,6 +231,10 @@ int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops);
  * n * (k / 256) * 144 bytes. */
 int q4k_relayout_host(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k);
 int q4k_unrelayout_host(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k);
+
+/* Same for ggml type Q4_K or Q6_K (n * (k / 256) * 144 or 210 bytes). */
+int q4k_relayout_host_typed(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k, uint32_t ggml_type);
+int q4k_unrelayout_host_typed(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k, uint32_t ggml_type);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,8 @@ EFORMAT = -7
 ENOTFOUND = -8
 
 GGML_TYPE_Q4_K = 12
+GGML_TYPE_Q6_K = 14
+BLOCK_BYTES_BY_TYPE = {GGML_TYPE_Q4_K: 144, GGML_TYPE_Q6_K: 210}
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 POST_STORE, POST_ADD, POST_GATE = 0, 1, 2
@@ -78,6 +80,8 @@ def _load():
         "q4k_gguf_meta_str": (c_int, [p, ctypes.c_char_p, ctypes.c_char_p, size_t]),
         "q4k_weight_from_gguf": (c_int, [p, ctypes.c_char_p, c_int, ctypes.POINTER(p)]),
         "q4k_unrelayout_host": (c_int, [p, p, u32, u32]),
+        "q4k_relayout_host_typed": (c_int, [p, p, u32, u32, u32]),
+        "q4k_unrelayout_host_typed": (c_int, [p, p, u32, u32, u32]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)

@@ -151,17 +151,21 @@ size_t q4k_bytes(uint32_t n, uint32_t k) {
   return (size_t)n * (k / 256) * kBlockBytes;
 }
 
+size_t type_bytes(uint32_t n, uint32_t k, uint32_t type) {
+  return (size_t)n * (k / 256) * (type == Q4K_GGML_TYPE_Q6_K ? kQ6BlockBytes : kBlockBytes);
+}
+
 int check_shape(uint32_t n, uint32_t k, uint32_t type, size_t bytes) {
-  if (type != Q4K_GGML_TYPE_Q4_K)
-    return fail(Q4K_ETYPE, "unsupported ggml type %u (only Q4_K = 12)", type);
+  if (type != Q4K_GGML_TYPE_Q4_K && type != Q4K_GGML_TYPE_Q6_K)
+    return fail(Q4K_ETYPE, "unsupported ggml type %u (Q4_K = 12 or Q6_K = 14)", type);
   if (n == 0 || k == 0 || k % 256 != 0)
     return fail(Q4K_ESHAPE, "k must be a positive multiple of 256 (got k=%u, n=%u)", k, n);
   if (n % 16 != 0)
     return fail(Q4K_ESHAPE, "n must be a multiple of 16 (got %u)", n);
-  if ((size_t)(k / 256) * kTileBlockBytes > 0x7fffffffull / 16)
+  if ((size_t)(k / 256) * kQ6TileBlockBytes > 0x7fffffffull / 16)
     return fail(Q4K_ESHAPE, "k too large (%u)", k);
-  if (bytes != q4k_bytes(n, k))
-    return fail(Q4K_ESHAPE, "byte count %zu does not match n=%u k=%u (expected %zu)", bytes, n, k, q4k_bytes(n, k));
+  if (bytes != type_bytes(n, k, type))
+    return fail(Q4K_ESHAPE, "byte count %zu does not match n=%u k=%u (expected %zu)", bytes, n, k, type_bytes(n, k, type));
   return Q4K_OK;
 }
 
@@ -204,6 +208,58 @@ void relayout(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, bool for
     }
 }
 
+// Host form of the Q6_K tiled layout (q4k_internal.h); `forward` selects
+// GGUF -> tiled, else tiled -> GGUF.
+void relayout_q6(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, bool forward) {
+  const uint32_t nb = k / 256;
+  for (uint32_t c = 0; c < n / 16; ++c)
+    for (uint32_t b = 0; b < nb; ++b) {
+      const size_t tb = ((size_t)c * nb + b) * kQ6TileBlockBytes;
+      for (uint32_t l = 0; l < 64; ++l) {
+        const uint32_t i = l & 15, g = l >> 4;
+        const size_t blk = ((size_t)(16 * c + i) * nb + b) * kQ6BlockBytes;
+        uint32_t wd[12] = {0};
+        if (forward) {
+          for (int o = 0; o < 32; ++o)
+            for (int hf = 0; hf < 2; ++hf)
+              q6_place(wd, o, hf, q6_quant(src + blk, q6_elem((int)g, o, hf)));
+          for (int s = 0; s < 3; ++s)
+            std::memcpy(dst + tb + s * 1024 + 16 * l, wd + 4 * s, 16);
+          for (int j = 0; j < 4; ++j)
+            dst[tb + kQ6ScaleOffset + 4 * l + j] = (uint8_t)(src[blk + 192 + 4 * g + j] ^ 0x80u);
+          if (g == 0)
+            std::memcpy(dst + tb + kQ6DOffset + 2 * i, src + blk + 208, 2);
+        } else {
+          for (int s = 0; s < 3; ++s)
+            std::memcpy(wd + 4 * s, src + tb + s * 1024 + 16 * l, 16);
+          uint8_t* out = dst + blk;
+          for (int o = 0; o < 32; ++o)
+            for (int hf = 0; hf < 2; ++hf) {
+              // Inverse of q6_quant's addressing for element e.
+              const int e = q6_elem((int)g, o, hf), h = e >> 7, rr = e & 127, ll = rr & 31;
+              const uint32_t v = q6_take(wd, o, hf);
+              uint8_t& qb = out[64 * h + (rr & 32) + ll];
+              qb = (rr & 64) ? (uint8_t)((qb & 0x0Fu) | ((v & 15u) << 4)) : (uint8_t)((qb & 0xF0u) | (v & 15u));
+              uint8_t& hb = out[128 + 32 * h + ll];
+              const int sh = 2 * (rr >> 5);
+              hb = (uint8_t)((hb & ~(3u << sh)) | ((v >> 4) << sh));
+            }
+          for (int j = 0; j < 4; ++j)
+            out[192 + 4 * g + j] = (uint8_t)(src[tb + kQ6ScaleOffset + 4 * l + j] ^ 0x80u);
+          if (g == 0)
+            std::memcpy(out + 208, src + tb + kQ6DOffset + 2 * i, 2);
+        }
+      }
+    }
+}
+
+void relayout_typed(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type, bool forward) {
+  if (type == Q4K_GGML_TYPE_Q6_K)
+    relayout_q6(src, dst, n, k, forward);
+  else
+    relayout(src, dst, n, k, forward);
+}
+
 // forward.cpp:52 with the decode flag accumulated as in forward.cpp:190.
 uint32_t phase_of(const uint32_t* counts, uint32_t nq, uint32_t m, bool gated) {
   bool decode = true;
@@ -238,8 +294,11 @@ Kernel& resolve(q4k_weight* w, uint32_t phase) {
   if (k.kind == kNone) {
     const char* suffix[] = {"decode", "prefill", "prefill_small", "gate_up_decode"};
     k.kind = phase == Q4K_PHASE_GATED_DECODE ? kGemvGated : phase == Q4K_PHASE_PREFILL ? kGemm : kGemv;
-    k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + "q4_k_k" + std::to_string(w->k) + "_n" + std::to_string(w->n) +
-             "_" + suffix[phase] + (k.kind == kGemm ? "_mfma32x32x16" : "_mfma16x16x32");
+    const bool q6 = w->type == Q4K_GGML_TYPE_Q6_K;
+    if (q6 && k.kind == kGemm)
+      k.kind = kGemv;  // Q6_K prefill: the GEMV per group of 8 rows
+    k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + (q6 ? "q6_k_k" : "q4_k_k") + std::to_string(w->k) + "_n" +
+             std::to_string(w->n) + "_" + suffix[phase] + (k.kind == kGemm ? "_mfma32x32x16" : q6 && phase == Q4K_PHASE_PREFILL ? "_mfma16x16x32_rows8" : "_mfma16x16x32");
   }
   return k;
 }
@@ -392,8 +451,43 @@ int set_device(int device) {
 // previous call, which must have been a projection of the same x with the
 // same (m, k, n) under the same lock; the decode pack and split-K paths always
 // stage (they are not reached by such pairs).
+// Q6_K projection (wu == nullptr): per group of up to 8 rows, the decode pack
+// of the group's x, then the Q6_K GEMV over the group's rows of y and aux.
+int run_q6k_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
+                   uint32_t dtype) {
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  for (uint32_t r0 = 0; r0 < m; r0 += 8) {
+    const uint32_t mg = m - r0 < 8u ? m - r0 : 8u;
+    const void* xg = static_cast<const uint8_t*>(x) + (size_t)r0 * w->k * es;
+    GemvArgs a{};
+    int rc = stage_pack(stream, ws, w->device, xg, dtype, mg, w->k, &a.pack);
+    if (rc)
+      return rc;
+    a.w = w->data;
+    a.x = xg;
+    a.y = static_cast<uint8_t*>(y) + (size_t)r0 * w->n * es;
+    a.aux = aux ? static_cast<const uint8_t*>(aux) + (size_t)r0 * w->n * es : nullptr;
+    a.m = (int)mg;
+    a.n = (int)w->n;
+    a.k = (int)w->k;
+    a.nb = (int)(w->k / 256);
+    a.post = (int)post;
+    a.rows = 2 * (int)mg;
+    a.split = 1;
+    LaunchTimer timer(stream, Q4K_KERNEL_GEMV);
+    Q4K_TRY_HIP(launch_q6k_gemv(stream, a, (int)dtype, device_cus(w->device)), "q6_k gemv launch");
+  }
+  return Q4K_OK;
+}
+
 int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m,
                       uint32_t post, uint32_t dtype, uint32_t phase, bool restage) {
+  if (w->type == Q4K_GGML_TYPE_Q6_K) {
+    if (wu)
+      return fail(Q4K_ETYPE, "the fused gate/up kernel takes Q4_K weights");
+    resolve(w, phase);
+    return run_q6k_locked(stream, ws, w, x, y, aux, m, post, dtype);
+  }
   Kernel& kern = resolve(w, phase);
   if (wu)
     resolve(wu, phase);
@@ -549,6 +643,28 @@ int q4k_unrelayout_host(const void* tiled, void* gguf_bytes, uint32_t n, uint32_
   return Q4K_OK;
 }
 
+int q4k_relayout_host_typed(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k, uint32_t ggml_type) {
+  if (!gguf_bytes || !tiled)
+    return fail(Q4K_EINVAL, "null buffer");
+  int rc = check_shape(n, k, ggml_type, type_bytes(n, k, ggml_type));
+  if (rc)
+    return rc;
+  relayout_typed(static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(tiled), n, k, ggml_type, true);
+  return Q4K_OK;
+}
+
+int q4k_unrelayout_host_typed(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k, uint32_t ggml_type) {
+  if (!gguf_bytes || !tiled)
+    return fail(Q4K_EINVAL, "null buffer");
+  int rc = check_shape(n, k, ggml_type, type_bytes(n, k, ggml_type));
+  if (rc)
+    return rc;
+  if (ggml_type == Q4K_GGML_TYPE_Q6_K)
+    std::memset(gguf_bytes, 0, type_bytes(n, k, ggml_type));  // the inverse merges bit fields into place
+  relayout_typed(static_cast<const uint8_t*>(tiled), static_cast<uint8_t*>(gguf_bytes), n, k, ggml_type, false);
+  return Q4K_OK;
+}
+
 int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device, q4k_weight** out) {
   if (!out)
     return fail(Q4K_EINVAL, "out is NULL");
@@ -564,7 +680,7 @@ int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t
   if (rc)
     return rc;
   std::vector<uint8_t> tiled(bytes);
-  relayout(static_cast<const uint8_t*>(gguf_bytes), tiled.data(), n, k, true);
+  relayout_typed(static_cast<const uint8_t*>(gguf_bytes), tiled.data(), n, k, ggml_type, true);
   q4k_weight* w = new (std::nothrow) q4k_weight;
   if (!w)
     return fail(Q4K_ENOMEM, "host allocation failed");
@@ -615,7 +731,8 @@ int q4k_weight_create_from_device(const void* gguf_device_bytes, size_t bytes, u
     return fail(Q4K_ENOMEM, "cannot allocate %zu bytes of weights on device %d", bytes, device);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k);
+  hipError_t e = ggml_type == Q4K_GGML_TYPE_Q6_K ? launch_q6k_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k)
+                                                 : launch_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k);
   if (e == hipSuccess)
     e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
@@ -735,11 +852,11 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
     return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint32_t phase = phase_of(query_counts, nqueries, m, true);
-  if (phase == Q4K_PHASE_GATED_DECODE) {
-    if (m > 16u * kGemvMaxRowTiles)
-      return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
+  const bool q4 = wg->type == Q4K_GGML_TYPE_Q4_K && wu->type == Q4K_GGML_TYPE_Q4_K;
+  if (phase == Q4K_PHASE_GATED_DECODE && m > 16u * kGemvMaxRowTiles)
+    return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
+  if (phase == Q4K_PHASE_GATED_DECODE && q4)
     return run_linear(s, wg, wu, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase);
-  }
   // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in
   // place.  Both read the same x: it is staged once, under one hold of the
   // workspace lock.
@@ -748,7 +865,8 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
   rc = run_linear_locked(s, ws, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, true);
   if (rc)
     return rc;
-  return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, false);
+  // The Q4_K projection of a Q4_K pair reuses the staged x; Q6_K packs its own.
+  return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, !q4);
 }
 
 int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const float* norm_w, float eps, const void* x, void* gate, void* hidden,
@@ -783,7 +901,8 @@ int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const 
   const uint32_t phase = phase_of(query_counts, nqueries, m, true);
   const void* xin = x;
   if (norm_w) {
-    if (phase == Q4K_PHASE_GATED_DECODE && gemv_gate_up_supported((int)m, (int)(wg->k / 256), (int)wg->n)) {
+    if (phase == Q4K_PHASE_GATED_DECODE && wg->type == Q4K_GGML_TYPE_Q4_K && wu->type == Q4K_GGML_TYPE_Q4_K &&
+        gemv_gate_up_supported((int)m, (int)(wg->k / 256), (int)wg->n)) {
       // The norm runs inside the fused gate/up GEMV (forward.cpp:114-118 in one launch).
       resolve(wg, phase);
       resolve(wu, phase);
@@ -952,6 +1071,8 @@ int q4k_embedding(void* stream, const q4k_weight* table, const int32_t* ids, uin
     return fail(Q4K_EINVAL, "null argument");
   if (dtype > Q4K_DTYPE_F16)
     return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (table->type != Q4K_GGML_TYPE_Q4_K)
+    return fail(Q4K_ETYPE, "the embedding table must be Q4_K (embedding_q4_k)");
   const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
   if (overlaps(ids, (size_t)rows * 4, y, (size_t)rows * table->k * es))
     return fail(Q4K_EALIAS, "y must not overlap ids");

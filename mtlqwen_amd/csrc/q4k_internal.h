@@ -32,6 +32,75 @@ constexpr int kTileBlockBytes = kTileN * kBlockBytes;  // 2304
 constexpr int kSlabBytes = 1024;
 constexpr int kHeaderOffset = 2048;
 
+// ---- block_q6_K device layout ----------------------------------------------
+// GGUF stores row n as k/256 consecutive 210-byte block_q6_K records (ql[128]
+// @0, qh[64] @128, int8 scales[16] @192, d fp16 @208; weight = d * sc * (q - 32)
+// with a 6-bit q).  The device copy uses the same 16-row column tiles; tile-
+// block (c, b) is 3360 bytes at ((c * nb) + b) * 3360:
+//   [0, 3072)     three slabs: lane l = 16g + i (row 16c + i) holds its quant
+//                 dwords 4s..4s+3 at s * 1024 + 16 l
+//   [3072, 3328)  lane l's scale dword at 3072 + 4 l: scales 4g..4g+3 of row
+//                 16c + i, each stored as sc + 128 (the byte sc ^ 0x80)
+//   [3328, 3360)  d of rows 16c..16c+15
+// Lane l covers elements 64g + [0, 64) of its row in the decode pack's order:
+// B-operand dword o = 4 fs + t of MFMA fs holds elements
+// e = 64g + 32 (fs / 4) + 8 (fs % 4) + 2t + {0, 1} (low half, high half), all
+// in sub-block 4g + o / 8.  The twelve dwords are four triples (A, B, C) =
+// dwords 3a..3a+2 for outputs o = 8a + r; per 16-bit half, r = 0, 2, 4 sit at
+// bits 4..9 of A, B, C; r = 1, 3, 5 at bits 10..15; r = 6 takes its low four
+// bits from bits 0..3 of A and its top two from bits 0..1 of B; r = 7 from
+// bits 0..3 of C and bits 2..3 of B.  Same byte count: 210 per 256 weights.
+constexpr int kQ6BlockBytes = 210;
+constexpr int kQ6TileBlockBytes = kTileN * kQ6BlockBytes;  // 3360
+constexpr int kQ6ScaleOffset = 3072;
+constexpr int kQ6DOffset = 3328;
+
+// 6-bit quant (0..63) of element e of a GGUF block_q6_K
+// (backend/metal/kernel/quant_linear.metal:69-86 addressing).
+__host__ __device__ inline uint32_t q6_quant(const uint8_t* blk, int e) {
+  const int h = e >> 7, rr = e & 127, l = rr & 31;
+  const uint32_t q = blk[64 * h + (rr & 32) + l];
+  const uint32_t lo = (rr & 64) ? (q >> 4) : (q & 15u);
+  return lo | (((uint32_t)(blk[128 + 32 * h + l] >> (2 * (rr >> 5))) & 3u) << 4);
+}
+
+// Element of block b's lane-group g for output dword o, half hf.
+__host__ __device__ inline int q6_elem(int g, int o, int hf) {
+  const int fs = o >> 2, t = o & 3;
+  return 64 * g + 32 * (fs >> 2) + 8 * (fs & 3) + 2 * t + hf;
+}
+
+// Writes / reads the 6-bit quant of (o, hf) in a lane's twelve dwords.
+__host__ __device__ inline void q6_place(uint32_t* wd, int o, int hf, uint32_t v) {
+  const int a = o >> 3, r = o & 7, sh = 16 * hf;
+  uint32_t* A = wd + 3 * a;
+  switch (r) {
+    case 6:
+      A[0] |= (v & 15u) << sh;
+      A[1] |= (v >> 4) << sh;
+      break;
+    case 7:
+      A[2] |= (v & 15u) << sh;
+      A[1] |= (v >> 4) << (2 + sh);
+      break;
+    default:
+      A[r >> 1] |= v << ((r & 1 ? 10 : 4) + sh);
+  }
+}
+
+__host__ __device__ inline uint32_t q6_take(const uint32_t* wd, int o, int hf) {
+  const int a = o >> 3, r = o & 7, sh = 16 * hf;
+  const uint32_t* A = wd + 3 * a;
+  switch (r) {
+    case 6:
+      return ((A[0] >> sh) & 15u) | (((A[1] >> sh) & 3u) << 4);
+    case 7:
+      return ((A[2] >> sh) & 15u) | (((A[1] >> (2 + sh)) & 3u) << 4);
+    default:
+      return (A[r >> 1] >> ((r & 1 ? 10 : 4) + sh)) & 63u;
+  }
+}
+
 // Rows of a GEMV call are padded to 16-row MFMA tiles; the GEMV handles up to
 // kGemvMaxRowTiles of them (48 rows: the 8 x 5 decode rows of the reference).
 constexpr int kGemvMaxRowTiles = 3;
@@ -166,6 +235,13 @@ hipError_t launch_rms_norm(hipStream_t s, const void* x, const float* w, void* y
 
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).
 hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
+
+// Q6_K GEMV for m <= 8 rows: a.w = tiled Q6_K weights, a.pack = the decode
+// pack of x (launch_stage_pack), post 0/1/2 on a.y / a.aux.
+hipError_t launch_q6k_gemv(hipStream_t s, const GemvArgs& a, int dtype, int cus);
+
+// Device-side GGUF -> tiled re-layout of block_q6_K weights.
+hipError_t launch_q6k_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
 
 // ---- dispatch --------------------------------------------------------------
 // Events attached to the calling thread's next kernel dispatches (both null

@@ -2114,6 +2114,184 @@ __global__ __launch_bounds__(64) void relayout_kernel(const uint8_t* __restrict_
   }
 }
 
+// ----------------------------------------------------------------------------
+// Q6_K (ggml type 14) on the same linear() surface: the LM head and the
+// down projections of mixed-type GGUF files (quant_linear.metal:69-86,
+// 437-497).
+//
+// GEMV for m <= 8 rows (decode, small prefill, LM head).  The B operand of
+// v_mfma_f32_16x16x32_f16 is (q - 32) * sc in fp16, built two quants per
+// dword: a quant stored at bits 4..9 of a half, masked and or'ed with 0x6400,
+// is the fp16 value 1024 + 16q, and one v_pk_fma_f16 with (sc / 16, -96 sc)
+// leaves (q - 32) * sc (|.| <= 4096: exact up to 2048, above that rounded
+// once to an even integer, a relative error below 2^-11 on those products).
+// The scales arrive biased (sc + 128), so one v_perm_b32 with 0x64 bytes makes
+// the fp16 value 1152 + sc.  The activations are the decode pack (hi / lo
+// fp16 rows 0..7 / 8..15, per-(row, block) power-of-two scale) from the
+// workspace.
+//
+// Workgroup = 8 waves over T column tiles; wave w takes blocks w, w + 8, ...
+// For each block it holds the x fragments (the next block's are loaded while
+// the current one runs) and streams its T tile-blocks through a register
+// window DQ tile-blocks deep: three 16-byte quant loads, one scale dword and
+// the column's d per lane.  Two MFMA chains per tile-block; the partial sums
+// of the 8 waves meet in LDS in wave order before the epilogue.
+// ----------------------------------------------------------------------------
+
+// Outputs o = 8a .. 8a+7 of triple (A, B, C) times their scale: b0 = MFMA 2a's
+// four B dwords, b1 = MFMA 2a + 1's (layout in q4k_internal.h).
+__device__ __forceinline__ void q6_triple(uint32_t A, uint32_t B, uint32_t C, h2_t mul, h2_t add, h8_t& b0, h8_t& b1) {
+  const uint32_t m6 = 0x03F003F0u, m4 = 0x00F000F0u, m2 = 0x03000300u, magic = 0x64006400u;
+  const uint32_t o0 = and_or(A, m6, magic), o1 = and_or(A >> 6, m6, magic);
+  const uint32_t o2 = and_or(B, m6, magic), o3 = and_or(B >> 6, m6, magic);
+  const uint32_t o4 = and_or(C, m6, magic), o5 = and_or(C >> 6, m6, magic);
+  const uint32_t o6 = and_or(A << 4, m4, and_or(B << 8, m2, magic));
+  const uint32_t o7 = and_or(C << 4, m4, and_or(B << 6, m2, magic));
+  auto f = [&](uint32_t o) { return as_u32(__builtin_elementwise_fma(as_h2(o), mul, add)); };
+  b0 = __builtin_bit_cast(h8_t, u4_t{f(o0), f(o1), f(o2), f(o3)});
+  b1 = __builtin_bit_cast(h8_t, u4_t{f(o4), f(o5), f(o6), f(o7)});
+}
+
+struct Q6X {
+  h8_t f[8];
+  float dv[4];
+};
+
+template <int T, typename OutT>
+__global__ __launch_bounds__(512) void q6k_gemv_kernel(GemvArgs a) {
+  constexpr int W = 8, DQ = 2;
+  static_assert(DQ <= T || T == 1, "window");
+  constexpr int D = DQ < T ? DQ : T;
+  __shared__ float part[W][T][8][16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int nb = a.nb, ntiles = a.n >> 4, tile0 = blockIdx.x * T;
+  const size_t tile_bytes = (size_t)nb * kQ6TileBlockBytes;
+  const int nbw = wave < nb ? (nb - 1 - wave) / W + 1 : 0;
+
+  u4_t s0[T], s1[T], s2[T];
+  uint32_t scw[T], dw[T];
+  auto issue = [&](int t, int bi) {
+    const int tile = tile0 + t < ntiles ? tile0 + t : ntiles - 1;
+    const uint8_t* src = a.w + (size_t)tile * tile_bytes + (size_t)(wave + W * bi) * kQ6TileBlockBytes;
+    s0[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    s1[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024) + lane);
+    s2[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 2048) + lane);
+    scw[t] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kQ6ScaleOffset) + lane);
+    dw[t] = *(reinterpret_cast<const uint16_t*>(src + kQ6DOffset) + col);
+  };
+  auto load_x = [&](Q6X& xf, int bi) {
+    const size_t b = (size_t)(wave + W * bi);
+    const u4_t* fr = a.pack.frag + b * 8 * 64 + lane;
+#pragma unroll
+    for (int fs = 0; fs < 8; ++fs)
+      xf.f[fs] = __builtin_bit_cast(h8_t, fr[fs * 64]);
+    const float* ds = a.pack.dsc + b * 8 + 4 * (g & 1);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      xf.dv[v] = ds[v];
+  };
+
+  f4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (nbw > 0) {
+    Q6X xc, xn;
+    load_x(xc, 0);
+#pragma unroll
+    for (int t = 0; t < D; ++t)
+      issue(t, 0);
+    for (int bi = 0; bi < nbw; ++bi) {
+      const bool more = bi + 1 < nbw;
+      if (more)
+        load_x(xn, bi + 1);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        // Take slot t before the window's next issue, which may reuse it.
+        const uint32_t wd[12] = {s0[t][0], s0[t][1], s0[t][2], s0[t][3], s1[t][0], s1[t][1],
+                                 s1[t][2], s1[t][3], s2[t][0], s2[t][1], s2[t][2], s2[t][3]};
+        const uint32_t sw = scw[t], dbits = dw[t];
+        const int tn = t + D;
+        if (tn < T)
+          issue(tn, bi);
+        else if (more)
+          issue(tn - T, bi + 1);
+        const float d = half_bits_to_float(dbits & 0xffffu);
+        f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int tr = 0; tr < 4; ++tr) {
+          // fp16 1152 + sc -> sc / 16 (exact), and -96 sc.
+          const uint32_t sel = 0x04000400u | (uint32_t)tr | ((uint32_t)tr << 16);
+          const h2_t p = as_h2(__builtin_amdgcn_perm(0x64646464u, sw, sel));
+          const h2_t mul = __builtin_elementwise_fma(p, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-72.0f, (_Float16)-72.0f});
+          const h2_t add = mul * h2_t{(_Float16)-1536.0f, (_Float16)-1536.0f};
+          h8_t b0, b1;
+          q6_triple(wd[3 * tr], wd[3 * tr + 1], wd[3 * tr + 2], mul, add, b0, b1);
+          c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xc.f[2 * tr], b0, c0, 0, 0, 0);
+          c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xc.f[2 * tr + 1], b1, c1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[t][v] = fmaf(c0[v] + c1[v], d * xc.dv[v], acc[t][v]);
+      }
+      if (more)
+        xc = xn;
+    }
+  }
+  // C row 4g + v: lanes g < 2 add the low parts held 32 lanes up.
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float tot = acc[t][v] + __shfl_xor(acc[t][v], 32);
+      if (g < 2)
+        part[wave][t][4 * g + v][col] = tot;
+    }
+  __syncthreads();
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  for (int o = tid; o < a.m * 16 * T; o += 64 * W) {
+    const int row = o / (16 * T), c = o % (16 * T), t = c >> 4, cc = c & 15;
+    if (tile0 + t >= ntiles)
+      continue;
+    float acc_v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      acc_v += part[w][t][row][cc];
+    if (sizeof(OutT) == 2)
+      acc_v = round_half(acc_v);
+    const size_t off = (size_t)row * a.n + (size_t)(tile0 + t) * 16 + cc;
+    const float out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+    store_elem(y, off, out);
+  }
+}
+
+// One workgroup of 64 lanes per Q6_K tile-block: lane 16g + i writes its
+// twelve quant dwords and its scale dword; lanes 0..15 write d.
+__global__ __launch_bounds__(64) void q6k_relayout_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t nb) {
+  const size_t tb = blockIdx.x;
+  const uint32_t c = (uint32_t)(tb / nb), b = (uint32_t)(tb % nb);
+  const int lane = threadIdx.x, i = lane & 15, g = lane >> 4;
+  const uint8_t* blk = src + ((size_t)(16 * c + i) * nb + b) * kQ6BlockBytes;
+  uint8_t* out = dst + tb * kQ6TileBlockBytes;
+  uint32_t wd[12] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  for (int o = 0; o < 32; ++o)
+    for (int hf = 0; hf < 2; ++hf)
+      q6_place(wd, o, hf, q6_quant(blk, q6_elem(g, o, hf)));
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+    *reinterpret_cast<u4_t*>(out + s * 1024 + 16 * lane) = u4_t{wd[4 * s], wd[4 * s + 1], wd[4 * s + 2], wd[4 * s + 3]};
+  uint32_t sc = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    sc |= (uint32_t)(blk[192 + 4 * g + j] ^ 0x80u) << (8 * j);
+  *reinterpret_cast<uint32_t*>(out + kQ6ScaleOffset + 4 * lane) = sc;
+  if (g == 0)
+    *reinterpret_cast<uint16_t*>(out + kQ6DOffset + 2 * i) = (uint16_t)(blk[208] | (blk[209] << 8));
+}
+
 int env_int(const char* name, int fallback) {
   const char* v = getenv(name);
   return v && *v ? atoi(v) : fallback;
@@ -2451,6 +2629,39 @@ hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint
   if (tiles == 0)
     return hipSuccess;
   (void)dispatch(relayout_kernel, dim3((unsigned)tiles), dim3(64), s, src, dst, n, nb);
+  return hipGetLastError();
+}
+
+template <int T>
+hipError_t q6k_gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
+  const int ntiles = a.n / 16;
+  const dim3 grid((unsigned)((ntiles + T - 1) / T)), block(512);
+  if (dtype == kF32)
+    (void)dispatch(q6k_gemv_kernel<T, float>, grid, block, s, a);
+  else
+    (void)dispatch(q6k_gemv_kernel<T, _Float16>, grid, block, s, a);
+  return hipGetLastError();
+}
+
+// Column tiles per workgroup: the most (of 4, 2, 1) that still gives every
+// CU at least two workgroups.
+hipError_t launch_q6k_gemv(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+  const int ntiles = a.n / 16;
+  static const int forced = env_int("Q6K_GEMV_TILES", 0);
+  const int t = forced == 1 || forced == 2 || forced == 4 ? forced : ntiles >= 8 * cus ? 4 : ntiles >= 4 * cus ? 2 : 1;
+  if (t == 4)
+    return q6k_gemv_launch<4>(s, a, dtype);
+  if (t == 2)
+    return q6k_gemv_launch<2>(s, a, dtype);
+  return q6k_gemv_launch<1>(s, a, dtype);
+}
+
+hipError_t launch_q6k_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k) {
+  const uint32_t nb = k / 256;
+  const size_t tiles = (size_t)(n / 16) * nb;
+  if (tiles == 0)
+    return hipSuccess;
+  (void)dispatch(q6k_relayout_kernel, dim3((unsigned)tiles), dim3(64), s, src, dst, nb);
   return hipGetLastError();
 }
 

@@ -75,7 +75,7 @@ class GGUFFile:
         return buf.value.decode()
 
     def weight(self, name, device=0):
-        """Upload the Q4_K matrix ``name`` as a Weight (forward.cpp:18-21)."""
+        """Upload the Q4_K or Q6_K matrix ``name`` as a Weight (forward.cpp:18-21)."""
         from .linear import Weight
         h = ctypes.c_void_p()
         check(lib.q4k_weight_from_gguf(self.handle, name.encode(), int(device), ctypes.byref(h)))

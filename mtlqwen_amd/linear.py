@@ -12,15 +12,16 @@ import ctypes
 import numpy as np
 import torch
 
-from ._lib import (DTYPE_F16, DTYPE_F32, GGML_TYPE_Q4_K, POST_ADD, POST_GATE, POST_STORE, Q4KError, check, lib,
-                   u32_array)
+from ._lib import (BLOCK_BYTES_BY_TYPE, DTYPE_F16, DTYPE_F32, GGML_TYPE_Q4_K, POST_ADD, POST_GATE, POST_STORE, Q4KError,
+                   check, lib, u32_array)
 
 BLOCK_BYTES = 144
 PHASE_NAMES = ("decode", "prefill", "prefill_small", "gated_decode")
 
 
-def q4k_nbytes(n, k):
-    return n * (k // 256) * BLOCK_BYTES
+def q4k_nbytes(n, k, ggml_type=GGML_TYPE_Q4_K):
+    """GGUF bytes of an n x k tensor of ggml type Q4_K (144 B per 256) or Q6_K (210 B)."""
+    return n * (k // 256) * BLOCK_BYTES_BY_TYPE[ggml_type]
 
 
 def _dtype_code(t):
@@ -50,10 +51,11 @@ def _ptr(t):
 
 
 class Weight:
-    """A Q4_K weight uploaded once to HBM (re-laid out for the kernels).
+    """A Q4_K (or Q6_K) weight uploaded once to HBM (re-laid out for the kernels).
 
-    ``data`` holds GGUF block_q4_K bytes for n rows of k/256 blocks: a host
-    numpy/bytes buffer, or a uint8 CUDA tensor (re-laid out on the device).
+    ``data`` holds GGUF block_q4_K (or block_q6_K, ``ggml_type=14``) bytes for
+    n rows of k/256 blocks: a host numpy/bytes buffer, or a uint8 CUDA tensor
+    (re-laid out on the device).
     """
 
     def __init__(self, data, n, k, ggml_type=GGML_TYPE_Q4_K, device=0):
@@ -97,7 +99,7 @@ class Weight:
 
     @property
     def nbytes(self):
-        return q4k_nbytes(self.n, self.k)
+        return q4k_nbytes(self.n, self.k, self.type)
 
     def close(self):
         if getattr(self, "_h", None) is not None:
@@ -244,17 +246,20 @@ def mfma_ceiling(device=0, iters=20000, stream=None):
     return t.value
 
 
-def relayout_host(gguf, n, k):
+def relayout_host(gguf, n, k, ggml_type=GGML_TYPE_Q4_K):
+    """GGUF-order bytes of type Q4_K or Q6_K -> the kernels' tiled order."""
     src = np.ascontiguousarray(gguf, dtype=np.uint8).reshape(-1)
     dst = np.empty_like(src)
-    check(lib.q4k_relayout_host(src.ctypes.data_as(ctypes.c_void_p), dst.ctypes.data_as(ctypes.c_void_p), n, k))
+    check(lib.q4k_relayout_host_typed(src.ctypes.data_as(ctypes.c_void_p), dst.ctypes.data_as(ctypes.c_void_p), n, k,
+                                      ggml_type))
     return dst
 
 
-def unrelayout_host(tiled, n, k):
+def unrelayout_host(tiled, n, k, ggml_type=GGML_TYPE_Q4_K):
     src = np.ascontiguousarray(tiled, dtype=np.uint8).reshape(-1)
     dst = np.empty_like(src)
-    check(lib.q4k_unrelayout_host(src.ctypes.data_as(ctypes.c_void_p), dst.ctypes.data_as(ctypes.c_void_p), n, k))
+    check(lib.q4k_unrelayout_host_typed(src.ctypes.data_as(ctypes.c_void_p), dst.ctypes.data_as(ctypes.c_void_p), n, k,
+                                        ggml_type))
     return dst
 
 

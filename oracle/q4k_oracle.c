@@ -126,6 +126,41 @@ void q4o_dequant_block_f16(const uint8_t* blk, uint16_t* out) {
     out[i] = q4o_float_to_half(tmp[i]);
 }
 
+/* quant_linear.metal:69-86 (dequant_tile<q6_k_tag>): half h = e / 128,
+ * rr = e % 128, l = rr % 32; the low nibble of ql[64h + 32((rr >> 5) & 1) + l]
+ * (high nibble when rr >= 64), the two bits (qh[32h + l] >> 2(rr / 32)) & 3
+ * on top. */
+int q6o_quant(const uint8_t* blk, int e) {
+  const int h = e >> 7, rr = e & 127, l = rr & 31, s = rr >> 5;
+  const uint8_t q = blk[64 * h + ((rr & 32) ? 32 : 0) + l];
+  const int lo = (rr & 64) ? (q >> 4) : (q & 15);
+  const int hi = (blk[128 + 32 * h + l] >> (2 * s)) & 3;
+  return (hi << 4) | lo;
+}
+
+/* quant_linear.metal:82: scales[8h + rr / 16] = scales[e / 16], int8. */
+int q6o_scale(const uint8_t* blk, int e) {
+  return (int8_t)blk[192 + 8 * (e >> 7) + ((e & 127) >> 4)];
+}
+
+/* quant_linear.metal:79-83: (d * sc) * (q - 32) in fp32. */
+void q6o_dequant_block(const uint8_t* blk, float* out) {
+  const float d = h2f(blk + 208);
+  for (int e = 0; e < 256; ++e)
+    out[e] = d * (float)q6o_scale(blk, e) * (float)(q6o_quant(blk, e) - 32);
+}
+
+void q6o_dequant_block_f16(const uint8_t* blk, uint16_t* out) {
+  float tmp[256];
+  q6o_dequant_block(blk, tmp);
+  for (int i = 0; i < 256; ++i)
+    out[i] = q4o_float_to_half(tmp[i]);
+}
+
+static size_t block_bytes(int type) {
+  return type == Q4O_TYPE_Q6_K ? Q6O_BLOCK_BYTES : Q4O_BLOCK_BYTES;
+}
+
 /* ------------------------------------------------------- contraction -- */
 
 /* One (row n of W) x (M rows of x) contraction in the decode algebraic form of
@@ -161,6 +196,33 @@ static void contract_row(float* acc, const float* x, int M, int K, const uint8_t
   }
 }
 
+/* The block_q6_K contraction in the decode form of quant_linear.metal:437-497:
+ * per 16-element sub-block j, sum(x * (q - 32)) in fp32, then
+ * acc += d * sum_j(sc_j * sum_j). */
+static void contract_row_q6(float* acc, const float* x, int M, int K, const uint8_t* wrow) {
+  int nb = K / 256;
+  for (int m = 0; m < M; ++m)
+    acc[m] = 0.0f;
+  float q[256];
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* blk = wrow + (size_t)b * Q6O_BLOCK_BYTES;
+    float d = h2f(blk + 208);
+    for (int e = 0; e < 256; ++e)
+      q[e] = (float)(q6o_quant(blk, e) - 32);
+    for (int m = 0; m < M; ++m) {
+      const float* xb = x + (size_t)m * K + (size_t)b * 256;
+      float bq = 0.0f;
+      for (int j = 0; j < 16; ++j) {
+        float sq = 0.0f;
+        for (int i = 0; i < 16; ++i)
+          sq += xb[j * 16 + i] * q[j * 16 + i];
+        bq += (float)q6o_scale(blk, j * 16) * sq;
+      }
+      acc[m] += d * bq;
+    }
+  }
+}
+
 static float silu(float g) {
   return g / (1.0f + expf(-g));
 }
@@ -168,7 +230,7 @@ static float silu(float g) {
 enum { KIND_F32, KIND_F16, KIND_GATE_F32, KIND_GATE_F16, KIND_F64 };
 
 typedef struct {
-  int kind, M, N, K, post;
+  int kind, M, N, K, post, type;
   void* y;
   const float* x; /* fp32 copy of the activations */
   const double* xd;
@@ -181,19 +243,24 @@ typedef struct {
 static void* run_job(void* arg) {
   job_t* j = (job_t*)arg;
   int M = j->M, N = j->N, K = j->K;
-  size_t row_bytes = (size_t)(K / 256) * Q4O_BLOCK_BYTES;
+  const size_t bb = block_bytes(j->type), row_bytes = (size_t)(K / 256) * bb;
+  const int q6 = j->type == Q4O_TYPE_Q6_K;
   if (j->kind == KIND_F64) {
     double* y = (double*)j->y;
     for (int n = j->n0; n < j->n1; ++n) {
       for (int m = 0; m < M; ++m)
         y[(size_t)m * N + n] = 0.0;
       for (int b = 0; b < K / 256; ++b) {
-        const uint8_t* p = j->w + n * row_bytes + (size_t)b * Q4O_BLOCK_BYTES;
-        double d = (double)h2f(p), dm = (double)h2f(p + 2);
+        const uint8_t* p = j->w + n * row_bytes + (size_t)b * bb;
         for (int e = 0; e < 256; ++e) {
-          uint8_t sc, mn;
-          q4o_scale_min(e / 32, p + 4, &sc, &mn);
-          double wv = d * (double)sc * (double)nibble(p + 16, e) - dm * (double)mn;
+          double wv;
+          if (q6) {
+            wv = (double)h2f(p + 208) * (double)q6o_scale(p, e) * (double)(q6o_quant(p, e) - 32);
+          } else {
+            uint8_t sc, mn;
+            q4o_scale_min(e / 32, p + 4, &sc, &mn);
+            wv = (double)h2f(p) * (double)sc * (double)nibble(p + 16, e) - (double)h2f(p + 2) * (double)mn;
+          }
           for (int m = 0; m < M; ++m)
             y[(size_t)m * N + n] += j->xd[(size_t)m * K + (size_t)b * 256 + e] * wv;
         }
@@ -204,9 +271,9 @@ static void* run_job(void* arg) {
   float* acc = (float*)malloc(sizeof(float) * (size_t)M);
   float* acc2 = (float*)malloc(sizeof(float) * (size_t)M);
   for (int n = j->n0; n < j->n1; ++n) {
-    contract_row(acc, j->x, M, K, j->w + n * row_bytes);
+    (q6 ? contract_row_q6 : contract_row)(acc, j->x, M, K, j->w + n * row_bytes);
     if (j->kind == KIND_GATE_F32 || j->kind == KIND_GATE_F16)
-      contract_row(acc2, j->x, M, K, j->wu + n * row_bytes);
+      (q6 ? contract_row_q6 : contract_row)(acc2, j->x, M, K, j->wu + n * row_bytes);
     for (int m = 0; m < M; ++m) {
       size_t o = (size_t)m * N + n;
       switch (j->kind) {
@@ -276,10 +343,14 @@ static int bad_shape(int M, int N, int K) {
   return M < 0 || N <= 0 || K <= 0 || (K % 256) != 0;
 }
 
+static int bad_type(int type) {
+  return type != Q4O_TYPE_Q4_K && type != Q4O_TYPE_Q6_K;
+}
+
 /* Results are written to a private buffer first so aux may alias y. */
-static int linear_common(int kind, void* y, size_t elem, const float* x, const uint8_t* w, const uint8_t* wu, const void* aux, int M, int N, int K,
-                         int post, int threads) {
-  if (bad_shape(M, N, K) || post < 0 || post > 2 || !w || (M && (!x || !y)) || (post && !aux))
+static int linear_common(int kind, int type, void* y, size_t elem, const float* x, const uint8_t* w, const uint8_t* wu, const void* aux, int M,
+                         int N, int K, int post, int threads) {
+  if (bad_shape(M, N, K) || post < 0 || post > 2 || !w || (M && (!x || !y)) || (post && !aux) || bad_type(type))
     return -1;
   if (M == 0)
     return 0;
@@ -287,6 +358,7 @@ static int linear_common(int kind, void* y, size_t elem, const float* x, const u
   job_t p;
   memset(&p, 0, sizeof(p));
   p.kind = kind;
+  p.type = type;
   p.M = M;
   p.N = N;
   p.K = K;
@@ -302,8 +374,12 @@ static int linear_common(int kind, void* y, size_t elem, const float* x, const u
   return 0;
 }
 
+int q4o_linear_typed_f32(float* y, const float* x, const uint8_t* w, int type, const float* aux, int M, int N, int K, int post, int threads) {
+  return linear_common(KIND_F32, type, y, 4, x, w, NULL, aux, M, N, K, post, threads);
+}
+
 int q4o_linear_f32(float* y, const float* x, const uint8_t* w, const float* aux, int M, int N, int K, int post, int threads) {
-  return linear_common(KIND_F32, y, 4, x, w, NULL, aux, M, N, K, post, threads);
+  return q4o_linear_typed_f32(y, x, w, Q4O_TYPE_Q4_K, aux, M, N, K, post, threads);
 }
 
 static float* widen(const uint16_t* x, size_t count) {
@@ -313,38 +389,52 @@ static float* widen(const uint16_t* x, size_t count) {
   return f;
 }
 
-int q4o_linear_f16(uint16_t* y, const uint16_t* x, const uint8_t* w, const uint16_t* aux, int M, int N, int K, int post, int threads) {
+int q4o_linear_typed_f16(uint16_t* y, const uint16_t* x, const uint8_t* w, int type, const uint16_t* aux, int M, int N, int K, int post,
+                         int threads) {
   if (bad_shape(M, N, K) || (M && !x))
     return -1;
   float* xf = widen(x, (size_t)M * K);
-  int rc = linear_common(KIND_F16, y, 2, xf, w, NULL, aux, M, N, K, post, threads);
+  int rc = linear_common(KIND_F16, type, y, 2, xf, w, NULL, aux, M, N, K, post, threads);
   free(xf);
   return rc;
+}
+
+int q4o_linear_f16(uint16_t* y, const uint16_t* x, const uint8_t* w, const uint16_t* aux, int M, int N, int K, int post, int threads) {
+  return q4o_linear_typed_f16(y, x, w, Q4O_TYPE_Q4_K, aux, M, N, K, post, threads);
+}
+
+int q4o_mlp_gate_up_typed_f32(float* y, const float* x, const uint8_t* wg, const uint8_t* wu, int type, int M, int N, int K, int threads) {
+  if (!wu)
+    return -1;
+  return linear_common(KIND_GATE_F32, type, y, 4, x, wg, wu, NULL, M, N, K, 0, threads);
 }
 
 int q4o_mlp_gate_up_f32(float* y, const float* x, const uint8_t* wg, const uint8_t* wu, int M, int N, int K, int threads) {
-  if (!wu)
-    return -1;
-  return linear_common(KIND_GATE_F32, y, 4, x, wg, wu, NULL, M, N, K, 0, threads);
+  return q4o_mlp_gate_up_typed_f32(y, x, wg, wu, Q4O_TYPE_Q4_K, M, N, K, threads);
 }
 
-int q4o_mlp_gate_up_f16(uint16_t* y, const uint16_t* x, const uint8_t* wg, const uint8_t* wu, int M, int N, int K, int threads) {
+int q4o_mlp_gate_up_typed_f16(uint16_t* y, const uint16_t* x, const uint8_t* wg, const uint8_t* wu, int type, int M, int N, int K, int threads) {
   if (bad_shape(M, N, K) || !wu || (M && !x))
     return -1;
   float* xf = widen(x, (size_t)M * K);
-  int rc = linear_common(KIND_GATE_F16, y, 2, xf, wg, wu, NULL, M, N, K, 0, threads);
+  int rc = linear_common(KIND_GATE_F16, type, y, 2, xf, wg, wu, NULL, M, N, K, 0, threads);
   free(xf);
   return rc;
 }
 
-int q4o_linear_f64(double* y, const double* x, const uint8_t* w, int M, int N, int K, int threads) {
-  if (bad_shape(M, N, K) || !w || (M && (!x || !y)))
+int q4o_mlp_gate_up_f16(uint16_t* y, const uint16_t* x, const uint8_t* wg, const uint8_t* wu, int M, int N, int K, int threads) {
+  return q4o_mlp_gate_up_typed_f16(y, x, wg, wu, Q4O_TYPE_Q4_K, M, N, K, threads);
+}
+
+int q4o_linear_typed_f64(double* y, const double* x, const uint8_t* w, int type, int M, int N, int K, int threads) {
+  if (bad_shape(M, N, K) || !w || (M && (!x || !y)) || bad_type(type))
     return -1;
   if (M == 0)
     return 0;
   job_t p;
   memset(&p, 0, sizeof(p));
   p.kind = KIND_F64;
+  p.type = type;
   p.M = M;
   p.N = N;
   p.K = K;
@@ -352,6 +442,10 @@ int q4o_linear_f64(double* y, const double* x, const uint8_t* w, int M, int N, i
   p.xd = x;
   p.w = w;
   return run(p, threads);
+}
+
+int q4o_linear_f64(double* y, const double* x, const uint8_t* w, int M, int N, int K, int threads) {
+  return q4o_linear_typed_f64(y, x, w, Q4O_TYPE_Q4_K, M, N, K, threads);
 }
 
 /* ------------------------------------------------- selection, packing -- */

@@ -68,6 +68,33 @@ int q4o_mlp_gate_up_f16(uint16_t* y, const uint16_t* x, const uint8_t* wg, const
  * fp32 decode form. */
 int q4o_linear_f64(double* y, const double* x, const uint8_t* w, int M, int N, int K, int threads);
 
+/* ---- block_q6_K (ggml type 14): ql[128] @0, qh[64] @128, int8 scales[16]
+ * @192, d fp16 @208; 210 bytes per 256 weights d * sc * (q - 32). */
+#define Q4O_TYPE_Q4_K 12
+#define Q4O_TYPE_Q6_K 14
+#define Q6O_BLOCK_BYTES 210
+
+/* Raw 6-bit quant (0..63) and int8 scale of element e (0..255) of a block.
+ * backend/metal/kernel/quant_linear.metal:69-86 (dequant_tile<q6_k_tag>). */
+int q6o_quant(const uint8_t* blk, int e);
+int q6o_scale(const uint8_t* blk, int e);
+
+/* Dequantize one block_q6_K: (d * sc) * (q - 32) in fp32 (quant_linear.metal:
+ * 79-83 before its half() store); the f16 variant is that store. */
+void q6o_dequant_block(const uint8_t* blk, float* out);
+void q6o_dequant_block_f16(const uint8_t* blk, uint16_t* out);
+
+/* q4o_linear_* / q4o_mlp_gate_up_* over weights of ggml type `type` (Q4_K or
+ * Q6_K).  Q6_K accumulates in the decode form of quant_linear.metal:437-497:
+ * per 16-element sub-block sum(x * (q - 32)) in fp32, then d * sum(sc * .).
+ * The untyped entry points above are type Q4_K.  Returns -1 for another type. */
+int q4o_linear_typed_f32(float* y, const float* x, const uint8_t* w, int type, const float* aux, int M, int N, int K, int post, int threads);
+int q4o_linear_typed_f16(uint16_t* y, const uint16_t* x, const uint8_t* w, int type, const uint16_t* aux, int M, int N, int K, int post,
+                         int threads);
+int q4o_mlp_gate_up_typed_f32(float* y, const float* x, const uint8_t* wg, const uint8_t* wu, int type, int M, int N, int K, int threads);
+int q4o_mlp_gate_up_typed_f16(uint16_t* y, const uint16_t* x, const uint8_t* wg, const uint8_t* wu, int type, int M, int N, int K, int threads);
+int q4o_linear_typed_f64(double* y, const double* x, const uint8_t* w, int type, int M, int N, int K, int threads);
+
 /* Kernel phase of Ops::linear: 0 decode, 1 prefill, 2 prefill_small, 3 gated
  * decode.  decode holds iff every query contributes <= 5 rows
  * (model/qwen35/forward.cpp:52,190; qwen35.hpp:22). */

@@ -13,6 +13,9 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libq4k_oracle.so")
 BLOCK_BYTES = 144
+Q6_BLOCK_BYTES = 210
+TYPE_Q4_K, TYPE_Q6_K = 12, 14
+TYPE_BLOCK_BYTES = {TYPE_Q4_K: BLOCK_BYTES, TYPE_Q6_K: Q6_BLOCK_BYTES}
 
 # --------------------------------------------------------------------------
 # Synthetic data (the BASELINE config-0 recipe).
@@ -27,6 +30,20 @@ def make_q4k(rng, n, k, dmax=0.01):
     d = rng.uniform(0.0, dmax, size=(n, nb, 2)).astype(np.float16)
     w[:, :, 0:4] = d.view(np.uint8).reshape(n, nb, 4)
     return w.reshape(n, nb * BLOCK_BYTES)
+
+
+def make_q6k(rng, n, k, dmax=0.01):
+    """GGUF block_q6_K bytes [n, k/256*210]: uniform quant and qh bytes,
+    uniform int8 scales (-128..127), d = fp16(U(0, dmax))."""
+    nb = k // 256
+    w = rng.integers(0, 256, size=(n, nb, Q6_BLOCK_BYTES), dtype=np.uint8)
+    d = rng.uniform(0.0, dmax, size=(n, nb, 1)).astype(np.float16)
+    w[:, :, 208:210] = d.view(np.uint8).reshape(n, nb, 2)
+    return w.reshape(n, nb * Q6_BLOCK_BYTES)
+
+
+def make_weight(rng, n, k, ggml_type, dmax=0.01):
+    return make_q6k(rng, n, k, dmax) if ggml_type == TYPE_Q6_K else make_q4k(rng, n, k, dmax)
 
 
 def make_x(rng, m, k, scale=1.0):
@@ -81,6 +98,34 @@ def dequant_numpy(w, n, k):
     return out.reshape(n, k)
 
 
+def dequant_q6k_numpy(w, n, k):
+    """[n, k] float64 weights from GGUF Q6_K bytes, in the bit-mask form of
+    the reference's Q6_K decode kernel (quant_linear.metal:473-478): for half
+    h and l < 32, with q1 = ql[64h + l], q2 = ql[64h + 32 + l], qh = qh[32h + l],
+    elements 128h + l + 32s are (q1 & 15) | (qh & 3) << 4, (q2 & 15) | (qh & 12) << 2,
+    (q1 >> 4) | (qh & 48), (q2 >> 4) | (qh & 192) >> 2, minus 32, with scales
+    sc[8h + l / 16 + 2s] (:451, :481) -- not the per-element addressing of
+    the oracle (quant_linear.metal:69-86)."""
+    nb = k // 256
+    blk = w.reshape(n, nb, Q6_BLOCK_BYTES).astype(np.int64)
+    d = w.reshape(n, nb, Q6_BLOCK_BYTES)[:, :, 208:210].copy().view(np.float16).astype(np.float64)[..., 0]
+    sc = w.reshape(n, nb, Q6_BLOCK_BYTES)[:, :, 192:208].copy().view(np.int8).astype(np.float64)
+    out = np.zeros((n, nb, 256), np.float64)
+    l = np.arange(32)
+    for h in range(2):
+        q1 = blk[:, :, 64 * h + l]
+        q2 = blk[:, :, 64 * h + 32 + l]
+        qh = blk[:, :, 128 + 32 * h + l]
+        vals = [(q1 & 15) | ((qh & 3) << 4), (q2 & 15) | ((qh & 12) << 2), (q1 >> 4) | (qh & 48), (q2 >> 4) | ((qh & 192) >> 2)]
+        for s_, v in enumerate(vals):
+            out[:, :, 128 * h + 32 * s_ + l] = d[..., None] * sc[:, :, 8 * h + l // 16 + 2 * s_] * (v - 32)
+    return out.reshape(n, k)
+
+
+def dequant_any_numpy(w, n, k, ggml_type):
+    return dequant_q6k_numpy(w, n, k) if ggml_type == TYPE_Q6_K else dequant_numpy(w, n, k)
+
+
 def silu64(g):
     return g / (1.0 + np.exp(-g))
 
@@ -110,11 +155,25 @@ def load_oracle():
     for name in ("q4o_linear_f32", "q4o_linear_f16"):
         getattr(lib, name).restype = i
         getattr(lib, name).argtypes = [p, p, u8p, p, i, i, i, i, i]
+    for name in ("q4o_linear_typed_f32", "q4o_linear_typed_f16"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = [p, p, u8p, i, p, i, i, i, i, i]
     for name in ("q4o_mlp_gate_up_f32", "q4o_mlp_gate_up_f16"):
         getattr(lib, name).restype = i
         getattr(lib, name).argtypes = [p, p, u8p, u8p, i, i, i, i]
+    for name in ("q4o_mlp_gate_up_typed_f32", "q4o_mlp_gate_up_typed_f16"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = [p, p, u8p, u8p, i, i, i, i, i]
     lib.q4o_linear_f64.restype = i
     lib.q4o_linear_f64.argtypes = [p, p, u8p, i, i, i, i]
+    lib.q4o_linear_typed_f64.restype = i
+    lib.q4o_linear_typed_f64.argtypes = [p, p, u8p, i, i, i, i, i]
+    lib.q6o_quant.restype = i
+    lib.q6o_quant.argtypes = [u8p, i]
+    lib.q6o_scale.restype = i
+    lib.q6o_scale.argtypes = [u8p, i]
+    lib.q6o_dequant_block.argtypes = [u8p, p]
+    lib.q6o_dequant_block_f16.argtypes = [u8p, p]
     lib.q4o_phase.restype = i
     lib.q4o_phase.argtypes = [ctypes.POINTER(ctypes.c_uint32), i, i]
     lib.q4o_pack.restype = ctypes.c_uint32
@@ -144,45 +203,56 @@ class Oracle:
     def _p(a):
         return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
 
-    def linear(self, x, w, n, k, aux=None, post=0, threads=DEFAULT_THREADS):
+    def linear(self, x, w, n, k, aux=None, post=0, threads=DEFAULT_THREADS, ggml_type=TYPE_Q4_K):
         x = np.ascontiguousarray(x)
         m = x.shape[0]
+        w = np.ascontiguousarray(w, np.uint8)
         if x.dtype == np.float16:
             y = np.empty((m, n), np.float16)
             auxa = None if aux is None else np.ascontiguousarray(aux, np.float16)
-            rc = self.lib.q4o_linear_f16(self._p(y), self._p(x.view(np.uint16)), self._p(w), self._p(auxa), m, n, k, post,
-                                         threads)
+            rc = self.lib.q4o_linear_typed_f16(self._p(y), self._p(x.view(np.uint16)), self._p(w), ggml_type, self._p(auxa),
+                                               m, n, k, post, threads)
         else:
             x = x.astype(np.float32, copy=False)
             y = np.empty((m, n), np.float32)
             auxa = None if aux is None else np.ascontiguousarray(aux, np.float32)
-            rc = self.lib.q4o_linear_f32(self._p(y), self._p(x), self._p(w), self._p(auxa), m, n, k, post, threads)
+            rc = self.lib.q4o_linear_typed_f32(self._p(y), self._p(x), self._p(w), ggml_type, self._p(auxa), m, n, k, post,
+                                               threads)
         assert rc == 0
         return y
 
-    def mlp_gate_up(self, x, wg, wu, n, k, threads=DEFAULT_THREADS):
+    def mlp_gate_up(self, x, wg, wu, n, k, threads=DEFAULT_THREADS, ggml_type=TYPE_Q4_K):
         x = np.ascontiguousarray(x)
         m = x.shape[0]
         if x.dtype == np.float16:
             y = np.empty((m, n), np.float16)
-            rc = self.lib.q4o_mlp_gate_up_f16(self._p(y), self._p(x), self._p(wg), self._p(wu), m, n, k, threads)
+            rc = self.lib.q4o_mlp_gate_up_typed_f16(self._p(y), self._p(x), self._p(wg), self._p(wu), ggml_type, m, n, k,
+                                                    threads)
         else:
             y = np.empty((m, n), np.float32)
-            rc = self.lib.q4o_mlp_gate_up_f32(self._p(y), self._p(x.astype(np.float32, copy=False)), self._p(wg),
-                                              self._p(wu), m, n, k, threads)
+            rc = self.lib.q4o_mlp_gate_up_typed_f32(self._p(y), self._p(x.astype(np.float32, copy=False)), self._p(wg),
+                                                    self._p(wu), ggml_type, m, n, k, threads)
         assert rc == 0
         return y
 
-    def linear_f64(self, x, w, n, k, threads=DEFAULT_THREADS):
+    def linear_f64(self, x, w, n, k, threads=DEFAULT_THREADS, ggml_type=TYPE_Q4_K):
         x = np.ascontiguousarray(x, np.float64)
         y = np.empty((x.shape[0], n), np.float64)
-        assert self.lib.q4o_linear_f64(self._p(y), self._p(x), self._p(w), x.shape[0], n, k, threads) == 0
+        assert self.lib.q4o_linear_typed_f64(self._p(y), self._p(x), self._p(np.ascontiguousarray(w, np.uint8)), ggml_type,
+                                             x.shape[0], n, k, threads) == 0
         return y
 
-    def dequant_block(self, blk):
+    def dequant_block(self, blk, ggml_type=TYPE_Q4_K):
         out = np.empty(256, np.float32)
-        self.lib.q4o_dequant_block(self._p(np.ascontiguousarray(blk, np.uint8)), self._p(out))
+        fn = self.lib.q6o_dequant_block if ggml_type == TYPE_Q6_K else self.lib.q4o_dequant_block
+        fn(self._p(np.ascontiguousarray(blk, np.uint8)), self._p(out))
         return out
+
+    def q6_fields(self, blk):
+        """(quants 0..63, int8 scales) of the 256 elements of one block_q6_K."""
+        b = np.ascontiguousarray(blk, np.uint8)
+        return (np.array([self.lib.q6o_quant(self._p(b), e) for e in range(256)]),
+                np.array([self.lib.q6o_scale(self._p(b), e) for e in range(256)]))
 
     def phase(self, counts, gated=False):
         arr = (ctypes.c_uint32 * len(counts))(*counts)

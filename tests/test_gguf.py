@@ -166,8 +166,9 @@ def test_weight_from_gguf_rejects_before_upload(q4k, tmp_path):
     path = tmp_path / "w.gguf"
     write_gguf(path, tensors, meta)
     with q4k.GGUFFile(path) as g:
-        for name, code in [("blk.0.ffn_norm.weight", ETYPE), ("output.weight", ETYPE), ("vec.q4k", ESHAPE),
-                           ("nope", ENOTFOUND)]:
+        # output.weight is Q6_K (served) but 4 rows: not a whole 16-row tile.
+        for name, code in [("blk.0.ffn_norm.weight", ETYPE), ("tiny.f16", ETYPE), ("output.weight", ESHAPE),
+                           ("vec.q4k", ESHAPE), ("nope", ENOTFOUND)]:
             with pytest.raises(q4k.Q4KError) as e:
                 g.weight(name)
             assert e.value.code == code, name
