@@ -259,6 +259,54 @@ def neighbours_bench(args, dev):
     return out
 
 
+def q6k_bench(args, dev):
+    """The Q6_K LM head of real Qwen3.5 GGUF files (output.weight, K = 4096 ->
+    N = 248,320, 834 MB; quant_linear.metal:644-650) on 8 gathered rows, as
+    config 3's LM-head pass runs it: the decode pack of x, then the Q6_K GEMV.
+    Timed per launch with dispatch-attached events (GEMV and pack), and as a
+    whole from a graph of both launches."""
+    import torch
+    import mtlqwen_amd as q4k
+
+    n, k, m = 248320, 4096, 8
+    nb = k // 256
+    g = torch.Generator(device=dev).manual_seed(0x51A70006)
+    raw = torch.randint(0, 256, (n, nb, 210), dtype=torch.uint8, device=dev, generator=g)
+    dd = (torch.rand((n, nb, 1), device=dev, generator=g) * 0.01).half().view(torch.uint8)
+    raw[:, :, 208:210] = dd.view(n, nb, 2)
+    W = q4k.Weight(raw.reshape(-1), n, k, ggml_type=q4k.GGML_TYPE_Q6_K)
+    del raw, dd
+    x = torch.randn((m, k), device=dev, generator=g)
+    y = torch.empty((m, n), device=dev)
+    counts = [1] * m
+    for _ in range(5):
+        q4k.linear(x, W, m, y, query_counts=counts)
+    torch.cuda.synchronize()
+    reps = 50
+    q4k.profile_enable(True)
+    for _ in range(reps):
+        q4k.linear(x, W, m, y, query_counts=counts)
+    torch.cuda.synchronize()
+    ng, tg, lg, _ = q4k.profile_query(q4k.KERNEL_GEMV)
+    ns, ts, _, _ = q4k.profile_query(q4k.KERNEL_STAGE)
+    q4k.profile_enable(False)
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for _ in range(reps):
+            q4k.linear(x, W, m, y, query_counts=counts)
+    graph.replay()
+    torch.cuda.synchronize()
+    step_ms = timed_graph(graph, 3) / (3 * reps) * 1e3
+    weight_bytes = n * nb * 210
+    nbytes = weight_bytes + m * k * 4 + m * n * 4
+    gemv_us = tg / ng * 1e3
+    return {"shape": f"Q6_K N={n} K={k} m={m}", "gemv_avg_us": round(gemv_us, 2), "gemv_min_us": round(lg * 1e3, 2),
+            "pack_avg_us": round(ts / ns * 1e3, 2), "step_us": round(step_ms * 1e3, 2), "bytes": nbytes,
+            "gemv_gbs": round(nbytes / (gemv_us * 1e-6) / 1e9, 1), "gemv_frac_of_8tbs": round(nbytes / (gemv_us * 1e-6) / 8e12, 3),
+            "step_gbs": round(nbytes / (step_ms * 1e-3) / 1e9, 1)}
+
+
 def prefill_bench(args, dev):
     import numpy as np
     import torch
@@ -402,6 +450,7 @@ def main():
     pre = None if args.no_prefill else prefill_bench(args, dev)
     shard = shard_bench(args, dev)
     neighbours = neighbours_bench(args, dev)
+    q6k = q6k_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
@@ -449,6 +498,7 @@ def main():
         },
         "shard_1of8": shard,
         "neighbours": neighbours,
+        "q6k_lm_head": q6k,
         "copy_ceiling_gbs": round(copy_gbs, 1),
         "mfma_ceiling_tflops": round(mfma_tf, 1),
         "cpu_baseline": cpu,

@@ -2157,9 +2157,9 @@ struct Q6X {
   float dv[4];
 };
 
-template <int T, typename OutT>
+template <int T, int DQ, typename OutT>
 __global__ __launch_bounds__(512) void q6k_gemv_kernel(GemvArgs a) {
-  constexpr int W = 8, DQ = 2;
+  constexpr int W = 8;
   static_assert(DQ <= T || T == 1, "window");
   constexpr int D = DQ < T ? DQ : T;
   __shared__ float part[W][T][8][16];
@@ -2265,6 +2265,115 @@ __global__ __launch_bounds__(512) void q6k_gemv_kernel(GemvArgs a) {
     const size_t off = (size_t)row * a.n + (size_t)(tile0 + t) * 16 + cc;
     const float out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
     store_elem(y, off, out);
+  }
+}
+
+// Persistent form for K = 4096 (16 blocks: two per wave): one workgroup per
+// CU loads its waves' x fragments once and then streams every item it owns
+// (items b, b + grid, ...) through one register window that runs across item
+// boundaries, so the next item's first tile-blocks are in flight during the
+// current item's epilogue.  Partial sums alternate between two LDS buffers:
+// one barrier per item.
+template <int T, typename OutT>
+__global__ __launch_bounds__(512) void q6k_gemv_persistent_kernel(GemvArgs a, int items) {
+  constexpr int W = 8, BPW = 2, DQ = 2, U = BPW * T;
+  __shared__ float part[2][W][T][8][16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int ntiles = a.n >> 4;
+  const size_t tile_bytes = (size_t)(W * BPW) * kQ6TileBlockBytes;
+  int item = blockIdx.x;
+  if (item >= items)
+    return;
+
+  Q6X xf[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    const size_t b = (size_t)(wave + W * j);
+    const u4_t* fr = a.pack.frag + b * 8 * 64 + lane;
+#pragma unroll
+    for (int fs = 0; fs < 8; ++fs)
+      xf[j].f[fs] = __builtin_bit_cast(h8_t, fr[fs * 64]);
+    const float* ds = a.pack.dsc + b * 8 + 4 * (g & 1);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      xf[j].dv[v] = ds[v];
+  }
+  u4_t s0[U], s1[U], s2[U];
+  uint32_t scw[U], dw[U];
+  auto issue = [&](int u, int it) {
+    const int j = u / T, t = u - j * T;
+    const int tile = it * T + t < ntiles ? it * T + t : ntiles - 1;
+    const uint8_t* src = a.w + (size_t)tile * tile_bytes + (size_t)(wave + W * j) * kQ6TileBlockBytes;
+    s0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    s1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024) + lane);
+    s2[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 2048) + lane);
+    scw[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kQ6ScaleOffset) + lane);
+    dw[u] = *(reinterpret_cast<const uint16_t*>(src + kQ6DOffset) + col);
+  };
+#pragma unroll
+  for (int u = 0; u < DQ; ++u)
+    issue(u, item);
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  for (int it = 0; item < items; ++it, item += gridDim.x) {
+    const int next = item + (int)gridDim.x;
+    f4_t acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = u / T, t = u - j * T;
+      const uint32_t wd[12] = {s0[u][0], s0[u][1], s0[u][2], s0[u][3], s1[u][0], s1[u][1],
+                               s1[u][2], s1[u][3], s2[u][0], s2[u][1], s2[u][2], s2[u][3]};
+      const uint32_t sw = scw[u], dbits = dw[u];
+      if (u + DQ < U)
+        issue(u + DQ, item);
+      else if (next < items)
+        issue(u + DQ - U, next);
+      const float d = half_bits_to_float(dbits & 0xffffu);
+      f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int tr = 0; tr < 4; ++tr) {
+        const uint32_t sel = 0x04000400u | (uint32_t)tr | ((uint32_t)tr << 16);
+        const h2_t p = as_h2(__builtin_amdgcn_perm(0x64646464u, sw, sel));
+        const h2_t mul = __builtin_elementwise_fma(p, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-72.0f, (_Float16)-72.0f});
+        const h2_t add = mul * h2_t{(_Float16)-1536.0f, (_Float16)-1536.0f};
+        h8_t b0, b1;
+        q6_triple(wd[3 * tr], wd[3 * tr + 1], wd[3 * tr + 2], mul, add, b0, b1);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j].f[2 * tr], b0, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j].f[2 * tr + 1], b1, c1, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[t][v] = fmaf(c0[v] + c1[v], d * xf[j].dv[v], acc[t][v]);
+    }
+    float(*pb)[T][8][16] = part[it & 1];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float tot = acc[t][v] + __shfl_xor(acc[t][v], 32);
+        if (g < 2)
+          pb[wave][t][4 * g + v][col] = tot;
+      }
+    __syncthreads();
+    for (int o = tid; o < a.m * 16 * T; o += 64 * W) {
+      const int row = o / (16 * T), c = o % (16 * T), t = c >> 4, cc = c & 15;
+      if (item * T + t >= ntiles)
+        continue;
+      float acc_v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        acc_v += pb[w][t][row][cc];
+      if (sizeof(OutT) == 2)
+        acc_v = round_half(acc_v);
+      const size_t off = (size_t)row * a.n + (size_t)(item * T + t) * 16 + cc;
+      const float out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+      store_elem(y, off, out);
+    }
   }
 }
 
@@ -2632,28 +2741,51 @@ hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint
   return hipGetLastError();
 }
 
-template <int T>
+template <int T, int DQ>
 hipError_t q6k_gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
   const int ntiles = a.n / 16;
   const dim3 grid((unsigned)((ntiles + T - 1) / T)), block(512);
   if (dtype == kF32)
-    (void)dispatch(q6k_gemv_kernel<T, float>, grid, block, s, a);
+    (void)dispatch(q6k_gemv_kernel<T, DQ, float>, grid, block, s, a);
   else
-    (void)dispatch(q6k_gemv_kernel<T, _Float16>, grid, block, s, a);
+    (void)dispatch(q6k_gemv_kernel<T, DQ, _Float16>, grid, block, s, a);
   return hipGetLastError();
 }
 
-// Column tiles per workgroup: the most (of 4, 2, 1) that still gives every
+template <int T>
+hipError_t q6k_persistent_launch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+  const int items = (a.n / 16 + T - 1) / T;
+  const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
+  if (dtype == kF32)
+    (void)dispatch(q6k_gemv_persistent_kernel<T, float>, grid, block, s, a, items);
+  else
+    (void)dispatch(q6k_gemv_persistent_kernel<T, _Float16>, grid, block, s, a, items);
+  return hipGetLastError();
+}
+
+// K = 4096 with at least 4 items per CU: the persistent form.  Otherwise
+// column tiles per workgroup: the most (of 4, 2, 1) that still gives every
 // CU at least two workgroups.
 hipError_t launch_q6k_gemv(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
   const int ntiles = a.n / 16;
+  static const int persistent = env_int("Q6K_GEMV_PERSISTENT", -1);  // -1 auto, 0 off, else T
+  if (a.nb == 16 && persistent != 0 && (persistent > 0 || ntiles >= 16 * cus)) {
+    if (persistent == 2)
+      return q6k_persistent_launch<2>(s, a, dtype, cus);
+    return q6k_persistent_launch<4>(s, a, dtype, cus);
+  }
   static const int forced = env_int("Q6K_GEMV_TILES", 0);
   const int t = forced == 1 || forced == 2 || forced == 4 ? forced : ntiles >= 8 * cus ? 4 : ntiles >= 4 * cus ? 2 : 1;
+  static const int depth = env_int("Q6K_GEMV_DEPTH", 2);
+  if (t == 4 && depth == 3)
+    return q6k_gemv_launch<4, 3>(s, a, dtype);
+  if (t == 4 && depth == 4)
+    return q6k_gemv_launch<4, 4>(s, a, dtype);
   if (t == 4)
-    return q6k_gemv_launch<4>(s, a, dtype);
+    return q6k_gemv_launch<4, 2>(s, a, dtype);
   if (t == 2)
-    return q6k_gemv_launch<2>(s, a, dtype);
-  return q6k_gemv_launch<1>(s, a, dtype);
+    return q6k_gemv_launch<2, 2>(s, a, dtype);
+  return q6k_gemv_launch<1, 2>(s, a, dtype);
 }
 
 hipError_t launch_q6k_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k) {
