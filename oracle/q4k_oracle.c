@@ -157,8 +157,100 @@ void q6o_dequant_block_f16(const uint8_t* blk, uint16_t* out) {
     out[i] = q4o_float_to_half(tmp[i]);
 }
 
+/* ---- block_q8_0 (quant_linear.metal:89-100): 8 records of (d fp16, 32 int8)
+ * per 256 elements; element e of record e / 32 is d * qs[e % 32]. */
+void q8o_dequant_block(const uint8_t* blk, float* out) {
+  for (int e = 0; e < 256; ++e) {
+    const uint8_t* r = blk + 34 * (e >> 5);
+    out[e] = h2f(r) * (float)(int8_t)r[2 + (e & 31)];
+  }
+}
+
+/* ---- block_q5_K (quant_linear.metal:50-67): d @0, dmin @2, the Q4_K 6-bit
+ * scale/min bytes @4, qh[32] @16, qs[128] @48.  Element e (t = e / 64,
+ * l = e % 32, high nibble when e % 64 >= 32): the nibble of qs[32t + l] plus
+ * 16 when bit 2t (+1 for the high nibble) of qh[l] is set. */
+int q5o_quant(const uint8_t* blk, int e) {
+  const int t = e >> 6, l = e & 31, hi = (e >> 5) & 1;
+  const uint8_t q = blk[48 + 32 * t + l];
+  const int lo = hi ? (q >> 4) : (q & 15);
+  return lo + (((blk[16 + l] >> (2 * t + hi)) & 1) << 4);
+}
+
+void q5o_dequant_block(const uint8_t* blk, float* out) {
+  const float d = h2f(blk), dm = h2f(blk + 2);
+  for (int e = 0; e < 256; ++e) {
+    uint8_t sc, mn;
+    q4o_scale_min(e >> 5, blk + 4, &sc, &mn);
+    out[e] = d * (float)sc * (float)q5o_quant(blk, e) - dm * (float)mn;
+  }
+}
+
+/* ---- block_iq4_xs (quant_linear.metal:102-115): d @0, scales_h u16 @2,
+ * scales_l[4] @4, qs[128] @8.  Sub-block j = e / 32 has the 6-bit scale
+ * ls = (scales_l[j / 2] >> 4(j % 2)) & 15 | ((scales_h >> 2j) & 3) << 4; element e
+ * is d * (ls - 32) * iq4nl[v] with v the low nibble of qs[16j + e % 16], the
+ * high nibble when e % 32 >= 16. */
+static const float kIq4nl[16] = {-127.0f, -104.0f, -83.0f, -65.0f, -49.0f, -35.0f, -22.0f, -10.0f,
+                                 1.0f,    13.0f,   25.0f,  38.0f,  53.0f,  69.0f,  89.0f,  113.0f};
+
+int iq4o_index(const uint8_t* blk, int e) {
+  const int j = e >> 5, r = e & 31;
+  const uint8_t q = blk[8 + 16 * j + (r & 15)];
+  return (r & 16) ? (q >> 4) : (q & 15);
+}
+
+int iq4o_scale(const uint8_t* blk, int j) {
+  const int sh = blk[2] | (blk[3] << 8);
+  return (((blk[4 + j / 2] >> (4 * (j % 2))) & 15) | (((sh >> (2 * j)) & 3) << 4)) - 32;
+}
+
+float iq4o_value(int v) {
+  return kIq4nl[v & 15];
+}
+
+void iq4o_dequant_block(const uint8_t* blk, float* out) {
+  const float d = h2f(blk);
+  for (int e = 0; e < 256; ++e)
+    out[e] = d * (float)iq4o_scale(blk, e >> 5) * kIq4nl[iq4o_index(blk, e)];
+}
+
 static size_t block_bytes(int type) {
-  return type == Q4O_TYPE_Q6_K ? Q6O_BLOCK_BYTES : Q4O_BLOCK_BYTES;
+  switch (type) {
+    case Q4O_TYPE_Q6_K:
+      return Q6O_BLOCK_BYTES;
+    case Q4O_TYPE_Q8_0:
+      return Q8O_BLOCK_BYTES;
+    case Q4O_TYPE_Q5_K:
+      return Q5O_BLOCK_BYTES;
+    case Q4O_TYPE_IQ4_XS:
+      return IQ4O_BLOCK_BYTES;
+    default:
+      return Q4O_BLOCK_BYTES;
+  }
+}
+
+/* Weight e of a 256-element block of any served type, in double (the
+ * dequantize-then-dot formulation). */
+static double weight64(const uint8_t* p, int type, int e) {
+  switch (type) {
+    case Q4O_TYPE_Q6_K:
+      return (double)h2f(p + 208) * (double)q6o_scale(p, e) * (double)(q6o_quant(p, e) - 32);
+    case Q4O_TYPE_Q8_0:
+      return (double)h2f(p + 34 * (e >> 5)) * (double)(int8_t)p[34 * (e >> 5) + 2 + (e & 31)];
+    case Q4O_TYPE_Q5_K: {
+      uint8_t sc, mn;
+      q4o_scale_min(e >> 5, p + 4, &sc, &mn);
+      return (double)h2f(p) * (double)sc * (double)q5o_quant(p, e) - (double)h2f(p + 2) * (double)mn;
+    }
+    case Q4O_TYPE_IQ4_XS:
+      return (double)h2f(p) * (double)iq4o_scale(p, e >> 5) * (double)kIq4nl[iq4o_index(p, e)];
+    default: {
+      uint8_t sc, mn;
+      q4o_scale_min(e / 32, p + 4, &sc, &mn);
+      return (double)h2f(p) * (double)sc * (double)nibble(p + 16, e) - (double)h2f(p + 2) * (double)mn;
+    }
+  }
 }
 
 /* ------------------------------------------------------- contraction -- */
@@ -199,6 +291,99 @@ static void contract_row(float* acc, const float* x, int M, int K, const uint8_t
 /* The block_q6_K contraction in the decode form of quant_linear.metal:437-497:
  * per 16-element sub-block j, sum(x * (q - 32)) in fp32, then
  * acc += d * sum_j(sc_j * sum_j). */
+/* block_q8_0 in the decode form of quant_linear.metal:525-533: per 32-element
+ * record, sum(q * x) in fp32, times d. */
+static void contract_row_q8(float* acc, const float* x, int M, int K, const uint8_t* wrow) {
+  const int nr = K / 32;
+  for (int m = 0; m < M; ++m) {
+    float a = 0.0f;
+    for (int r = 0; r < nr; ++r) {
+      const uint8_t* rec = wrow + (size_t)r * 34;
+      const float* xb = x + (size_t)m * K + (size_t)r * 32;
+      float sq = 0.0f;
+      for (int i = 0; i < 32; ++i)
+        sq += (float)(int8_t)rec[2 + i] * xb[i];
+      a += sq * h2f(rec);
+    }
+    acc[m] = a;
+  }
+}
+
+/* block_q5_K in the decode form of quant_linear.metal:345-412: per 32-element
+ * sub-block sum(x * q5) and sum(x) in fp32, then d * sum(sc * .) - dmin * sum(m * .). */
+static void contract_row_q5(float* acc, const float* x, int M, int K, const uint8_t* wrow) {
+  const int nb = K / 256;
+  for (int m = 0; m < M; ++m)
+    acc[m] = 0.0f;
+  float q[256];
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* blk = wrow + (size_t)b * Q5O_BLOCK_BYTES;
+    const float d = h2f(blk), dm = h2f(blk + 2);
+    uint8_t sc[8], mn[8];
+    for (int j = 0; j < 8; ++j)
+      q4o_scale_min(j, blk + 4, &sc[j], &mn[j]);
+    for (int e = 0; e < 256; ++e)
+      q[e] = (float)q5o_quant(blk, e);
+    for (int m = 0; m < M; ++m) {
+      const float* xb = x + (size_t)m * K + (size_t)b * 256;
+      float bq = 0.0f, bm = 0.0f;
+      for (int j = 0; j < 8; ++j) {
+        float sq = 0.0f, sx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+          sq += xb[j * 32 + i] * q[j * 32 + i];
+          sx += xb[j * 32 + i];
+        }
+        bq += (float)sc[j] * sq;
+        bm += (float)mn[j] * sx;
+      }
+      acc[m] += d * bq - dm * bm;
+    }
+  }
+}
+
+/* block_iq4_xs in the decode form of fused_kernels.metal:156-178: per 32-element
+ * sub-block sum(x * iq4nl[v]) in fp32, times d * (ls - 32). */
+static void contract_row_iq4(float* acc, const float* x, int M, int K, const uint8_t* wrow) {
+  const int nb = K / 256;
+  for (int m = 0; m < M; ++m)
+    acc[m] = 0.0f;
+  float v[256];
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* blk = wrow + (size_t)b * IQ4O_BLOCK_BYTES;
+    const float d = h2f(blk);
+    for (int e = 0; e < 256; ++e)
+      v[e] = kIq4nl[iq4o_index(blk, e)];
+    for (int m = 0; m < M; ++m) {
+      const float* xb = x + (size_t)m * K + (size_t)b * 256;
+      for (int j = 0; j < 8; ++j) {
+        float s = 0.0f;
+        for (int i = 0; i < 32; ++i)
+          s += xb[j * 32 + i] * v[j * 32 + i];
+        acc[m] += d * (float)iq4o_scale(blk, j) * s;
+      }
+    }
+  }
+}
+
+typedef void (*contract_fn)(float*, const float*, int, int, const uint8_t*);
+
+static void contract_row_q6(float* acc, const float* x, int M, int K, const uint8_t* wrow);
+
+static contract_fn contract_for(int type) {
+  switch (type) {
+    case Q4O_TYPE_Q6_K:
+      return contract_row_q6;
+    case Q4O_TYPE_Q8_0:
+      return contract_row_q8;
+    case Q4O_TYPE_Q5_K:
+      return contract_row_q5;
+    case Q4O_TYPE_IQ4_XS:
+      return contract_row_iq4;
+    default:
+      return contract_row;
+  }
+}
+
 static void contract_row_q6(float* acc, const float* x, int M, int K, const uint8_t* wrow) {
   int nb = K / 256;
   for (int m = 0; m < M; ++m)
@@ -244,7 +429,7 @@ static void* run_job(void* arg) {
   job_t* j = (job_t*)arg;
   int M = j->M, N = j->N, K = j->K;
   const size_t bb = block_bytes(j->type), row_bytes = (size_t)(K / 256) * bb;
-  const int q6 = j->type == Q4O_TYPE_Q6_K;
+  const contract_fn contract = contract_for(j->type);
   if (j->kind == KIND_F64) {
     double* y = (double*)j->y;
     for (int n = j->n0; n < j->n1; ++n) {
@@ -253,14 +438,7 @@ static void* run_job(void* arg) {
       for (int b = 0; b < K / 256; ++b) {
         const uint8_t* p = j->w + n * row_bytes + (size_t)b * bb;
         for (int e = 0; e < 256; ++e) {
-          double wv;
-          if (q6) {
-            wv = (double)h2f(p + 208) * (double)q6o_scale(p, e) * (double)(q6o_quant(p, e) - 32);
-          } else {
-            uint8_t sc, mn;
-            q4o_scale_min(e / 32, p + 4, &sc, &mn);
-            wv = (double)h2f(p) * (double)sc * (double)nibble(p + 16, e) - (double)h2f(p + 2) * (double)mn;
-          }
+          const double wv = weight64(p, j->type, e);
           for (int m = 0; m < M; ++m)
             y[(size_t)m * N + n] += j->xd[(size_t)m * K + (size_t)b * 256 + e] * wv;
         }
@@ -271,9 +449,9 @@ static void* run_job(void* arg) {
   float* acc = (float*)malloc(sizeof(float) * (size_t)M);
   float* acc2 = (float*)malloc(sizeof(float) * (size_t)M);
   for (int n = j->n0; n < j->n1; ++n) {
-    (q6 ? contract_row_q6 : contract_row)(acc, j->x, M, K, j->w + n * row_bytes);
+    contract(acc, j->x, M, K, j->w + n * row_bytes);
     if (j->kind == KIND_GATE_F32 || j->kind == KIND_GATE_F16)
-      (q6 ? contract_row_q6 : contract_row)(acc2, j->x, M, K, j->wu + n * row_bytes);
+      contract(acc2, j->x, M, K, j->wu + n * row_bytes);
     for (int m = 0; m < M; ++m) {
       size_t o = (size_t)m * N + n;
       switch (j->kind) {
@@ -344,7 +522,7 @@ static int bad_shape(int M, int N, int K) {
 }
 
 static int bad_type(int type) {
-  return type != Q4O_TYPE_Q4_K && type != Q4O_TYPE_Q6_K;
+  return type != Q4O_TYPE_Q4_K && type != Q4O_TYPE_Q6_K && type != Q4O_TYPE_Q8_0 && type != Q4O_TYPE_Q5_K && type != Q4O_TYPE_IQ4_XS;
 }
 
 /* Results are written to a private buffer first so aux may alias y. */

@@ -84,10 +84,33 @@ int q6o_scale(const uint8_t* blk, int e);
 void q6o_dequant_block(const uint8_t* blk, float* out);
 void q6o_dequant_block_f16(const uint8_t* blk, uint16_t* out);
 
-/* q4o_linear_* / q4o_mlp_gate_up_* over weights of ggml type `type` (Q4_K or
- * Q6_K).  Q6_K accumulates in the decode form of quant_linear.metal:437-497:
- * per 16-element sub-block sum(x * (q - 32)) in fp32, then d * sum(sc * .).
- * The untyped entry points above are type Q4_K.  Returns -1 for another type. */
+/* ---- block_q8_0 (type 8, 34 B per 32: d fp16, int8 qs[32]), block_q5_K
+ * (type 13, 176 B per 256: d, dmin, Q4_K scale/min bytes, qh[32], qs[128]) and
+ * block_iq4_xs (type 23, 136 B per 256: d, scales_h, scales_l[4], qs[128]),
+ * backend/metal/kernel/quant_linear.metal:50-115 (dequant_tile). */
+#define Q4O_TYPE_Q8_0 8
+#define Q4O_TYPE_Q5_K 13
+#define Q4O_TYPE_IQ4_XS 23
+#define Q8O_BLOCK_BYTES 272 /* eight 34-byte records per 256 elements */
+#define Q5O_BLOCK_BYTES 176
+#define IQ4O_BLOCK_BYTES 136
+
+void q8o_dequant_block(const uint8_t* blk, float* out);       /* 256 elements = 8 records */
+int q5o_quant(const uint8_t* blk, int e);                      /* 5-bit quant 0..31 */
+void q5o_dequant_block(const uint8_t* blk, float* out);       /* d * sc * q - dmin * m */
+int iq4o_index(const uint8_t* blk, int e);                     /* 4-bit codebook index */
+int iq4o_scale(const uint8_t* blk, int j);                     /* ls_j - 32, sub-block j of 8 */
+float iq4o_value(int v);                                       /* the iq4nl codebook (quant_linear.metal:5) */
+void iq4o_dequant_block(const uint8_t* blk, float* out);      /* d * (ls - 32) * iq4nl[v] */
+
+/* q4o_linear_* / q4o_mlp_gate_up_* over weights of ggml type `type` (Q4_K,
+ * Q6_K, Q8_0, Q5_K or IQ4_XS), each accumulated in the decode form of its
+ * reference kernel: Q6_K per 16-element sub-block sum(x * (q - 32)), then
+ * d * sum(sc * .) (quant_linear.metal:437-497); Q8_0 per 32-element record
+ * sum(q * x) * d (:525-533); Q5_K as Q4_K with 5-bit quants (:345-412);
+ * IQ4_XS per 32-element sub-block d * (ls - 32) * sum(x * iq4nl[v])
+ * (fused_kernels.metal:156-178).  The untyped entry points above are type
+ * Q4_K.  Returns -1 for another type. */
 int q4o_linear_typed_f32(float* y, const float* x, const uint8_t* w, int type, const float* aux, int M, int N, int K, int post, int threads);
 int q4o_linear_typed_f16(uint16_t* y, const uint16_t* x, const uint8_t* w, int type, const uint16_t* aux, int M, int N, int K, int post,
                          int threads);

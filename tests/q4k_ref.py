@@ -14,8 +14,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libq4k_oracle.so")
 BLOCK_BYTES = 144
 Q6_BLOCK_BYTES = 210
-TYPE_Q4_K, TYPE_Q6_K = 12, 14
-TYPE_BLOCK_BYTES = {TYPE_Q4_K: BLOCK_BYTES, TYPE_Q6_K: Q6_BLOCK_BYTES}
+TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q5_K, TYPE_IQ4_XS = 12, 14, 8, 13, 23
+# bytes per 256 weights
+TYPE_BLOCK_BYTES = {TYPE_Q4_K: BLOCK_BYTES, TYPE_Q6_K: Q6_BLOCK_BYTES, TYPE_Q8_0: 272, TYPE_Q5_K: 176, TYPE_IQ4_XS: 136}
+IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float64)
 
 # --------------------------------------------------------------------------
 # Synthetic data (the BASELINE config-0 recipe).
@@ -42,8 +44,35 @@ def make_q6k(rng, n, k, dmax=0.01):
     return w.reshape(n, nb * Q6_BLOCK_BYTES)
 
 
+def make_q8_0(rng, n, k, dmax=0.01):
+    """GGUF block_q8_0 bytes [n, k/32*34]: d = fp16(U(0, dmax)) per 32, uniform int8."""
+    nr = k // 32
+    w = rng.integers(0, 256, size=(n, nr, 34), dtype=np.uint8)
+    w[:, :, 0:2] = rng.uniform(0.0, dmax, size=(n, nr, 1)).astype(np.float16).view(np.uint8).reshape(n, nr, 2)
+    return w.reshape(n, nr * 34)
+
+
+def make_q5k(rng, n, k, dmax=0.01):
+    """GGUF block_q5_K bytes [n, k/256*176]: d, dmin = fp16(U(0, dmax)), uniform rest."""
+    nb = k // 256
+    w = rng.integers(0, 256, size=(n, nb, 176), dtype=np.uint8)
+    w[:, :, 0:4] = rng.uniform(0.0, dmax, size=(n, nb, 2)).astype(np.float16).view(np.uint8).reshape(n, nb, 4)
+    return w.reshape(n, nb * 176)
+
+
+def make_iq4xs(rng, n, k, dmax=0.01):
+    """GGUF block_iq4_xs bytes [n, k/256*136]: d = fp16(U(0, dmax)), uniform rest."""
+    nb = k // 256
+    w = rng.integers(0, 256, size=(n, nb, 136), dtype=np.uint8)
+    w[:, :, 0:2] = rng.uniform(0.0, dmax, size=(n, nb, 1)).astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    return w.reshape(n, nb * 136)
+
+
+_MAKERS = {TYPE_Q4_K: make_q4k, TYPE_Q6_K: make_q6k, TYPE_Q8_0: make_q8_0, TYPE_Q5_K: make_q5k, TYPE_IQ4_XS: make_iq4xs}
+
+
 def make_weight(rng, n, k, ggml_type, dmax=0.01):
-    return make_q6k(rng, n, k, dmax) if ggml_type == TYPE_Q6_K else make_q4k(rng, n, k, dmax)
+    return _MAKERS[ggml_type](rng, n, k, dmax)
 
 
 def make_x(rng, m, k, scale=1.0):
@@ -122,8 +151,69 @@ def dequant_q6k_numpy(w, n, k):
     return out.reshape(n, k)
 
 
+def dequant_q8_0_numpy(w, n, k):
+    """[n, k] float64 from Q8_0 bytes: per 34-byte record d * int8 (the decode
+    kernel's qs = o + 2 + 8 il, d = the record's half, quant_linear.metal:529-533)."""
+    rec = w.reshape(n, k // 32, 34)
+    d = rec[:, :, 0:2].copy().view(np.float16).astype(np.float64)
+    q = rec[:, :, 2:].copy().view(np.int8).astype(np.float64)
+    return (d * q).reshape(n, k)
+
+
+def dequant_q5k_numpy(w, n, k):
+    """[n, k] float64 from Q5_K bytes, in the bit-mask form of the reference's
+    Q5_K decode kernel (quant_linear.metal:356-406): for iq in {0, 1, 2, 3}
+    (two per 128-element half) and l < 32, low nibbles of qs[32 iq + l] with qh
+    bit 2 iq, high nibbles with bit 2 iq + 1 (hm1..hm4), scales and mins from
+    the kmask words -- not the per-element addressing of the oracle."""
+    nb = k // 256
+    blk = w.reshape(n, nb, 176)
+    d = blk[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    dmin = blk[:, :, 2:4].copy().view(np.float16).astype(np.float64)[..., 0]
+    sc, mn = scale_min_kmask(blk[:, :, 4:16])
+    qh = blk[:, :, 16:48].astype(np.int64)
+    qs = blk[:, :, 48:176].astype(np.int64)
+    out = np.zeros((n, nb, 256), np.float64)
+    l = np.arange(32)
+    for iq in range(4):
+        q = qs[:, :, 32 * iq + l]
+        lo = (q & 0x0F) + np.where(qh & (1 << (2 * iq)), 16, 0)
+        hi = (q & 0xF0) / 16 + np.where(qh & (1 << (2 * iq + 1)), 16, 0)
+        for j, v in ((2 * iq, lo), (2 * iq + 1, hi)):
+            out[:, :, 32 * j + l] = d[..., None] * sc[:, :, j:j + 1] * v - dmin[..., None] * mn[:, :, j:j + 1]
+    return out.reshape(n, k)
+
+
+def dequant_iq4xs_numpy(w, n, k):
+    """[n, k] float64 from IQ4_XS bytes, in the form of the reference's fused
+    IQ4_XS decode (fused_kernels.metal:159-174): for sub-block part and il in
+    {0, 1}, the words of qs[16 part + 8 il ..] masked with 0x0f0f0f0f give
+    elements 32 part + 8 il + [0, 8) and, shifted by 4, the same + 16."""
+    nb = k // 256
+    blk = w.reshape(n, nb, 136)
+    d = blk[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    sh = blk[:, :, 2].astype(np.int64) | (blk[:, :, 3].astype(np.int64) << 8)
+    out = np.zeros((n, nb, 256), np.float64)
+    for part in range(8):
+        ls = ((blk[:, :, 4 + part // 2].astype(np.int64) >> (4 * (part % 2))) & 15) | (((sh >> (2 * part)) & 3) << 4)
+        for il in range(2):
+            words = blk[:, :, 8 + 16 * part + 8 * il:8 + 16 * part + 8 * il + 8].copy().view(np.uint32).astype(np.int64)
+            for wi in range(2):
+                lo = (words[:, :, wi] & 0x0F0F0F0F)
+                hi = ((words[:, :, wi] >> 4) & 0x0F0F0F0F)
+                for b in range(4):
+                    e = 32 * part + 8 * il + 4 * wi + b
+                    out[:, :, e] = d * (ls - 32) * IQ4NL[(lo >> (8 * b)) & 15]
+                    out[:, :, e + 16] = d * (ls - 32) * IQ4NL[(hi >> (8 * b)) & 15]
+    return out.reshape(n, k)
+
+
+_DEQUANT = {TYPE_Q4_K: dequant_numpy, TYPE_Q6_K: dequant_q6k_numpy, TYPE_Q8_0: dequant_q8_0_numpy, TYPE_Q5_K: dequant_q5k_numpy,
+            TYPE_IQ4_XS: dequant_iq4xs_numpy}
+
+
 def dequant_any_numpy(w, n, k, ggml_type):
-    return dequant_q6k_numpy(w, n, k) if ggml_type == TYPE_Q6_K else dequant_numpy(w, n, k)
+    return _DEQUANT[ggml_type](w, n, k)
 
 
 def silu64(g):
@@ -174,6 +264,16 @@ def load_oracle():
     lib.q6o_scale.argtypes = [u8p, i]
     lib.q6o_dequant_block.argtypes = [u8p, p]
     lib.q6o_dequant_block_f16.argtypes = [u8p, p]
+    for name in ("q8o_dequant_block", "q5o_dequant_block", "iq4o_dequant_block"):
+        getattr(lib, name).argtypes = [u8p, p]
+    lib.q5o_quant.restype = i
+    lib.q5o_quant.argtypes = [u8p, i]
+    lib.iq4o_index.restype = i
+    lib.iq4o_index.argtypes = [u8p, i]
+    lib.iq4o_scale.restype = i
+    lib.iq4o_scale.argtypes = [u8p, i]
+    lib.iq4o_value.restype = ctypes.c_float
+    lib.iq4o_value.argtypes = [i]
     lib.q4o_phase.restype = i
     lib.q4o_phase.argtypes = [ctypes.POINTER(ctypes.c_uint32), i, i]
     lib.q4o_pack.restype = ctypes.c_uint32
@@ -244,7 +344,8 @@ class Oracle:
 
     def dequant_block(self, blk, ggml_type=TYPE_Q4_K):
         out = np.empty(256, np.float32)
-        fn = self.lib.q6o_dequant_block if ggml_type == TYPE_Q6_K else self.lib.q4o_dequant_block
+        fn = {TYPE_Q6_K: self.lib.q6o_dequant_block, TYPE_Q8_0: self.lib.q8o_dequant_block, TYPE_Q5_K: self.lib.q5o_dequant_block,
+              TYPE_IQ4_XS: self.lib.iq4o_dequant_block}.get(ggml_type, self.lib.q4o_dequant_block)
         fn(self._p(np.ascontiguousarray(blk, np.uint8)), self._p(out))
         return out
 
