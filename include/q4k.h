@@ -39,7 +39,10 @@ extern "C" {
 #define Q4K_ENOTFOUND (-8) /* missing file, tensor or metadata key */
 
 #define Q4K_GGML_TYPE_Q4_K 12u
-#define Q4K_GGML_TYPE_Q6_K 14u /* the Q6_K LM head / mixed-type files (quant_linear.metal:69-86,437-497) */
+#define Q4K_GGML_TYPE_Q6_K 14u   /* the Q6_K LM head / mixed-type files (quant_linear.metal:69-86,437-497) */
+#define Q4K_GGML_TYPE_Q8_0 8u    /* quant_linear.metal:89-100, 513-570 */
+#define Q4K_GGML_TYPE_Q5_K 13u   /* quant_linear.metal:50-67, 329-435 */
+#define Q4K_GGML_TYPE_IQ4_XS 23u /* quant_linear.metal:102-115; fused_kernels.metal:156-200 */
 
 #define Q4K_DTYPE_F32 0u
 #define Q4K_DTYPE_F16 1u
@@ -67,13 +70,15 @@ typedef struct q4k_weight q4k_weight;
 const char* q4k_last_error(void);
 
 /* Upload one GGUF tensor of type Q4_K (n rows of k/256 block_q4_K records,
- * 144 B each) or Q6_K (block_q6_K, 210 B each); ggml ne[0] = k, ne[1] = n.
+ * 144 B each), Q6_K (210 B per 256), Q5_K (176), IQ4_XS (136) or Q8_0 (eight
+ * 34-byte records per 256); ggml ne[0] = k, ne[1] = n.
  * The bytes are re-laid out for the kernels during the upload; the caller's
  * buffer is not retained.  Replaces the zero-copy Weight view built by
  * loadWeights (model/qwen35/forward.cpp:12-23, qwen35.hpp:34-37), whose
- * Weight keys its kernels on the type (forward.cpp:55-57).  Q6_K weights
- * serve q4k_linear and the two-call form of the gated projection; the fused
- * gate/up kernel and q4k_embedding take Q4_K only (Q4K_ETYPE otherwise). */
+ * Weight keys its kernels on the type (forward.cpp:55-57).  The types other
+ * than Q4_K serve q4k_linear and the two-call form of the gated projection;
+ * the fused gate/up kernel and q4k_embedding take Q4_K only (Q4K_ETYPE
+ * otherwise). */
 int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device, q4k_weight** out);
 
 /* Same, from bytes already in device memory of `device` (GGUF order). */
@@ -232,7 +237,8 @@ int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops);
 int q4k_relayout_host(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k);
 int q4k_unrelayout_host(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k);
 
-/* Same for ggml type Q4_K or Q6_K (n * (k / 256) * 144 or 210 bytes). */
+/* Same for any served ggml type (n * (k / 256) * bytes per 256); the inverse
+ * covers Q4_K and Q6_K (Q4K_ETYPE for the others). */
 int q4k_relayout_host_typed(const void* gguf_bytes, void* tiled, uint32_t n, uint32_t k, uint32_t ggml_type);
 int q4k_unrelayout_host_typed(const void* tiled, void* gguf_bytes, uint32_t n, uint32_t k, uint32_t ggml_type);
 

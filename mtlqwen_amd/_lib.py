@@ -23,7 +23,11 @@ ENOTFOUND = -8
 
 GGML_TYPE_Q4_K = 12
 GGML_TYPE_Q6_K = 14
-BLOCK_BYTES_BY_TYPE = {GGML_TYPE_Q4_K: 144, GGML_TYPE_Q6_K: 210}
+GGML_TYPE_Q8_0 = 8
+GGML_TYPE_Q5_K = 13
+GGML_TYPE_IQ4_XS = 23
+# bytes per 256 weights
+BLOCK_BYTES_BY_TYPE = {GGML_TYPE_Q4_K: 144, GGML_TYPE_Q6_K: 210, GGML_TYPE_Q8_0: 272, GGML_TYPE_Q5_K: 176, GGML_TYPE_IQ4_XS: 136}
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 POST_STORE, POST_ADD, POST_GATE = 0, 1, 2

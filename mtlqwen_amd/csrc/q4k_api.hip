@@ -152,12 +152,27 @@ size_t q4k_bytes(uint32_t n, uint32_t k) {
 }
 
 size_t type_bytes(uint32_t n, uint32_t k, uint32_t type) {
-  return (size_t)n * (k / 256) * (type == Q4K_GGML_TYPE_Q6_K ? kQ6BlockBytes : kBlockBytes);
+  return (size_t)n * (k / 256) * (size_t)type_block_bytes(type);
+}
+
+const char* type_name(uint32_t type) {
+  switch (type) {
+    case Q4K_GGML_TYPE_Q6_K:
+      return "q6_k";
+    case Q4K_GGML_TYPE_Q8_0:
+      return "q8_0";
+    case Q4K_GGML_TYPE_Q5_K:
+      return "q5_k";
+    case Q4K_GGML_TYPE_IQ4_XS:
+      return "iq4_xs";
+    default:
+      return "q4_k";
+  }
 }
 
 int check_shape(uint32_t n, uint32_t k, uint32_t type, size_t bytes) {
-  if (type != Q4K_GGML_TYPE_Q4_K && type != Q4K_GGML_TYPE_Q6_K)
-    return fail(Q4K_ETYPE, "unsupported ggml type %u (Q4_K = 12 or Q6_K = 14)", type);
+  if (type_block_bytes(type) == 0)
+    return fail(Q4K_ETYPE, "unsupported ggml type %u (Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ4_XS = 23)", type);
   if (n == 0 || k == 0 || k % 256 != 0)
     return fail(Q4K_ESHAPE, "k must be a positive multiple of 256 (got k=%u, n=%u)", k, n);
   if (n % 16 != 0)
@@ -208,56 +223,48 @@ void relayout(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, bool for
     }
 }
 
-// Host form of the Q6_K tiled layout (q4k_internal.h); `forward` selects
-// GGUF -> tiled, else tiled -> GGUF.
-void relayout_q6(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, bool forward) {
+// Host form of the tiled layouts of the types other than Q4_K (encode_lane,
+// q4k_internal.h): GGUF -> tiled.
+void relayout_encode(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type) {
+  const uint32_t nb = k / 256;
+  const size_t bb = (size_t)type_block_bytes(type);
+  for (uint32_t c = 0; c < n / 16; ++c)
+    for (uint32_t b = 0; b < nb; ++b) {
+      uint8_t* tb = dst + ((size_t)c * nb + b) * 16 * bb;
+      for (int l = 0; l < 64; ++l)
+        encode_lane(type, src + ((size_t)(16 * c + (l & 15)) * nb + b) * bb, tb, l);
+    }
+}
+
+// Tiled -> GGUF for Q6_K (the layout tooling's inverse; dst zeroed first).
+void relayout_q6_inverse(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k) {
   const uint32_t nb = k / 256;
   for (uint32_t c = 0; c < n / 16; ++c)
     for (uint32_t b = 0; b < nb; ++b) {
       const size_t tb = ((size_t)c * nb + b) * kQ6TileBlockBytes;
       for (uint32_t l = 0; l < 64; ++l) {
         const uint32_t i = l & 15, g = l >> 4;
-        const size_t blk = ((size_t)(16 * c + i) * nb + b) * kQ6BlockBytes;
+        uint8_t* out = dst + ((size_t)(16 * c + i) * nb + b) * kQ6BlockBytes;
         uint32_t wd[12] = {0};
-        if (forward) {
-          for (int o = 0; o < 32; ++o)
-            for (int hf = 0; hf < 2; ++hf)
-              q6_place(wd, o, hf, q6_quant(src + blk, q6_elem((int)g, o, hf)));
-          for (int s = 0; s < 3; ++s)
-            std::memcpy(dst + tb + s * 1024 + 16 * l, wd + 4 * s, 16);
-          for (int j = 0; j < 4; ++j)
-            dst[tb + kQ6ScaleOffset + 4 * l + j] = (uint8_t)(src[blk + 192 + 4 * g + j] ^ 0x80u);
-          if (g == 0)
-            std::memcpy(dst + tb + kQ6DOffset + 2 * i, src + blk + 208, 2);
-        } else {
-          for (int s = 0; s < 3; ++s)
-            std::memcpy(wd + 4 * s, src + tb + s * 1024 + 16 * l, 16);
-          uint8_t* out = dst + blk;
-          for (int o = 0; o < 32; ++o)
-            for (int hf = 0; hf < 2; ++hf) {
-              // Inverse of q6_quant's addressing for element e.
-              const int e = q6_elem((int)g, o, hf), h = e >> 7, rr = e & 127, ll = rr & 31;
-              const uint32_t v = q6_take(wd, o, hf);
-              uint8_t& qb = out[64 * h + (rr & 32) + ll];
-              qb = (rr & 64) ? (uint8_t)((qb & 0x0Fu) | ((v & 15u) << 4)) : (uint8_t)((qb & 0xF0u) | (v & 15u));
-              uint8_t& hb = out[128 + 32 * h + ll];
-              const int sh = 2 * (rr >> 5);
-              hb = (uint8_t)((hb & ~(3u << sh)) | ((v >> 4) << sh));
-            }
-          for (int j = 0; j < 4; ++j)
-            out[192 + 4 * g + j] = (uint8_t)(src[tb + kQ6ScaleOffset + 4 * l + j] ^ 0x80u);
-          if (g == 0)
-            std::memcpy(out + 208, src + tb + kQ6DOffset + 2 * i, 2);
-        }
+        for (int s2 = 0; s2 < 3; ++s2)
+          std::memcpy(wd + 4 * s2, src + tb + s2 * 1024 + 16 * l, 16);
+        for (int o = 0; o < 32; ++o)
+          for (int hf = 0; hf < 2; ++hf) {
+            // Inverse of q6_quant's addressing for element e.
+            const int e = q6_elem((int)g, o, hf), h = e >> 7, rr = e & 127, ll = rr & 31;
+            const uint32_t v = q6_take(wd, o, hf);
+            uint8_t& qb = out[64 * h + (rr & 32) + ll];
+            qb = (rr & 64) ? (uint8_t)((qb & 0x0Fu) | ((v & 15u) << 4)) : (uint8_t)((qb & 0xF0u) | (v & 15u));
+            uint8_t& hb = out[128 + 32 * h + ll];
+            const int sh = 2 * (rr >> 5);
+            hb = (uint8_t)((hb & ~(3u << sh)) | ((v >> 4) << sh));
+          }
+        for (int j = 0; j < 4; ++j)
+          out[192 + 4 * g + j] = (uint8_t)(src[tb + kQ6ScaleOffset + 4 * l + j] ^ 0x80u);
+        if (g == 0)
+          std::memcpy(out + 208, src + tb + kQ6DOffset + 2 * i, 2);
       }
     }
-}
-
-void relayout_typed(const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type, bool forward) {
-  if (type == Q4K_GGML_TYPE_Q6_K)
-    relayout_q6(src, dst, n, k, forward);
-  else
-    relayout(src, dst, n, k, forward);
 }
 
 // forward.cpp:52 with the decode flag accumulated as in forward.cpp:190.
@@ -294,11 +301,12 @@ Kernel& resolve(q4k_weight* w, uint32_t phase) {
   if (k.kind == kNone) {
     const char* suffix[] = {"decode", "prefill", "prefill_small", "gate_up_decode"};
     k.kind = phase == Q4K_PHASE_GATED_DECODE ? kGemvGated : phase == Q4K_PHASE_PREFILL ? kGemm : kGemv;
-    const bool q6 = w->type == Q4K_GGML_TYPE_Q6_K;
-    if (q6 && k.kind == kGemm)
-      k.kind = kGemv;  // Q6_K prefill: the GEMV per group of 8 rows
-    k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + (q6 ? "q6_k_k" : "q4_k_k") + std::to_string(w->k) + "_n" +
-             std::to_string(w->n) + "_" + suffix[phase] + (k.kind == kGemm ? "_mfma32x32x16" : q6 && phase == Q4K_PHASE_PREFILL ? "_mfma16x16x32_rows8" : "_mfma16x16x32");
+    const bool other = w->type != Q4K_GGML_TYPE_Q4_K;
+    if (other && k.kind == kGemm)
+      k.kind = kGemv;  // prefill of the other types: the GEMV per group of 8 rows
+    k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + type_name(w->type) + "_k" + std::to_string(w->k) + "_n" +
+             std::to_string(w->n) + "_" + suffix[phase] +
+             (k.kind == kGemm ? "_mfma32x32x16" : other && phase == Q4K_PHASE_PREFILL ? "_mfma16x16x32_rows8" : "_mfma16x16x32");
   }
   return k;
 }
@@ -451,9 +459,10 @@ int set_device(int device) {
 // previous call, which must have been a projection of the same x with the
 // same (m, k, n) under the same lock; the decode pack and split-K paths always
 // stage (they are not reached by such pairs).
-// Q6_K projection (wu == nullptr): per group of up to 8 rows, the decode pack
-// of the group's x, then the Q6_K GEMV over the group's rows of y and aux.
-int run_q6k_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
+// Projection with weights of a type other than Q4_K (wu == nullptr): per group
+// of up to 8 rows, the decode pack of the group's x, then the type's GEMV over
+// the group's rows of y and aux.
+int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
                    uint32_t dtype) {
   const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
   for (uint32_t r0 = 0; r0 < m; r0 += 8) {
@@ -475,18 +484,18 @@ int run_q6k_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void*
     a.rows = 2 * (int)mg;
     a.split = 1;
     LaunchTimer timer(stream, Q4K_KERNEL_GEMV);
-    Q4K_TRY_HIP(launch_q6k_gemv(stream, a, (int)dtype, device_cus(w->device)), "q6_k gemv launch");
+    Q4K_TRY_HIP(launch_typed_gemv(stream, a, w->type, (int)dtype, device_cus(w->device)), "typed gemv launch");
   }
   return Q4K_OK;
 }
 
 int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m,
                       uint32_t post, uint32_t dtype, uint32_t phase, bool restage) {
-  if (w->type == Q4K_GGML_TYPE_Q6_K) {
+  if (w->type != Q4K_GGML_TYPE_Q4_K) {
     if (wu)
       return fail(Q4K_ETYPE, "the fused gate/up kernel takes Q4_K weights");
     resolve(w, phase);
-    return run_q6k_locked(stream, ws, w, x, y, aux, m, post, dtype);
+    return run_typed_locked(stream, ws, w, x, y, aux, m, post, dtype);
   }
   Kernel& kern = resolve(w, phase);
   if (wu)
@@ -649,7 +658,10 @@ int q4k_relayout_host_typed(const void* gguf_bytes, void* tiled, uint32_t n, uin
   int rc = check_shape(n, k, ggml_type, type_bytes(n, k, ggml_type));
   if (rc)
     return rc;
-  relayout_typed(static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(tiled), n, k, ggml_type, true);
+  if (ggml_type == Q4K_GGML_TYPE_Q4_K)
+    relayout(static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(tiled), n, k, true);
+  else
+    relayout_encode(static_cast<const uint8_t*>(gguf_bytes), static_cast<uint8_t*>(tiled), n, k, ggml_type);
   return Q4K_OK;
 }
 
@@ -659,9 +671,14 @@ int q4k_unrelayout_host_typed(const void* tiled, void* gguf_bytes, uint32_t n, u
   int rc = check_shape(n, k, ggml_type, type_bytes(n, k, ggml_type));
   if (rc)
     return rc;
-  if (ggml_type == Q4K_GGML_TYPE_Q6_K)
+  if (ggml_type == Q4K_GGML_TYPE_Q4_K) {
+    relayout(static_cast<const uint8_t*>(tiled), static_cast<uint8_t*>(gguf_bytes), n, k, false);
+  } else if (ggml_type == Q4K_GGML_TYPE_Q6_K) {
     std::memset(gguf_bytes, 0, type_bytes(n, k, ggml_type));  // the inverse merges bit fields into place
-  relayout_typed(static_cast<const uint8_t*>(tiled), static_cast<uint8_t*>(gguf_bytes), n, k, ggml_type, false);
+    relayout_q6_inverse(static_cast<const uint8_t*>(tiled), static_cast<uint8_t*>(gguf_bytes), n, k);
+  } else {
+    return fail(Q4K_ETYPE, "the inverse re-layout covers Q4_K and Q6_K (got type %u)", ggml_type);
+  }
   return Q4K_OK;
 }
 
@@ -680,7 +697,10 @@ int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t
   if (rc)
     return rc;
   std::vector<uint8_t> tiled(bytes);
-  relayout_typed(static_cast<const uint8_t*>(gguf_bytes), tiled.data(), n, k, ggml_type, true);
+  if (ggml_type == Q4K_GGML_TYPE_Q4_K)
+    relayout(static_cast<const uint8_t*>(gguf_bytes), tiled.data(), n, k, true);
+  else
+    relayout_encode(static_cast<const uint8_t*>(gguf_bytes), tiled.data(), n, k, ggml_type);
   q4k_weight* w = new (std::nothrow) q4k_weight;
   if (!w)
     return fail(Q4K_ENOMEM, "host allocation failed");
@@ -731,8 +751,9 @@ int q4k_weight_create_from_device(const void* gguf_device_bytes, size_t bytes, u
     return fail(Q4K_ENOMEM, "cannot allocate %zu bytes of weights on device %d", bytes, device);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = ggml_type == Q4K_GGML_TYPE_Q6_K ? launch_q6k_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k)
-                                                 : launch_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k);
+  hipError_t e = ggml_type == Q4K_GGML_TYPE_Q4_K
+                    ? launch_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k)
+                    : launch_typed_relayout(s, static_cast<const uint8_t*>(gguf_device_bytes), w->data, n, k, ggml_type);
   if (e == hipSuccess)
     e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
@@ -865,7 +886,7 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
   rc = run_linear_locked(s, ws, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, true);
   if (rc)
     return rc;
-  // The Q4_K projection of a Q4_K pair reuses the staged x; Q6_K packs its own.
+  // The Q4_K projection of a Q4_K pair reuses the staged x; other types pack their own.
   return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, !q4);
 }
 

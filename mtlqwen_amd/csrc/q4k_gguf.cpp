@@ -453,8 +453,9 @@ int q4k_weight_from_gguf(const q4k_gguf* g, const char* name, int device, q4k_we
   if (rc)
     return rc;
   const Tensor& t = g->tensors[(size_t)i];
-  if (t.type != Q4K_GGML_TYPE_Q4_K && t.type != Q4K_GGML_TYPE_Q6_K)
-    return gfail(Q4K_ETYPE, "tensor %s has ggml type %u, not Q4_K or Q6_K", name, t.type);
+  if (t.type != Q4K_GGML_TYPE_Q4_K && t.type != Q4K_GGML_TYPE_Q6_K && t.type != Q4K_GGML_TYPE_Q8_0 && t.type != Q4K_GGML_TYPE_Q5_K &&
+      t.type != Q4K_GGML_TYPE_IQ4_XS)
+    return gfail(Q4K_ETYPE, "tensor %s has ggml type %u, not one the linear path serves", name, t.type);
   if (t.n_dims != 2 || t.ne[0] > UINT32_MAX || t.ne[1] > UINT32_MAX)
     return gfail(Q4K_ESHAPE, "tensor %s is not a 2-D matrix within 32-bit dimensions", name);
   const void* data = static_cast<const uint8_t*>(g->map) + g->data_offset + t.offset;

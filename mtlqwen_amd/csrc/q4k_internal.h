@@ -101,6 +101,120 @@ __host__ __device__ inline uint32_t q6_take(const uint32_t* wd, int o, int hf) {
   }
 }
 
+// ---- the other GGUF types on the same surface ------------------------------
+// Per 256 elements: block_q8_0 is eight 34-byte records (d fp16, 32 int8),
+// block_q5_K 176 bytes (d, dmin, the Q4_K 6-bit scale/min bytes, qh[32],
+// qs[128]), block_iq4_xs 136 bytes (d, scales_h, scales_l[4], qs[128]).  Every
+// tile-block keeps its type's byte count (16 rows x one block):
+//   Q8_0 (4352 B): four slabs, lane l = 16g + i holding the 64 quants of its
+//     elements (the Q6_K element order) as bytes q ^ 0x80, byte 2o + hf of the
+//     lane for B dword o, half hf; then lane l's dword at 4096 + 4l with d of
+//     records 2g, 2g + 1 of row 16c + i.
+//   Q5_K (2816 B): the Q4_K tile-block of the low nibbles and headers (2304 B),
+//     then lane l's two dwords at 2304 + 8l with the fifth bits: bit
+//     4 (fs % 4) + t (+16 for the high half) of dword fs / 4 for B dword t of
+//     MFMA fs.
+//   IQ4_XS (2176 B): two slabs, lane l's dword fs (slab fs / 4, word fs % 4)
+//     holding the codebook indices of MFMA fs: byte b's low nibble for value
+//     b, its high nibble for value 4 + b (value h = B dword h / 2, half h % 2);
+//     then the 16 rows' first 8 bytes (d, scales_h, scales_l) at 2048 + 8i.
+constexpr int kQ8BlockBytes = 272;
+constexpr int kQ5BlockBytes = 176;
+constexpr int kIQ4BlockBytes = 136;
+constexpr uint32_t kTypeQ8_0 = 8, kTypeQ4_K = 12, kTypeQ5_K = 13, kTypeQ6_K = 14, kTypeIQ4_XS = 23;
+
+// Bytes per 256-element block of a served ggml type (0 if not served).
+__host__ __device__ inline int type_block_bytes(uint32_t type) {
+  switch (type) {
+    case kTypeQ4_K:
+      return kBlockBytes;
+    case kTypeQ6_K:
+      return kQ6BlockBytes;
+    case kTypeQ8_0:
+      return kQ8BlockBytes;
+    case kTypeQ5_K:
+      return kQ5BlockBytes;
+    case kTypeIQ4_XS:
+      return kIQ4BlockBytes;
+    default:
+      return 0;
+  }
+}
+
+__host__ __device__ inline void put_u32(uint8_t* p, uint32_t v) {
+  p[0] = (uint8_t)v;
+  p[1] = (uint8_t)(v >> 8);
+  p[2] = (uint8_t)(v >> 16);
+  p[3] = (uint8_t)(v >> 24);
+}
+
+// Lane `lane`'s share of one tile-block `tb` of a Q6_K, Q8_0, Q5_K or IQ4_XS
+// tensor, from block `blk` of row 16c + lane % 16 (lanes 0..15 also write
+// their row's per-row bytes).  Shared by the host and device re-layouts.
+__host__ __device__ inline void encode_lane(uint32_t type, const uint8_t* blk, uint8_t* tb, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  if (type == kTypeQ6_K) {
+    uint32_t wd[12] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    for (int o = 0; o < 32; ++o)
+      for (int hf = 0; hf < 2; ++hf)
+        q6_place(wd, o, hf, q6_quant(blk, q6_elem(g, o, hf)));
+    for (int j = 0; j < 12; ++j)
+      put_u32(tb + (j >> 2) * 1024 + 16 * lane + 4 * (j & 3), wd[j]);
+    for (int j = 0; j < 4; ++j)
+      tb[kQ6ScaleOffset + 4 * lane + j] = (uint8_t)(blk[192 + 4 * g + j] ^ 0x80u);
+    if (g == 0) {
+      tb[kQ6DOffset + 2 * i] = blk[208];
+      tb[kQ6DOffset + 2 * i + 1] = blk[209];
+    }
+  } else if (type == kTypeQ8_0) {
+    for (int o = 0; o < 32; ++o)
+      for (int hf = 0; hf < 2; ++hf) {
+        const int e = q6_elem(g, o, hf), byte = 2 * o + hf;
+        tb[(byte >> 4) * 1024 + 16 * lane + (byte & 15)] = (uint8_t)(blk[34 * (e >> 5) + 2 + (e & 31)] ^ 0x80u);
+      }
+    const uint8_t* r0 = blk + 34 * (2 * g);
+    const uint8_t* r1 = blk + 34 * (2 * g + 1);
+    put_u32(tb + 4096 + 4 * lane, (uint32_t)r0[0] | ((uint32_t)r0[1] << 8) | ((uint32_t)r1[0] << 16) | ((uint32_t)r1[1] << 24));
+  } else if (type == kTypeQ5_K) {
+    // Low nibbles and header exactly as Q4_K (its qs sit at byte 48, not 16).
+    for (int h = 0; h < 2; ++h)
+      for (int w = 0; w < 4; ++w) {
+        const uint8_t* q = blk + 48 + 32 * g + 16 * h + 4 * w;
+        uint8_t* t = tb + h * kSlabBytes + 16 * lane + 4 * w;
+        t[0] = q[0];
+        t[1] = q[2];
+        t[2] = q[1];
+        t[3] = q[3];
+      }
+    if (g == 0)
+      for (int j = 0; j < 16; ++j)
+        tb[kHeaderOffset + 16 * i + j] = blk[j];
+    uint32_t hw[2] = {0u, 0u};
+    for (int fs = 0; fs < 8; ++fs)
+      for (int t = 0; t < 4; ++t)
+        for (int hf = 0; hf < 2; ++hf) {
+          const int e = q6_elem(g, 4 * fs + t, hf);
+          const uint32_t bit = (blk[16 + (e & 31)] >> (2 * (e >> 6) + ((e >> 5) & 1))) & 1u;
+          hw[fs >> 2] |= bit << (4 * (fs & 3) + t + 16 * hf);
+        }
+    put_u32(tb + 2304 + 8 * lane, hw[0]);
+    put_u32(tb + 2304 + 8 * lane + 4, hw[1]);
+  } else if (type == kTypeIQ4_XS) {
+    for (int fs = 0; fs < 8; ++fs) {
+      uint32_t w = 0;
+      for (int h = 0; h < 8; ++h) {
+        const int e = q6_elem(g, 4 * fs + (h >> 1), h & 1);
+        const uint32_t v = (blk[8 + 16 * (e >> 5) + (e & 15)] >> (4 * ((e >> 4) & 1))) & 15u;
+        w |= v << (h < 4 ? 8 * h : 8 * (h - 4) + 4);
+      }
+      put_u32(tb + (fs >> 2) * 1024 + 16 * lane + 4 * (fs & 3), w);
+    }
+    if (g == 0)
+      for (int j = 0; j < 8; ++j)
+        tb[2048 + 8 * i + j] = blk[j];
+  }
+}
+
 // Rows of a GEMV call are padded to 16-row MFMA tiles; the GEMV handles up to
 // kGemvMaxRowTiles of them (48 rows: the 8 x 5 decode rows of the reference).
 constexpr int kGemvMaxRowTiles = 3;
@@ -236,12 +350,13 @@ hipError_t launch_rms_norm(hipStream_t s, const void* x, const float* w, void* y
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).
 hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
 
-// Q6_K GEMV for m <= 8 rows: a.w = tiled Q6_K weights, a.pack = the decode
-// pack of x (launch_stage_pack), post 0/1/2 on a.y / a.aux.
-hipError_t launch_q6k_gemv(hipStream_t s, const GemvArgs& a, int dtype, int cus);
+// GEMV of the other GGUF types for m <= 8 rows: a.w = tiled weights of ggml
+// type `type` (Q6_K, Q8_0, Q5_K or IQ4_XS), a.pack = the decode pack of x
+// (launch_stage_pack), post 0/1/2 on a.y / a.aux.
+hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus);
 
-// Device-side GGUF -> tiled re-layout of block_q6_K weights.
-hipError_t launch_q6k_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
+// Device-side GGUF -> tiled re-layout of Q6_K, Q8_0, Q5_K or IQ4_XS weights.
+hipError_t launch_typed_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type);
 
 // ---- dispatch --------------------------------------------------------------
 // Events attached to the calling thread's next kernel dispatches (both null

@@ -2115,31 +2115,68 @@ __global__ __launch_bounds__(64) void relayout_kernel(const uint8_t* __restrict_
 }
 
 // ----------------------------------------------------------------------------
-// Q6_K (ggml type 14) on the same linear() surface: the LM head and the
-// down projections of mixed-type GGUF files (quant_linear.metal:69-86,
-// 437-497).
+// The other GGUF types on the same linear() surface: Q6_K (the LM head of real
+// files, mixed-type down projections), Q8_0, Q5_K and IQ4_XS
+// (quant_linear.metal:50-115 dequant, :329-570 decode GEMVs, :620-662 shapes;
+// fused_kernels.metal:80-200).
 //
-// GEMV for m <= 8 rows (decode, small prefill, LM head).  The B operand of
-// v_mfma_f32_16x16x32_f16 is (q - 32) * sc in fp16, built two quants per
-// dword: a quant stored at bits 4..9 of a half, masked and or'ed with 0x6400,
-// is the fp16 value 1024 + 16q, and one v_pk_fma_f16 with (sc / 16, -96 sc)
-// leaves (q - 32) * sc (|.| <= 4096: exact up to 2048, above that rounded
-// once to an even integer, a relative error below 2^-11 on those products).
-// The scales arrive biased (sc + 128), so one v_perm_b32 with 0x64 bytes makes
-// the fp16 value 1152 + sc.  The activations are the decode pack (hi / lo
-// fp16 rows 0..7 / 8..15, per-(row, block) power-of-two scale) from the
-// workspace.
+// GEMV for m <= 8 rows (decode, small prefill, LM head) over the decode pack
+// of x (hi / lo fp16 rows 0..7 / 8..15, per-(row, block) power-of-two scale;
+// the sub-block sums for the Q5_K min term).  A format policy F supplies the
+// per-lane registers of one tile-block (U), their loads, and `mac`: the eight
+// B operands of v_mfma_f32_16x16x32_f16 in fp16, the MFMAs, and the tile-
+// block's contribution scaled into the lane's four accumulator rows:
+//   Q6_K   (q - 32) * sc per dword: (w & 0x03F003F0) | 0x6400 = 1024 + 16q for
+//          two quants stored at bits 4..9 of each half, one v_pk_fma_f16 with
+//          (sc / 16, -96 sc); d * row unscale after the MFMAs.
+//   Q8_0   q * d per dword: v_perm_b32 of two biased bytes with 0x64 bytes is
+//          1024 + 128 + q; v_pk_add_f16 -1152 leaves q, v_pk_mul_f16 by the
+//          record's d (one rounding); row unscale after the MFMAs.
+//   Q5_K   the Q4_K nibble decode with the fifth bit or'ed into the fp16 bias
+//          (16 for low nibbles, 256 for high ones), q * sc exact (<= 1953), the
+//          min term on a 16x16x16 MFMA of the sub-block sums.
+//   IQ4_XS codebook lookup of four indices per v_perm_b32 pair (entries 0..7,
+//          8..15, selected by bit 3 with v_bfi_b32), biased bytes to fp16 as for
+//          Q8_0, one v_pk_fma_f16 with (ls - 32, -1152 (ls - 32)).
+// Products above 2048 in magnitude (Q6_K, IQ4_XS) and q * d (Q8_0) are
+// rounded once to fp16; the reference's prefill tiles round every dequantised
+// weight to fp16 (quant_linear.metal:65,83,98,112).
 //
-// Workgroup = 8 waves over T column tiles; wave w takes blocks w, w + 8, ...
-// For each block it holds the x fragments (the next block's are loaded while
-// the current one runs) and streams its T tile-blocks through a register
-// window DQ tile-blocks deep: three 16-byte quant loads, one scale dword and
-// the column's d per lane.  Two MFMA chains per tile-block; the partial sums
-// of the 8 waves meet in LDS in wave order before the epilogue.
+// Workgroup = 8 waves; wave w takes blocks w, w + 8, ...  The persistent form
+// (K = 4096, 16 blocks: two per wave) keeps each wave's x fragments in
+// registers and streams every item (T column tiles) it owns through one
+// register window that runs across item boundaries; partial sums alternate
+// between two LDS buffers, one barrier per item.  The other form (any K)
+// takes one item per workgroup, double-buffers the next block's x fragments
+// and streams its T tile-blocks per block through a window DQ deep.
 // ----------------------------------------------------------------------------
 
-// Outputs o = 8a .. 8a+7 of triple (A, B, C) times their scale: b0 = MFMA 2a's
-// four B dwords, b1 = MFMA 2a + 1's (layout in q4k_internal.h).
+struct XF {
+  h8_t f[8];
+  float dv[4];
+  h4_t xs;
+};
+
+template <bool MIN>
+__device__ __forceinline__ void load_xf(XF& xf, const DecodePack& pk, size_t b, int lane) {
+  const u4_t* fr = pk.frag + b * 8 * 64 + lane;
+#pragma unroll
+  for (int fs = 0; fs < 8; ++fs)
+    xf.f[fs] = __builtin_bit_cast(h8_t, fr[fs * 64]);
+  const float* ds = pk.dsc + b * 8 + 4 * ((lane >> 4) & 1);
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    xf.dv[v] = ds[v];
+  if constexpr (MIN)
+    xf.xs = pk.xs[b * 64 + lane];
+}
+
+__device__ __forceinline__ h2_t h2_splat(float v) {
+  return h2_t{(_Float16)v, (_Float16)v};
+}
+
+// Outputs o = 8a .. 8a+7 of Q6_K triple (A, B, C) times their scale: b0 = MFMA
+// 2a's four B dwords, b1 = MFMA 2a + 1's (layout in q4k_internal.h).
 __device__ __forceinline__ void q6_triple(uint32_t A, uint32_t B, uint32_t C, h2_t mul, h2_t add, h8_t& b0, h8_t& b1) {
   const uint32_t m6 = 0x03F003F0u, m4 = 0x00F000F0u, m2 = 0x03000300u, magic = 0x64006400u;
   const uint32_t o0 = and_or(A, m6, magic), o1 = and_or(A >> 6, m6, magic);
@@ -2152,13 +2189,207 @@ __device__ __forceinline__ void q6_triple(uint32_t A, uint32_t B, uint32_t C, h2
   b1 = __builtin_bit_cast(h8_t, u4_t{f(o4), f(o5), f(o6), f(o7)});
 }
 
-struct Q6X {
-  h8_t f[8];
-  float dv[4];
+// Each policy also names the column tiles per item of its persistent form
+// (kPT: the most that stays within the register file without spilling).
+struct FmtQ6K {
+  static constexpr int kTB = kQ6TileBlockBytes;
+  static constexpr bool kMin = false;
+  static constexpr int kPT = 4;
+  struct U {
+    u4_t s0, s1, s2;
+    uint32_t sc, d;
+  };
+  static __device__ __forceinline__ void load(U& u, const uint8_t* src, int lane) {
+    u.s0 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    u.s1 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024) + lane);
+    u.s2 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 2048) + lane);
+    u.sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kQ6ScaleOffset) + lane);
+    u.d = *(reinterpret_cast<const uint16_t*>(src + kQ6DOffset) + (lane & 15));
+  }
+  static __device__ __forceinline__ void mac(const U& u, const XF& x, int, f4_t& acc) {
+    const uint32_t wd[12] = {u.s0[0], u.s0[1], u.s0[2], u.s0[3], u.s1[0], u.s1[1], u.s1[2], u.s1[3], u.s2[0], u.s2[1], u.s2[2], u.s2[3]};
+    const float d = half_bits_to_float(u.d & 0xffffu);
+    f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int tr = 0; tr < 4; ++tr) {
+      // fp16 1152 + sc -> sc / 16 (exact), and -96 sc.
+      const uint32_t sel = 0x04000400u | (uint32_t)tr | ((uint32_t)tr << 16);
+      const h2_t p = as_h2(__builtin_amdgcn_perm(0x64646464u, u.sc, sel));
+      const h2_t mul = __builtin_elementwise_fma(p, h2_splat(0.0625f), h2_splat(-72.0f));
+      const h2_t add = mul * h2_splat(-1536.0f);
+      h8_t b0, b1;
+      q6_triple(wd[3 * tr], wd[3 * tr + 1], wd[3 * tr + 2], mul, add, b0, b1);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[2 * tr], b0, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[2 * tr + 1], b1, c1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      acc[v] = fmaf(c0[v] + c1[v], d * x.dv[v], acc[v]);
+  }
 };
 
-template <int T, int DQ, typename OutT>
-__global__ __launch_bounds__(512) void q6k_gemv_kernel(GemvArgs a) {
+struct FmtQ8_0 {
+  static constexpr int kTB = kTileN * kQ8BlockBytes;
+  static constexpr bool kMin = false;
+  static constexpr int kPT = 4;
+  struct U {
+    u4_t s[4];
+    uint32_t d;
+  };
+  static __device__ __forceinline__ void load(U& u, const uint8_t* src, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      u.s[j] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024 * j) + lane);
+    u.d = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + 4096) + lane);
+  }
+  static __device__ __forceinline__ void mac(const U& u, const XF& x, int, f4_t& acc) {
+    // d of the lane's two records, each in both halves.
+    const h2_t d0 = as_h2(__builtin_amdgcn_perm(u.d, u.d, 0x01000100u)), d1 = as_h2(__builtin_amdgcn_perm(u.d, u.d, 0x03020302u));
+    const h2_t k1152 = h2_splat(-1152.0f);
+    f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int fs = 0; fs < 8; ++fs) {
+      const u4_t sl = u.s[fs >> 1];
+      const uint32_t w0 = sl[2 * (fs & 1)], w1 = sl[2 * (fs & 1) + 1];
+      const h2_t d = fs < 4 ? d0 : d1;
+      auto q = [&](uint32_t w, uint32_t sel) { return as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, w, sel)) + k1152) * d); };
+      const h8_t b = __builtin_bit_cast(h8_t, u4_t{q(w0, 0x04010400u), q(w0, 0x04030402u), q(w1, 0x04010400u), q(w1, 0x04030402u)});
+      if (fs & 1)
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[fs], b, c1, 0, 0, 0);
+      else
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[fs], b, c0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      acc[v] = fmaf(c0[v] + c1[v], x.dv[v], acc[v]);
+  }
+};
+
+struct FmtQ5K {
+  static constexpr int kTB = kTileN * kQ5BlockBytes;
+  static constexpr bool kMin = true;
+  static constexpr int kPT = 2;
+  struct U {
+    u4_t q0, q1, hd;
+    uint32_t h0, h1;
+  };
+  static __device__ __forceinline__ void load(U& u, const uint8_t* src, int lane) {
+    u.q0 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    u.q1 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
+    u.hd = *(reinterpret_cast<const u4_t*>(src + kHeaderOffset) + (lane & 15));
+    typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+    const u2_t h = __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(src + 2304) + lane);
+    u.h0 = h[0];
+    u.h1 = h[1];
+  }
+  // Fifth bits of B dword k (= 4 (fs % 4) + t) moved to bit P of each half,
+  // or'ed with the fp16 bias 0x6400.
+  template <int P>
+  static __device__ __forceinline__ uint32_t bias(uint32_t h, int k) {
+    const uint32_t moved = k < P ? h << (P - k) : h >> (k - P);
+    return and_or(moved, (1u << P) | (1u << (16 + P)), 0x64006400u);
+  }
+  static __device__ __forceinline__ void mac(const U& u, const XF& x, int lane, f4_t& acc) {
+    const BlockConsts kc = block_consts(u.hd, lane >> 4);
+    f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u4_t qq = s < 2 ? u.q0 : u.q1;
+      const uint32_t wa = qq[2 * (s & 1)], wb = qq[2 * (s & 1) + 1];
+      const uint32_t src[4] = {wa, wa >> 8, wb, wb >> 8};
+      u4_t lo, hi;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        lo[t] = as_u32(__builtin_elementwise_fma(as_h2(and_or(src[t], 0x000F000Fu, bias<4>(u.h0, 4 * s + t))), kc.mul_lo, kc.add_lo));
+        hi[t] = as_u32(__builtin_elementwise_fma(as_h2(and_or(src[t], 0x00F000F0u, bias<8>(u.h1, 4 * s + t))), kc.mul_hi, kc.add_hi));
+      }
+      cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[s], __builtin_bit_cast(h8_t, lo), cl, 0, 0, 0);
+      ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[4 + s], __builtin_bit_cast(h8_t, hi), ch, 0, 0, 0);
+    }
+    const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(x.xs, kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      acc[v] += fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * x.dv[v];
+  }
+};
+
+struct FmtIQ4XS {
+  static constexpr int kTB = kTileN * kIQ4BlockBytes;
+  static constexpr bool kMin = false;
+  static constexpr int kPT = 4;
+  struct U {
+    u4_t q0, q1;
+    uint2 hd;
+  };
+  static __device__ __forceinline__ void load(U& u, const uint8_t* src, int lane) {
+    u.q0 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    u.q1 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024) + lane);
+    u.hd = *(reinterpret_cast<const uint2*>(src + 2048) + (lane & 15));
+  }
+  // Codebook entries (iq4nl, quant_linear.metal:5) + 128 as bytes, four per word.
+  static constexpr uint32_t kT0 = 0x3F2D1801u, kT1 = 0x766A5D4Fu, kT2 = 0xA6998D81u, kT3 = 0xF1D9C5B5u;
+  // Four codebook bytes for the four 4-bit indices at bits 0..3 of each byte of w.
+  static __device__ __forceinline__ uint32_t lookup(uint32_t w) {
+    const uint32_t t = w & 0x07070707u;
+    const uint32_t a = __builtin_amdgcn_perm(kT1, kT0, t), b = __builtin_amdgcn_perm(kT3, kT2, t);
+    // Selector byte 0x0C gives 0x00, 0x0D gives 0xFF: a byte mask of bit 3.
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, and_or(w >> 3, 0x01010101u, 0x0C0C0C0Cu));
+    return (m & b) | (~m & a);
+  }
+  static __device__ __forceinline__ void mac(const U& u, const XF& x, int lane, f4_t& acc) {
+    const int g = lane >> 4;
+    const uint32_t sh = u.hd.x >> 16, sl = u.hd.y;
+    const float d = half_bits_to_float(u.hd.x & 0xffffu);
+    // ls - 32 of sub-blocks 2g (MFMAs 0..3) and 2g + 1 (MFMAs 4..7).
+    const int j0 = 2 * g;
+    const int ls0 = (int)(((sl >> (4 * j0)) & 15u) | (((sh >> (2 * j0)) & 3u) << 4)) - 32;
+    const int ls1 = (int)(((sl >> (4 * j0 + 4)) & 15u) | (((sh >> (2 * j0 + 2)) & 3u) << 4)) - 32;
+    const h2_t mul0 = h2_splat((float)ls0), mul1 = h2_splat((float)ls1);
+    const h2_t add0 = mul0 * h2_splat(-1152.0f), add1 = mul1 * h2_splat(-1152.0f);
+    f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int fs = 0; fs < 8; ++fs) {
+      const uint32_t w = (fs < 4 ? u.q0 : u.q1)[fs & 3];
+      const uint32_t vlo = lookup(w), vhi = lookup(w >> 4);
+      const h2_t mul = fs < 4 ? mul0 : mul1, add = fs < 4 ? add0 : add1;
+      auto f = [&](uint32_t v, uint32_t sel) {
+        return as_u32(__builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, v, sel)), mul, add));
+      };
+      const h8_t b = __builtin_bit_cast(h8_t, u4_t{f(vlo, 0x04010400u), f(vlo, 0x04030402u), f(vhi, 0x04010400u), f(vhi, 0x04030402u)});
+      if (fs & 1)
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[fs], b, c1, 0, 0, 0);
+      else
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[fs], b, c0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      acc[v] = fmaf(c0[v] + c1[v], d * x.dv[v], acc[v]);
+  }
+};
+
+template <typename OutT>
+__device__ __forceinline__ void typed_epilogue(const GemvArgs& a, const float* part, int t_count, int tile0, int ntiles) {
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  const int tid = threadIdx.x;
+  for (int o = tid; o < a.m * 16 * t_count; o += 512) {
+    const int row = o / (16 * t_count), c = o % (16 * t_count), t = c >> 4, cc = c & 15;
+    if (tile0 + t >= ntiles)
+      continue;
+    float acc_v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+      acc_v += part[((w * t_count + t) * 8 + row) * 16 + cc];
+    if (sizeof(OutT) == 2)
+      acc_v = round_half(acc_v);
+    const size_t off = (size_t)row * a.n + (size_t)(tile0 + t) * 16 + cc;
+    const float out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+    store_elem(y, off, out);
+  }
+}
+
+template <class F, int T, int DQ, typename OutT>
+__global__ __launch_bounds__(512) void typed_gemv_kernel(GemvArgs a) {
   constexpr int W = 8;
   static_assert(DQ <= T || T == 1, "window");
   constexpr int D = DQ < T ? DQ : T;
@@ -2167,74 +2398,38 @@ __global__ __launch_bounds__(512) void q6k_gemv_kernel(GemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
   const int nb = a.nb, ntiles = a.n >> 4, tile0 = blockIdx.x * T;
-  const size_t tile_bytes = (size_t)nb * kQ6TileBlockBytes;
+  const size_t tile_bytes = (size_t)nb * F::kTB;
   const int nbw = wave < nb ? (nb - 1 - wave) / W + 1 : 0;
 
-  u4_t s0[T], s1[T], s2[T];
-  uint32_t scw[T], dw[T];
+  typename F::U ring[T];
   auto issue = [&](int t, int bi) {
     const int tile = tile0 + t < ntiles ? tile0 + t : ntiles - 1;
-    const uint8_t* src = a.w + (size_t)tile * tile_bytes + (size_t)(wave + W * bi) * kQ6TileBlockBytes;
-    s0[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
-    s1[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024) + lane);
-    s2[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 2048) + lane);
-    scw[t] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kQ6ScaleOffset) + lane);
-    dw[t] = *(reinterpret_cast<const uint16_t*>(src + kQ6DOffset) + col);
+    F::load(ring[t], a.w + (size_t)tile * tile_bytes + (size_t)(wave + W * bi) * F::kTB, lane);
   };
-  auto load_x = [&](Q6X& xf, int bi) {
-    const size_t b = (size_t)(wave + W * bi);
-    const u4_t* fr = a.pack.frag + b * 8 * 64 + lane;
-#pragma unroll
-    for (int fs = 0; fs < 8; ++fs)
-      xf.f[fs] = __builtin_bit_cast(h8_t, fr[fs * 64]);
-    const float* ds = a.pack.dsc + b * 8 + 4 * (g & 1);
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      xf.dv[v] = ds[v];
-  };
-
   f4_t acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t)
     acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
   if (nbw > 0) {
-    Q6X xc, xn;
-    load_x(xc, 0);
+    XF xc, xn;
+    load_xf<F::kMin>(xc, a.pack, (size_t)wave, lane);
 #pragma unroll
     for (int t = 0; t < D; ++t)
       issue(t, 0);
     for (int bi = 0; bi < nbw; ++bi) {
       const bool more = bi + 1 < nbw;
       if (more)
-        load_x(xn, bi + 1);
+        load_xf<F::kMin>(xn, a.pack, (size_t)(wave + W * (bi + 1)), lane);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         // Take slot t before the window's next issue, which may reuse it.
-        const uint32_t wd[12] = {s0[t][0], s0[t][1], s0[t][2], s0[t][3], s1[t][0], s1[t][1],
-                                 s1[t][2], s1[t][3], s2[t][0], s2[t][1], s2[t][2], s2[t][3]};
-        const uint32_t sw = scw[t], dbits = dw[t];
+        const typename F::U cur = ring[t];
         const int tn = t + D;
         if (tn < T)
           issue(tn, bi);
         else if (more)
           issue(tn - T, bi + 1);
-        const float d = half_bits_to_float(dbits & 0xffffu);
-        f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int tr = 0; tr < 4; ++tr) {
-          // fp16 1152 + sc -> sc / 16 (exact), and -96 sc.
-          const uint32_t sel = 0x04000400u | (uint32_t)tr | ((uint32_t)tr << 16);
-          const h2_t p = as_h2(__builtin_amdgcn_perm(0x64646464u, sw, sel));
-          const h2_t mul = __builtin_elementwise_fma(p, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-72.0f, (_Float16)-72.0f});
-          const h2_t add = mul * h2_t{(_Float16)-1536.0f, (_Float16)-1536.0f};
-          h8_t b0, b1;
-          q6_triple(wd[3 * tr], wd[3 * tr + 1], wd[3 * tr + 2], mul, add, b0, b1);
-          c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xc.f[2 * tr], b0, c0, 0, 0, 0);
-          c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xc.f[2 * tr + 1], b1, c1, 0, 0, 0);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          acc[t][v] = fmaf(c0[v] + c1[v], d * xc.dv[v], acc[t][v]);
+        F::mac(cur, xc, lane, acc[t]);
       }
       if (more)
         xc = xn;
@@ -2250,73 +2445,35 @@ __global__ __launch_bounds__(512) void q6k_gemv_kernel(GemvArgs a) {
         part[wave][t][4 * g + v][col] = tot;
     }
   __syncthreads();
-  OutT* y = reinterpret_cast<OutT*>(a.y);
-  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
-  for (int o = tid; o < a.m * 16 * T; o += 64 * W) {
-    const int row = o / (16 * T), c = o % (16 * T), t = c >> 4, cc = c & 15;
-    if (tile0 + t >= ntiles)
-      continue;
-    float acc_v = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w)
-      acc_v += part[w][t][row][cc];
-    if (sizeof(OutT) == 2)
-      acc_v = round_half(acc_v);
-    const size_t off = (size_t)row * a.n + (size_t)(tile0 + t) * 16 + cc;
-    const float out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
-    store_elem(y, off, out);
-  }
+  typed_epilogue<OutT>(a, &part[0][0][0][0], T, tile0, ntiles);
 }
 
-// Persistent form for K = 4096 (16 blocks: two per wave): one workgroup per
-// CU loads its waves' x fragments once and then streams every item it owns
-// (items b, b + grid, ...) through one register window that runs across item
-// boundaries, so the next item's first tile-blocks are in flight during the
-// current item's epilogue.  Partial sums alternate between two LDS buffers:
-// one barrier per item.
-template <int T, typename OutT>
-__global__ __launch_bounds__(512) void q6k_gemv_persistent_kernel(GemvArgs a, int items) {
+template <class F, int T, typename OutT>
+__global__ __launch_bounds__(512) void typed_gemv_persistent_kernel(GemvArgs a, int items) {
   constexpr int W = 8, BPW = 2, DQ = 2, U = BPW * T;
   __shared__ float part[2][W][T][8][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
   const int ntiles = a.n >> 4;
-  const size_t tile_bytes = (size_t)(W * BPW) * kQ6TileBlockBytes;
+  const size_t tile_bytes = (size_t)(W * BPW) * F::kTB;
   int item = blockIdx.x;
   if (item >= items)
     return;
 
-  Q6X xf[BPW];
+  XF xf[BPW];
 #pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-    const size_t b = (size_t)(wave + W * j);
-    const u4_t* fr = a.pack.frag + b * 8 * 64 + lane;
-#pragma unroll
-    for (int fs = 0; fs < 8; ++fs)
-      xf[j].f[fs] = __builtin_bit_cast(h8_t, fr[fs * 64]);
-    const float* ds = a.pack.dsc + b * 8 + 4 * (g & 1);
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      xf[j].dv[v] = ds[v];
-  }
-  u4_t s0[U], s1[U], s2[U];
-  uint32_t scw[U], dw[U];
+  for (int j = 0; j < BPW; ++j)
+    load_xf<F::kMin>(xf[j], a.pack, (size_t)(wave + W * j), lane);
+  typename F::U ring[U];
   auto issue = [&](int u, int it) {
     const int j = u / T, t = u - j * T;
     const int tile = it * T + t < ntiles ? it * T + t : ntiles - 1;
-    const uint8_t* src = a.w + (size_t)tile * tile_bytes + (size_t)(wave + W * j) * kQ6TileBlockBytes;
-    s0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
-    s1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 1024) + lane);
-    s2[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + 2048) + lane);
-    scw[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kQ6ScaleOffset) + lane);
-    dw[u] = *(reinterpret_cast<const uint16_t*>(src + kQ6DOffset) + col);
+    F::load(ring[u], a.w + (size_t)tile * tile_bytes + (size_t)(wave + W * j) * F::kTB, lane);
   };
 #pragma unroll
   for (int u = 0; u < DQ; ++u)
     issue(u, item);
-  OutT* y = reinterpret_cast<OutT*>(a.y);
-  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   for (int it = 0; item < items; ++it, item += gridDim.x) {
     const int next = item + (int)gridDim.x;
     f4_t acc[T];
@@ -2326,29 +2483,12 @@ __global__ __launch_bounds__(512) void q6k_gemv_persistent_kernel(GemvArgs a, in
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = u / T, t = u - j * T;
-      const uint32_t wd[12] = {s0[u][0], s0[u][1], s0[u][2], s0[u][3], s1[u][0], s1[u][1],
-                               s1[u][2], s1[u][3], s2[u][0], s2[u][1], s2[u][2], s2[u][3]};
-      const uint32_t sw = scw[u], dbits = dw[u];
+      const typename F::U cur = ring[u];
       if (u + DQ < U)
         issue(u + DQ, item);
       else if (next < items)
         issue(u + DQ - U, next);
-      const float d = half_bits_to_float(dbits & 0xffffu);
-      f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int tr = 0; tr < 4; ++tr) {
-        const uint32_t sel = 0x04000400u | (uint32_t)tr | ((uint32_t)tr << 16);
-        const h2_t p = as_h2(__builtin_amdgcn_perm(0x64646464u, sw, sel));
-        const h2_t mul = __builtin_elementwise_fma(p, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-72.0f, (_Float16)-72.0f});
-        const h2_t add = mul * h2_t{(_Float16)-1536.0f, (_Float16)-1536.0f};
-        h8_t b0, b1;
-        q6_triple(wd[3 * tr], wd[3 * tr + 1], wd[3 * tr + 2], mul, add, b0, b1);
-        c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j].f[2 * tr], b0, c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j].f[2 * tr + 1], b1, c1, 0, 0, 0);
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        acc[t][v] = fmaf(c0[v] + c1[v], d * xf[j].dv[v], acc[t][v]);
+      F::mac(cur, xf[j], lane, acc[t]);
     }
     float(*pb)[T][8][16] = part[it & 1];
 #pragma unroll
@@ -2360,45 +2500,17 @@ __global__ __launch_bounds__(512) void q6k_gemv_persistent_kernel(GemvArgs a, in
           pb[wave][t][4 * g + v][col] = tot;
       }
     __syncthreads();
-    for (int o = tid; o < a.m * 16 * T; o += 64 * W) {
-      const int row = o / (16 * T), c = o % (16 * T), t = c >> 4, cc = c & 15;
-      if (item * T + t >= ntiles)
-        continue;
-      float acc_v = 0.0f;
-#pragma unroll
-      for (int w = 0; w < W; ++w)
-        acc_v += pb[w][t][row][cc];
-      if (sizeof(OutT) == 2)
-        acc_v = round_half(acc_v);
-      const size_t off = (size_t)row * a.n + (size_t)(item * T + t) * 16 + cc;
-      const float out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
-      store_elem(y, off, out);
-    }
+    typed_epilogue<OutT>(a, &pb[0][0][0][0], T, item * T, ntiles);
   }
 }
 
-// One workgroup of 64 lanes per Q6_K tile-block: lane 16g + i writes its
-// twelve quant dwords and its scale dword; lanes 0..15 write d.
-__global__ __launch_bounds__(64) void q6k_relayout_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t nb) {
+// One workgroup of 64 lanes per tile-block (encode_lane, q4k_internal.h).
+__global__ __launch_bounds__(64) void typed_relayout_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t nb, uint32_t type) {
   const size_t tb = blockIdx.x;
   const uint32_t c = (uint32_t)(tb / nb), b = (uint32_t)(tb % nb);
-  const int lane = threadIdx.x, i = lane & 15, g = lane >> 4;
-  const uint8_t* blk = src + ((size_t)(16 * c + i) * nb + b) * kQ6BlockBytes;
-  uint8_t* out = dst + tb * kQ6TileBlockBytes;
-  uint32_t wd[12] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-  for (int o = 0; o < 32; ++o)
-    for (int hf = 0; hf < 2; ++hf)
-      q6_place(wd, o, hf, q6_quant(blk, q6_elem(g, o, hf)));
-#pragma unroll
-  for (int s = 0; s < 3; ++s)
-    *reinterpret_cast<u4_t*>(out + s * 1024 + 16 * lane) = u4_t{wd[4 * s], wd[4 * s + 1], wd[4 * s + 2], wd[4 * s + 3]};
-  uint32_t sc = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    sc |= (uint32_t)(blk[192 + 4 * g + j] ^ 0x80u) << (8 * j);
-  *reinterpret_cast<uint32_t*>(out + kQ6ScaleOffset + 4 * lane) = sc;
-  if (g == 0)
-    *reinterpret_cast<uint16_t*>(out + kQ6DOffset + 2 * i) = (uint16_t)(blk[208] | (blk[209] << 8));
+  const int lane = threadIdx.x;
+  const size_t bb = (size_t)type_block_bytes(type);
+  encode_lane(type, src + ((size_t)(16 * c + (lane & 15)) * nb + b) * bb, dst + tb * 16 * bb, lane);
 }
 
 int env_int(const char* name, int fallback) {
@@ -2741,59 +2853,69 @@ hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint
   return hipGetLastError();
 }
 
-template <int T, int DQ>
-hipError_t q6k_gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
+template <class F, int T, int DQ>
+hipError_t typed_gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
   const int ntiles = a.n / 16;
   const dim3 grid((unsigned)((ntiles + T - 1) / T)), block(512);
   if (dtype == kF32)
-    (void)dispatch(q6k_gemv_kernel<T, DQ, float>, grid, block, s, a);
+    (void)dispatch(typed_gemv_kernel<F, T, DQ, float>, grid, block, s, a);
   else
-    (void)dispatch(q6k_gemv_kernel<T, DQ, _Float16>, grid, block, s, a);
+    (void)dispatch(typed_gemv_kernel<F, T, DQ, _Float16>, grid, block, s, a);
   return hipGetLastError();
 }
 
-template <int T>
-hipError_t q6k_persistent_launch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+template <class F, int T>
+hipError_t typed_persistent_launch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
   const int items = (a.n / 16 + T - 1) / T;
   const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
   if (dtype == kF32)
-    (void)dispatch(q6k_gemv_persistent_kernel<T, float>, grid, block, s, a, items);
+    (void)dispatch(typed_gemv_persistent_kernel<F, T, float>, grid, block, s, a, items);
   else
-    (void)dispatch(q6k_gemv_persistent_kernel<T, _Float16>, grid, block, s, a, items);
+    (void)dispatch(typed_gemv_persistent_kernel<F, T, _Float16>, grid, block, s, a, items);
   return hipGetLastError();
 }
 
-// K = 4096 with at least 4 items per CU: the persistent form.  Otherwise
-// column tiles per workgroup: the most (of 4, 2, 1) that still gives every
-// CU at least two workgroups.
-hipError_t launch_q6k_gemv(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+// K = 4096 with at least 16 column tiles per CU: the persistent form (F::kPT
+// tiles per item).  Otherwise column tiles per workgroup: the most (of 4, 2,
+// 1) that still gives every CU at least two workgroups.
+template <class F>
+hipError_t typed_gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
   const int ntiles = a.n / 16;
-  static const int persistent = env_int("Q6K_GEMV_PERSISTENT", -1);  // -1 auto, 0 off, else T
-  if (a.nb == 16 && persistent != 0 && (persistent > 0 || ntiles >= 16 * cus)) {
-    if (persistent == 2)
-      return q6k_persistent_launch<2>(s, a, dtype, cus);
-    return q6k_persistent_launch<4>(s, a, dtype, cus);
-  }
+  static const int persistent = env_int("Q6K_GEMV_PERSISTENT", -1);  // -1 auto, 0 off, 2: two tiles per item
+  if (a.nb == 16 && persistent != 0 && (persistent > 0 || ntiles >= 16 * cus))
+    return persistent == 2 ? typed_persistent_launch<F, 2>(s, a, dtype, cus) : typed_persistent_launch<F, F::kPT>(s, a, dtype, cus);
   static const int forced = env_int("Q6K_GEMV_TILES", 0);
   const int t = forced == 1 || forced == 2 || forced == 4 ? forced : ntiles >= 8 * cus ? 4 : ntiles >= 4 * cus ? 2 : 1;
-  static const int depth = env_int("Q6K_GEMV_DEPTH", 2);
-  if (t == 4 && depth == 3)
-    return q6k_gemv_launch<4, 3>(s, a, dtype);
-  if (t == 4 && depth == 4)
-    return q6k_gemv_launch<4, 4>(s, a, dtype);
   if (t == 4)
-    return q6k_gemv_launch<4, 2>(s, a, dtype);
+    return typed_gemv_launch<F, 4, 2>(s, a, dtype);
   if (t == 2)
-    return q6k_gemv_launch<2, 2>(s, a, dtype);
-  return q6k_gemv_launch<1, 2>(s, a, dtype);
+    return typed_gemv_launch<F, 2, 2>(s, a, dtype);
+  return typed_gemv_launch<F, 1, 2>(s, a, dtype);
 }
 
-hipError_t launch_q6k_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k) {
+hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus) {
+  switch (type) {
+    case kTypeQ6_K:
+      return typed_gemv_dispatch<FmtQ6K>(s, a, dtype, cus);
+    case kTypeQ8_0:
+      return typed_gemv_dispatch<FmtQ8_0>(s, a, dtype, cus);
+    case kTypeQ5_K:
+      return typed_gemv_dispatch<FmtQ5K>(s, a, dtype, cus);
+    case kTypeIQ4_XS:
+      return typed_gemv_dispatch<FmtIQ4XS>(s, a, dtype, cus);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_typed_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type) {
   const uint32_t nb = k / 256;
   const size_t tiles = (size_t)(n / 16) * nb;
   if (tiles == 0)
     return hipSuccess;
-  (void)dispatch(q6k_relayout_kernel, dim3((unsigned)tiles), dim3(64), s, src, dst, nb);
+  if (type_block_bytes(type) == 0 || type == kTypeQ4_K)
+    return hipErrorInvalidValue;
+  (void)dispatch(typed_relayout_kernel, dim3((unsigned)tiles), dim3(64), s, src, dst, nb, type);
   return hipGetLastError();
 }
 

@@ -11,8 +11,9 @@ U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
 _SCALAR = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<?", U64: "<Q", I64: "<q",
            F64: "<d"}
 
-GGML_F32, GGML_F16, GGML_Q4_K, GGML_Q6_K = 0, 1, 12, 14
-BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_IQ4_XS = 0, 1, 8, 12, 13, 14, 23
+BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q5_K: (256, 176),
+         GGML_Q6_K: (256, 210), GGML_IQ4_XS: (256, 136)}
 
 
 def _str(s):

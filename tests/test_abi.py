@@ -94,7 +94,7 @@ def test_relayout_positions(q4k):
 def test_weight_validation_before_hip(q4k):
     w = np.zeros(16 * 144, np.uint8)
     with pytest.raises(q4k.Q4KError) as e:
-        q4k.Weight(w, 16, 256, ggml_type=13)  # Q5_K: not served
+        q4k.Weight(w, 16, 256, ggml_type=10)  # Q2_K: not served
     assert e.value.code == -2
     with pytest.raises(q4k.Q4KError) as e:
         q4k.Weight(w, 16, 256, ggml_type=14)  # Q6_K needs 210 bytes per block

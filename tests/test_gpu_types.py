@@ -1,0 +1,113 @@
+"""Q8_0, Q5_K and IQ4_XS weights on the linear() surface against the CPU
+oracle on identical seeded inputs (the Q6_K cases are in test_gpu_q6k.py).
+Bar: max row-relative error 1e-3.  Q5_K products q * sc are exact in fp16;
+Q8_0 rounds q * d and IQ4_XS rounds products above 2048 once to fp16 (as the
+reference's prefill tiles round every dequantised weight), so their expected
+errors are ~1e-4 and ~1e-6.
+
+Per type: decode and small-prefill row counts; K from one block (waves 1..7
+idle) to 48 blocks (six per wave) and 9 blocks (ragged per wave); ragged
+column tails of the 4- and 2-tile workgroups; the persistent form at K = 4096
+(16 * 4401 columns, one tile in the last item); post 1 / 2 in place in
+decode and prefill (per-8-row groups); fp16 activations; the device-side
+upload (bit-identical to the host one); the gated projection; a GGUF file.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gguf_writer import write_gguf
+from q4k_ref import TYPE_IQ4_XS, TYPE_Q5_K, TYPE_Q8_0, make_weight, make_x, row_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+TYPES = [TYPE_Q8_0, TYPE_Q5_K, TYPE_IQ4_XS]
+
+
+def _t(a, dev, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
+
+
+def _linear(q4k, oracle, gpu, t, seed, m, n, k, post=0, dtype=torch.float32, counts=None, device_upload=False):
+    rng = np.random.default_rng(seed)
+    w = make_weight(rng, n, k, t)
+    x = make_x(rng, m, k)
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    xq = x.astype(npdt)
+    aux = make_x(rng, m, n, 2.0).astype(npdt) if post else None
+    W = q4k.Weight(torch.from_numpy(w).to(gpu) if device_upload else w, n, k, ggml_type=t)
+    y = torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+    auxt = None
+    if post:
+        y.copy_(_t(aux, gpu, dtype))
+        auxt = y
+    q4k.linear(_t(xq, gpu, dtype), W, m, y, auxiliary=auxt, gated=(post == 2), query_counts=counts)
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    ref = oracle.linear(xq, w, n, k, aux=aux, post=post, ggml_type=t)
+    assert np.all(np.isfinite(got))
+    err = row_rel_err(got, ref)
+    assert err <= TOL, f"type={t} m={m} n={n} k={k} post={post} {dtype}: rel err {err:.3g}"
+    return W, got
+
+
+SHAPES = [(1, 16, 256), (8, 48, 768), (2, 80, 2304), (5, 4096, 4096), (8, 1024, 12288), (2, 16 * 2049, 512),
+          (1, 16 * 1025, 256), (3, 16 * 4401, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+@pytest.mark.parametrize("t", TYPES)
+def test_linear_store(q4k, oracle, gpu, t, m, n, k):
+    _linear(q4k, oracle, gpu, t, 900 + m + k + t, m, n, k, counts=[1] * m)
+
+
+@pytest.mark.parametrize("post", [1, 2])
+@pytest.mark.parametrize("m,counts", [(8, [1] * 8), (20, [20])])
+@pytest.mark.parametrize("t", TYPES)
+def test_epilogues_in_place(q4k, oracle, gpu, t, post, m, counts):
+    _linear(q4k, oracle, gpu, t, 910 + post + m + t, m, 1024, 4096, post=post, counts=counts)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_fp16_and_kernel_names(q4k, oracle, gpu, t):
+    W, _ = _linear(q4k, oracle, gpu, t, 920 + t, 8, 2048, 4096, post=1, dtype=torch.float16, counts=[8])
+    name = {TYPE_Q8_0: "q8_0", TYPE_Q5_K: "q5_k", TYPE_IQ4_XS: "iq4_xs"}[t]
+    assert W.kernel_name(2) == f"linear_{name}_k4096_n2048_prefill_small_mfma16x16x32"
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_device_upload_is_bit_identical(q4k, oracle, gpu, t):
+    _, a = _linear(q4k, oracle, gpu, t, 930 + t, 8, 4096, 4096, counts=[1] * 8)
+    _, b = _linear(q4k, oracle, gpu, t, 930 + t, 8, 4096, 4096, counts=[1] * 8, device_upload=True)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("m,counts", [(8, [1] * 8), (12, [12])])
+@pytest.mark.parametrize("t", TYPES)
+def test_gate_up(q4k, oracle, gpu, t, m, counts):
+    n, k = 1536, 4096
+    rng = np.random.default_rng(940 + m + t)
+    wg, wu = make_weight(rng, n, k, t), make_weight(rng, n, k, t)
+    x = make_x(rng, m, k, 0.5)
+    G, U = q4k.Weight(wg, n, k, ggml_type=t), q4k.Weight(wu, n, k, ggml_type=t)
+    gate = torch.full((m, n), float("nan"), device=gpu)
+    q4k.mlp_gate_up(_t(x, gpu), G, U, m, gate, query_counts=counts)
+    torch.cuda.synchronize()
+    assert row_rel_err(gate.cpu().numpy(), oracle.mlp_gate_up(x, wg, wu, n, k, ggml_type=t)) <= TOL
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_tensor_from_gguf(q4k, oracle, gpu, tmp_path, t):
+    n, k, m = 512, 4096, 8
+    rng = np.random.default_rng(950 + t)
+    w = make_weight(rng, n, k, t)
+    path = tmp_path / "w.gguf"
+    write_gguf(path, [("blk.0.ffn_down.weight", t, (k, n), w.tobytes())])
+    with q4k.GGUFFile(path) as f:
+        W = f.weight("blk.0.ffn_down.weight")
+    assert (W.n, W.k, W.type) == (n, k, t)
+    x = make_x(rng, m, k)
+    y = torch.empty((m, n), device=gpu)
+    q4k.linear(_t(x, gpu), W, m, y, query_counts=[m])
+    torch.cuda.synchronize()
+    assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k, ggml_type=t)) <= TOL

@@ -139,4 +139,4 @@ def test_unknown_type_rejected(oracle):
     x = np.zeros((1, 256), np.float32)
     w = np.zeros(16 * 256, np.uint8)
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
-    assert oracle.lib.q4o_linear_typed_f32(p(y), p(x), p(w), 13, None, 1, 16, 256, 0, 1) == -1
+    assert oracle.lib.q4o_linear_typed_f32(p(y), p(x), p(w), 10, None, 1, 16, 256, 0, 1) == -1

@@ -94,11 +94,11 @@ def test_kernel_decode_matches_oracle(q4k, oracle, seed):
 def test_typed_validation_before_hip(q4k):
     buf = np.zeros(16 * 210, np.uint8)
     with pytest.raises(q4k.Q4KError) as e:
-        q4k.Weight(buf, 16, 256, ggml_type=13)
+        q4k.Weight(buf, 16, 256, ggml_type=10)
     assert e.value.code == -2
     with pytest.raises(q4k.Q4KError) as e:
         q4k.Weight(buf[:-1], 16, 256, ggml_type=TYPE_Q6_K)
     assert e.value.code == -3
     assert q4k.q4k_nbytes(16, 512, TYPE_Q6_K) == 16 * 2 * 210
     with pytest.raises(q4k.Q4KError):
-        q4k.relayout_host(np.zeros(16 * 210, np.uint8), 16, 256, 13)
+        q4k.relayout_host(np.zeros(16 * 210, np.uint8), 16, 256, 10)
