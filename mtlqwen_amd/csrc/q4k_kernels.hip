@@ -2207,21 +2207,25 @@ struct FmtQ6K {
     u.d = *(reinterpret_cast<const uint16_t*>(src + kQ6DOffset) + (lane & 15));
   }
   static __device__ __forceinline__ void mac(const U& u, const XF& x, int, f4_t& acc) {
-    const uint32_t wd[12] = {u.s0[0], u.s0[1], u.s0[2], u.s0[3], u.s1[0], u.s1[1], u.s1[2], u.s1[3], u.s2[0], u.s2[1], u.s2[2], u.s2[3]};
     const float d = half_bits_to_float(u.d & 0xffffu);
     f4_t c0 = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int tr = 0; tr < 4; ++tr) {
+    // Triple tr = dwords 3tr..3tr+2 of the lane's twelve (named directly: a
+    // local array of them is not always kept in registers).
+    auto triple = [&](int tr, uint32_t A, uint32_t B, uint32_t C) {
       // fp16 1152 + sc -> sc / 16 (exact), and -96 sc.
       const uint32_t sel = 0x04000400u | (uint32_t)tr | ((uint32_t)tr << 16);
       const h2_t p = as_h2(__builtin_amdgcn_perm(0x64646464u, u.sc, sel));
       const h2_t mul = __builtin_elementwise_fma(p, h2_splat(0.0625f), h2_splat(-72.0f));
       const h2_t add = mul * h2_splat(-1536.0f);
       h8_t b0, b1;
-      q6_triple(wd[3 * tr], wd[3 * tr + 1], wd[3 * tr + 2], mul, add, b0, b1);
+      q6_triple(A, B, C, mul, add, b0, b1);
       c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[2 * tr], b0, c0, 0, 0, 0);
       c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[2 * tr + 1], b1, c1, 0, 0, 0);
-    }
+    };
+    triple(0, u.s0[0], u.s0[1], u.s0[2]);
+    triple(1, u.s0[3], u.s1[0], u.s1[1]);
+    triple(2, u.s1[2], u.s1[3], u.s2[0]);
+    triple(3, u.s2[1], u.s2[2], u.s2[3]);
 #pragma unroll
     for (int v = 0; v < 4; ++v)
       acc[v] = fmaf(c0[v] + c1[v], d * x.dv[v], acc[v]);
