@@ -307,6 +307,49 @@ def q6k_bench(args, dev):
             "step_gbs": round(nbytes / (step_ms * 1e-3) / 1e9, 1)}
 
 
+def types_bench(args, dev):
+    """The other GGUF types of the linear() surface at the LM-head shape
+    (8 rows, K = 4096 -> N = 248,320; persistent GEMV), per launch with
+    dispatch-attached events: Q8_0 (1.08 GB), Q5_K (699 MB), IQ4_XS (540 MB)."""
+    import torch
+    import mtlqwen_amd as q4k
+
+    n, k, m = 248320, 4096, 8
+    nb = k // 256
+    out = {}
+    for name, t in (("q8_0", q4k.GGML_TYPE_Q8_0), ("q5_k", q4k.GGML_TYPE_Q5_K), ("iq4_xs", q4k.GGML_TYPE_IQ4_XS)):
+        bb = q4k.q4k_nbytes(1, 256, t)
+        g = torch.Generator(device=dev).manual_seed(0x51A70007 + t)
+        raw = torch.randint(0, 256, (n * nb * bb,), dtype=torch.uint8, device=dev, generator=g)
+        # fp16 scale fields of magnitude below 2^-7 (finite outputs).
+        if t == q4k.GGML_TYPE_Q8_0:
+            raw.view(n, nb * 8, 34)[:, :, 1] &= 0x1F
+        else:
+            raw.view(n, nb, bb)[:, :, 1] &= 0x1F
+            if t == q4k.GGML_TYPE_Q5_K:
+                raw.view(n, nb, bb)[:, :, 3] &= 0x1F
+        W = q4k.Weight(raw, n, k, ggml_type=t)
+        del raw
+        x = torch.randn((m, k), device=dev, generator=g)
+        y = torch.empty((m, n), device=dev)
+        for _ in range(10):
+            q4k.linear(x, W, m, y, query_counts=[1] * m)
+        torch.cuda.synchronize()
+        q4k.profile_enable(True)
+        for _ in range(30):
+            q4k.linear(x, W, m, y, query_counts=[1] * m)
+        torch.cuda.synchronize()
+        ng, tg, _, _ = q4k.profile_query(q4k.KERNEL_GEMV)
+        q4k.profile_enable(False)
+        us = tg / ng * 1e3
+        nbytes = n * nb * bb + m * k * 4 + m * n * 4
+        out[name] = {"gemv_avg_us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_of_8tbs": round(nbytes / (us * 1e-6) / 8e12, 3)}
+        W.close()
+        torch.cuda.empty_cache()
+    return out
+
+
 def prefill_bench(args, dev):
     import numpy as np
     import torch
@@ -451,6 +494,7 @@ def main():
     shard = shard_bench(args, dev)
     neighbours = neighbours_bench(args, dev)
     q6k = q6k_bench(args, dev)
+    types = types_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
@@ -499,6 +543,7 @@ def main():
         "shard_1of8": shard,
         "neighbours": neighbours,
         "q6k_lm_head": q6k,
+        "types_lm_head": types,
         "copy_ceiling_gbs": round(copy_gbs, 1),
         "mfma_ceiling_tflops": round(mfma_tf, 1),
         "cpu_baseline": cpu,
