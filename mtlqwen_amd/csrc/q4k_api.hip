@@ -14,6 +14,8 @@
 #include <string>
 #include <vector>
 
+#include <rocblas/rocblas.h>
+
 #include "../../include/q4k.h"
 #include "q4k_internal.h"
 
@@ -81,6 +83,11 @@ struct Workspace {
   size_t pack_bytes = 0;
   void* normed = nullptr;  // q4k_mlp's RMS-normalised x when the norm is not fused
   size_t normed_bytes = 0;
+  _Float16* wdq = nullptr;  // prefill with the other types: dequantised fp16 weights [n, k]
+  size_t wdq_elems = 0;
+  float* cbuf = nullptr;  // ... and the library GEMM's fp32 result [m, n]
+  size_t cbuf_elems = 0;
+  rocblas_handle blas = nullptr;
   std::vector<void*> retired;
 };
 
@@ -303,10 +310,10 @@ Kernel& resolve(q4k_weight* w, uint32_t phase) {
     k.kind = phase == Q4K_PHASE_GATED_DECODE ? kGemvGated : phase == Q4K_PHASE_PREFILL ? kGemm : kGemv;
     const bool other = w->type != Q4K_GGML_TYPE_Q4_K;
     if (other && k.kind == kGemm)
-      k.kind = kGemv;  // prefill of the other types: the GEMV per group of 8 rows
+      k.kind = kGemv;  // prefill of the other types: GEMV per 8-row group below 64 rows, dequantised fp16 GEMM from 64
     k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + type_name(w->type) + "_k" + std::to_string(w->k) + "_n" +
              std::to_string(w->n) + "_" + suffix[phase] +
-             (k.kind == kGemm ? "_mfma32x32x16" : other && phase == Q4K_PHASE_PREFILL ? "_mfma16x16x32_rows8" : "_mfma16x16x32");
+             (k.kind == kGemm ? "_mfma32x32x16" : other && phase == Q4K_PHASE_PREFILL ? "_fp16_gemm" : "_mfma16x16x32");
   }
   return k;
 }
@@ -364,6 +371,22 @@ int ensure_splitk_workspace(Workspace& ws, int device, size_t part_floats, size_
     Q4K_TRY_HIP(hipMemset(ws.counters, 0, n * sizeof(int)), "hipMemset");
     ws.counter_elems = n;
   }
+  return Q4K_OK;
+}
+
+// Grow-only device buffer (retired buffers stay allocated: a captured graph
+// may still name them).
+template <typename T>
+int ensure_buffer(Workspace& ws, int device, T*& buf, size_t& have, size_t need, const char* what) {
+  if (have >= need)
+    return Q4K_OK;
+  if (buf)
+    ws.retired.push_back(buf);
+  buf = nullptr;
+  have = 0;
+  if (hipMalloc(&buf, need * sizeof(T)) != hipSuccess)
+    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte %s on device %d", need * sizeof(T), what, device);
+  have = need;
   return Q4K_OK;
 }
 
@@ -459,11 +482,56 @@ int set_device(int device) {
 // previous call, which must have been a projection of the same x with the
 // same (m, k, n) under the same lock; the decode pack and split-K paths always
 // stage (they are not reached by such pairs).
-// Projection with weights of a type other than Q4_K (wu == nullptr): per group
-// of up to 8 rows, the decode pack of the group's x, then the type's GEMV over
-// the group's rows of y and aux.
+// Projection with weights of a type other than Q4_K (wu == nullptr): up to 63
+// rows, per group of up to 8 rows, the decode pack of the group's x, then the
+// type's GEMV over the group's rows of y and aux; from 64 rows the GEMM above.
+constexpr uint32_t kTypedGemmRows = 64;
+// Prefill-sized batches with the other types (m >= 64): x staged as fp16 rows
+// with power-of-two row scales, the weights dequantised to fp16 [n, k] (the
+// reference's prefill tile values), one rocBLAS GEMM with fp32 accumulation
+// and output, then the epilogue (row unscale, post 0/1/2, fp16 rounding).
+int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
+                          uint32_t dtype) {
+  const size_t n = w->n, k = w->k;
+  int rc = ensure_workspace(ws, w->device, (size_t)m * k, m);
+  if (!rc)
+    rc = ensure_buffer(ws, w->device, ws.wdq, ws.wdq_elems, n * k, "dequantised-weight workspace");
+  if (!rc)
+    rc = ensure_buffer(ws, w->device, ws.cbuf, ws.cbuf_elems, (size_t)m * n, "GEMM result workspace");
+  if (rc)
+    return rc;
+  if (!ws.blas && rocblas_create_handle(&ws.blas) != rocblas_status_success) {
+    ws.blas = nullptr;
+    return fail(Q4K_EHIP, "rocblas_create_handle failed on device %d", w->device);
+  }
+  {
+    LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, nullptr, ws.scale, (int)m, (int)k, kStageRowMajor), "stage_x launch");
+  }
+  {
+    LaunchTimer timer(stream, Q4K_KERNEL_AUX);
+    Q4K_TRY_HIP(launch_typed_dequant(stream, w->data, w->type, (uint32_t)n, (uint32_t)k, ws.wdq), "dequant launch");
+  }
+  // Row-major C [m, n] = X [m, k] . W [n, k]^T is column-major C^T = W^T' . X^T'
+  // with W read transposed.
+  if (rocblas_set_stream(ws.blas, stream) != rocblas_status_success)
+    return fail(Q4K_EHIP, "rocblas_set_stream failed");
+  const float one = 1.0f, zero = 0.0f;
+  const rocblas_status st =
+      rocblas_gemm_ex(ws.blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)n, (rocblas_int)m, (rocblas_int)k, &one, ws.wdq,
+                      rocblas_datatype_f16_r, (rocblas_int)k, ws.x, rocblas_datatype_f16_r, (rocblas_int)k, &zero, ws.cbuf, rocblas_datatype_f32_r,
+                      (rocblas_int)n, ws.cbuf, rocblas_datatype_f32_r, (rocblas_int)n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success)
+    return fail(Q4K_EHIP, "rocblas_gemm_ex failed (%d)", (int)st);
+  LaunchTimer timer(stream, Q4K_KERNEL_AUX);
+  Q4K_TRY_HIP(launch_gemm_post(stream, ws.cbuf, ws.scale, y, aux, (int)m, (int)n, (int)post, (int)dtype), "gemm epilogue launch");
+  return Q4K_OK;
+}
+
 int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
                    uint32_t dtype) {
+  if (m >= kTypedGemmRows)
+    return run_typed_gemm_locked(stream, ws, w, x, y, aux, m, post, dtype);
   const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
   for (uint32_t r0 = 0; r0 < m; r0 += 8) {
     const uint32_t mg = m - r0 < 8u ? m - r0 : 8u;

@@ -215,6 +215,86 @@ __host__ __device__ inline void encode_lane(uint32_t type, const uint8_t* blk, u
   }
 }
 
+__host__ __device__ inline uint32_t get_u32(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+__host__ __device__ inline float half_to_float(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// The 64 weights of lane `lane` of one tile-block of a type other than Q4_K,
+// in fp32 as the reference's prefill tiles compute them before their half()
+// store (quant_linear.metal:54-115): w[8 fs + h] is element
+// q6_elem(g, 4 fs + h / 2, h % 2) of row 16c + lane % 16.
+__host__ __device__ inline void decode_lane(uint32_t type, const uint8_t* tb, int lane, float* w) {
+  const int g = lane >> 4, i = lane & 15;
+  if (type == kTypeQ6_K) {
+    uint32_t wd[12];
+    #pragma unroll
+    for (int j = 0; j < 12; ++j)
+      wd[j] = get_u32(tb + (j >> 2) * 1024 + 16 * lane + 4 * (j & 3));
+    const float d = half_to_float(tb[kQ6DOffset + 2 * i] | (tb[kQ6DOffset + 2 * i + 1] << 8));
+    #pragma unroll
+    for (int o = 0; o < 32; ++o) {
+      const float sc = (float)(int8_t)(tb[kQ6ScaleOffset + 4 * lane + (o >> 3)] ^ 0x80u);
+      #pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        w[2 * o + hf] = d * sc * (float)((int)q6_take(wd, o, hf) - 32);
+    }
+  } else if (type == kTypeQ8_0) {
+    const uint32_t dd = get_u32(tb + 4096 + 4 * lane);
+    #pragma unroll
+    for (int o = 0; o < 32; ++o)
+      #pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int byte = 2 * o + hf;
+        const float d = half_to_float(o < 16 ? dd & 0xffffu : dd >> 16);
+        w[byte] = d * (float)(int8_t)(tb[(byte >> 4) * 1024 + 16 * lane + (byte & 15)] ^ 0x80u);
+      }
+  } else if (type == kTypeQ5_K) {
+    const uint8_t* hd = tb + kHeaderOffset + 16 * i;
+    const float d = half_to_float(hd[0] | (hd[1] << 8)), dm = half_to_float(hd[2] | (hd[3] << 8));
+    const uint32_t hb[2] = {get_u32(tb + 2304 + 8 * lane), get_u32(tb + 2304 + 8 * lane + 4)};
+    #pragma unroll
+    for (int fs = 0; fs < 8; ++fs) {
+      // sub-block 2g + fs / 4: the 6-bit scale / min of the header (quant_linear.metal:12-20)
+      const int j = 2 * g + (fs >> 2);
+      const uint8_t* q = hd + 4;
+      const uint32_t sc = j < 4 ? q[j] & 63u : (q[j + 4] & 15u) | ((q[j - 4] >> 6) << 4);
+      const uint32_t mn = j < 4 ? q[j + 4] & 63u : (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+      #pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const int t = h >> 1, hf = h & 1;
+        const int jj = 8 * (fs & 3) + 2 * t + hf;  // quant byte 32g + jj of the row
+        const int ob = jj & 3, sb = ob == 1 ? 2 : ob == 2 ? 1 : ob;  // middle bytes swapped
+        const uint32_t byte = tb[(jj >> 4) * kSlabBytes + 16 * lane + (jj & 12) + sb];
+        const uint32_t nib = fs < 4 ? byte & 15u : byte >> 4;
+        const uint32_t bit = (hb[fs >> 2] >> (4 * (fs & 3) + t + 16 * hf)) & 1u;
+        w[8 * fs + h] = d * (float)sc * (float)(nib + 16 * bit) - dm * (float)mn;
+      }
+    }
+  } else if (type == kTypeIQ4_XS) {
+    const uint8_t* hd = tb + 2048 + 8 * i;
+    const float d = half_to_float(hd[0] | (hd[1] << 8));
+    const uint32_t sh = hd[2] | (hd[3] << 8), sl = get_u32(hd + 4);
+    // iq4nl (quant_linear.metal:5) + 128, four bytes per word.
+    const uint32_t tab[4] = {0x3F2D1801u, 0x766A5D4Fu, 0xA6998D81u, 0xF1D9C5B5u};
+    #pragma unroll
+    for (int fs = 0; fs < 8; ++fs) {
+      const int j = 2 * g + (fs >> 2);
+      const int ls = (int)(((sl >> (4 * j)) & 15u) | (((sh >> (2 * j)) & 3u) << 4)) - 32;
+      const uint32_t wq = get_u32(tb + (fs >> 2) * 1024 + 16 * lane + 4 * (fs & 3));
+      #pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const uint32_t v = h < 4 ? (wq >> (8 * h)) & 15u : (wq >> (8 * (h - 4) + 4)) & 15u;
+        const float cb = (float)((int)((tab[v >> 2] >> (8 * (v & 3))) & 0xFFu) - 128);
+        w[8 * fs + h] = d * (float)ls * cb;
+      }
+    }
+  }
+}
+
 // Rows of a GEMV call are padded to 16-row MFMA tiles; the GEMV handles up to
 // kGemvMaxRowTiles of them (48 rows: the 8 x 5 decode rows of the reference).
 constexpr int kGemvMaxRowTiles = 3;
@@ -354,6 +434,12 @@ hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint
 // type `type` (Q6_K, Q8_0, Q5_K or IQ4_XS), a.pack = the decode pack of x
 // (launch_stage_pack), post 0/1/2 on a.y / a.aux.
 hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus);
+
+// Prefill with the other types: their weights dequantised to fp16 [n, k]
+// (the reference's prefill tile values, rounded once), and the epilogue of a
+// library GEMM's fp32 result c [m, n]: y = post(c * rowscale[row], aux).
+hipError_t launch_typed_dequant(hipStream_t s, const uint8_t* w, uint32_t type, uint32_t n, uint32_t k, _Float16* out);
+hipError_t launch_gemm_post(hipStream_t s, const float* c, const float* rowscale, void* y, const void* aux, int m, int n, int post, int dtype);
 
 // Device-side GGUF -> tiled re-layout of Q6_K, Q8_0, Q5_K or IQ4_XS weights.
 hipError_t launch_typed_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type);

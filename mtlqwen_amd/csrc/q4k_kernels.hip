@@ -2508,6 +2508,43 @@ __global__ __launch_bounds__(512) void typed_gemv_persistent_kernel(GemvArgs a, 
   }
 }
 
+// One workgroup of 64 lanes per tile-block: lane 16g + i writes its 64
+// weights (decode_lane) as fp16 into row 16c + i of out [n, k], eight
+// consecutive k per 16-byte store.
+template <uint32_t TYPE>
+__global__ __launch_bounds__(64) void typed_dequant_kernel(const uint8_t* __restrict__ w, _Float16* __restrict__ out, uint32_t nb, uint32_t k) {
+  const size_t tb = blockIdx.x;
+  const uint32_t c = (uint32_t)(tb / nb), b = (uint32_t)(tb % nb);
+  const int lane = threadIdx.x, g = lane >> 4, i = lane & 15;
+  float v[64];
+  decode_lane(TYPE, w + tb * 16 * (size_t)type_block_bytes(TYPE), lane, v);
+  _Float16* row = out + (size_t)(16 * c + i) * k + 256 * (size_t)b + 64 * g;
+#pragma unroll
+  for (int fs = 0; fs < 8; ++fs) {
+    h8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      h[e] = (_Float16)v[8 * fs + e];
+    *reinterpret_cast<h8_t*>(row + 32 * (fs >> 2) + 8 * (fs & 3)) = h;
+  }
+}
+
+// y = post(c * rowscale[row], aux) over [m, n], the rounding points of the
+// GEMM epilogue (fp16: the accumulator rounded before the post operation).
+template <typename OutT>
+__global__ __launch_bounds__(256) void gemm_post_kernel(const float* __restrict__ c, const float* __restrict__ rowscale, OutT* y, const OutT* aux,
+                                                        int m, int n, int post) {
+  const size_t total = (size_t)m * n;
+  for (size_t o = (size_t)blockIdx.x * 256 + threadIdx.x; o < total; o += (size_t)gridDim.x * 256) {
+    const int row = (int)(o / (size_t)n);
+    float acc_v = c[o] * rowscale[row];
+    if (sizeof(OutT) == 2)
+      acc_v = round_half(acc_v);
+    const float out = post == 1 ? acc_v + load_elem(aux, o) : post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
+    store_elem(y, o, out);
+  }
+}
+
 // One workgroup of 64 lanes per tile-block (encode_lane, q4k_internal.h).
 __global__ __launch_bounds__(64) void typed_relayout_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t nb, uint32_t type) {
   const size_t tb = blockIdx.x;
@@ -2910,6 +2947,44 @@ hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, in
     default:
       return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_typed_dequant(hipStream_t s, const uint8_t* w, uint32_t type, uint32_t n, uint32_t k, _Float16* out) {
+  const uint32_t nb = k / 256;
+  const size_t tiles = (size_t)(n / 16) * nb;
+  if (tiles == 0)
+    return hipSuccess;
+  const dim3 grid((unsigned)tiles), block(64);
+  switch (type) {
+    case kTypeQ6_K:
+      (void)dispatch(typed_dequant_kernel<kTypeQ6_K>, grid, block, s, w, out, nb, k);
+      break;
+    case kTypeQ8_0:
+      (void)dispatch(typed_dequant_kernel<kTypeQ8_0>, grid, block, s, w, out, nb, k);
+      break;
+    case kTypeQ5_K:
+      (void)dispatch(typed_dequant_kernel<kTypeQ5_K>, grid, block, s, w, out, nb, k);
+      break;
+    case kTypeIQ4_XS:
+      (void)dispatch(typed_dequant_kernel<kTypeIQ4_XS>, grid, block, s, w, out, nb, k);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_post(hipStream_t s, const float* c, const float* rowscale, void* y, const void* aux, int m, int n, int post, int dtype) {
+  const size_t total = (size_t)m * n;
+  const unsigned grid = (unsigned)((total + 255) / 256 < 16384 ? (total + 255) / 256 : 16384);
+  if (total == 0)
+    return hipSuccess;
+  if (dtype == kF32)
+    (void)dispatch(gemm_post_kernel<float>, dim3(grid), dim3(256), s, c, rowscale, static_cast<float*>(y), static_cast<const float*>(aux), m, n, post);
+  else
+    (void)dispatch(gemm_post_kernel<_Float16>, dim3(grid), dim3(256), s, c, rowscale, static_cast<_Float16*>(y), static_cast<const _Float16*>(aux), m,
+                   n, post);
+  return hipGetLastError();
 }
 
 hipError_t launch_typed_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type) {

@@ -10,7 +10,9 @@ idle) to 48 blocks (six per wave) and 9 blocks (ragged per wave); ragged
 column tails of the 4- and 2-tile workgroups; the persistent form at K = 4096
 (16 * 4401 columns, one tile in the last item); post 1 / 2 in place in
 decode and prefill (per-8-row groups); fp16 activations; the device-side
-upload (bit-identical to the host one); the gated projection; a GGUF file.
+upload (bit-identical to the host one); the gated projection; a GGUF file;
+and, for every non-Q4_K type, prefill batches of 64 rows and more (the
+dequantised fp16 GEMM) with post 0 / 1 / 2 and fp16 activations.
 """
 import numpy as np
 import pytest
@@ -111,3 +113,23 @@ def test_tensor_from_gguf(q4k, oracle, gpu, tmp_path, t):
     q4k.linear(_t(x, gpu), W, m, y, query_counts=[m])
     torch.cuda.synchronize()
     assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k, ggml_type=t)) <= TOL
+
+
+# Prefill-sized batches (m >= 64) of the other types: x staged as fp16 rows,
+# the weights dequantised to fp16 (the reference's prefill tile values), one
+# rocBLAS GEMM, the library's epilogue.  Like the Q4_K GEMM, activations and
+# weights are single fp16 (expected row errors ~4e-4).
+ALL_TYPES = TYPES + [14]
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 1024, 4096), (97, 2048, 2304), (200, 4096, 12288)])
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_prefill_gemm(q4k, oracle, gpu, t, m, n, k):
+    W, _ = _linear(q4k, oracle, gpu, t, 960 + m + t, m, n, k, counts=[m])
+    assert W.kernel_name(1).endswith("_prefill_fp16_gemm")
+
+
+@pytest.mark.parametrize("post,dtype", [(1, torch.float32), (2, torch.float32), (0, torch.float16), (1, torch.float16)])
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_prefill_gemm_epilogues(q4k, oracle, gpu, t, post, dtype):
+    _linear(q4k, oracle, gpu, t, 970 + post + t, 128, 1024, 4096, post=post, dtype=dtype, counts=[100, 28])
