@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-types", action="store_true", help="skip the Q8_0 / Q5_K / IQ4_XS LM-head timings")
     return ap.parse_args()
 
 
@@ -494,7 +495,7 @@ def main():
     shard = shard_bench(args, dev)
     neighbours = neighbours_bench(args, dev)
     q6k = q6k_bench(args, dev)
-    types = types_bench(args, dev)
+    types = None if args.no_types else types_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
