@@ -484,7 +484,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the Q4_K path has no multi-GPU sharding "
-                                   "(a column/row-parallel design is described in DESIGN.md); run with --gpus 1"}))
+                                   "(gate/up would shard column-parallel over N, down row-parallel over K with one all-reduce); run with --gpus 1"}))
         sys.exit(2)
     import torch
     import mtlqwen_amd  # fails loudly if libq4k.so is missing
