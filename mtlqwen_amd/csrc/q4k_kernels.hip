@@ -1309,7 +1309,7 @@ __device__ __forceinline__ void reset_counter(int* ctr) {
 // Bytes of LDS one split-K slice uses.
 template <int NM, int T, int BPS, int DP>
 constexpr int splitk_lds_bytes() {
-  return 8 * DP * (NM * T / 8) * kTileBlockBytes + BPS * 8 * 64 * 16 + BPS * 64 * 8 + BPS * 8 * 4;
+  return 8 * DP * (NM * T / 8) * kTileBlockBytes + BPS * 8 * 64 * 16 + BPS * 64 * 8 + BPS * 8 * 4 + BPS * 8 * 1024;
 }
 
 // One workgroup's K-slice ks of column group grp (see above), over LDS of
@@ -1324,10 +1324,11 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
   constexpr int kFragBytes = BPS * 8 * 64 * 16;  // [BPS][8 fragments][64 lanes] x 16 B
   constexpr int kXsBytes = BPS * 64 * 8;         // [BPS][64 lanes] x 4 halves
   constexpr int kDscBytes = BPS * 8 * 4;         // [BPS][8 rows]
-  constexpr int kPackChunks = (kFragBytes + kXsBytes + kDscBytes) / 16;
+  constexpr int kStageBytes = BPS * 8 * 1024;    // the slice of x as read: [BPS * 8 (block, row) pairs] x 1 KB
   constexpr int kSlots = DP * PW;                // ring slots per wave
   constexpr int kRingBytes = W * kSlots * kTileBlockBytes;
-  static_assert(kRingBytes + kFragBytes + kXsBytes + kDscBytes == splitk_lds_bytes<NM, T, BPS, DP>(), "LDS layout");
+  static_assert(kRingBytes + kFragBytes + kXsBytes + kDscBytes + kStageBytes == splitk_lds_bytes<NM, T, BPS, DP>(), "LDS layout");
+  uint8_t* const stage = lds + kRingBytes + kFragBytes + kXsBytes + kDscBytes;
   u4_t* const xf = reinterpret_cast<u4_t*>(lds + kRingBytes);
   _Float16* const xs = reinterpret_cast<_Float16*>(lds + kRingBytes + kFragBytes);
   const float* const dscl = reinterpret_cast<const float*>(lds + kRingBytes + kFragBytes + kXsBytes);
@@ -1361,44 +1362,53 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
 
   // 1. The workgroup packs its slice of x into LDS (the decode pack layout,
   // see stage_pack_kernel): wave w converts (block, row) pairs w, w + 8, ...
-  // of the slice.  Its loads of x are queued before any weight load.
+  // of the slice.  The slice arrives by LDS DMA like the weights, issued
+  // before them; a wait that leaves the weight loads in flight
+  // (vmcnt(3 * PW * DP)) then covers x alone.  (Compiler-visible loads of x
+  // would be waited for with vmcnt(0): the compiler does not count the
+  // weight DMAs, so that wait would also cover the first weight steps.)
   constexpr int PPW = BPS * 8 / W;  // (block, row) pairs per wave
   static_assert(BPS * 8 % W == 0, "whole pairs per wave");
+  static_assert(3 * PW * DP <= 63, "vmcnt range");
   const OutT* const xin = reinterpret_cast<const OutT*>(a.x);
-  float xv[PPW][4];
-  // Ordinary loads: the compiler waits for them (vmcnt(0), which also
-  // covers the weight prologue issued meanwhile) before their first use.
-  // Loads issued as asm would save that wait but leave their destinations
-  // open to register copies made before the data arrives.
+  const bool live = (wave & 7) < a.m;  // row (wave + 8j) & 7 of every pair of this wave
+  if (live) {
 #pragma unroll
-  for (int j = 0; j < PPW; ++j) {
-    const int pr = wave + W * j, r = pr & 7;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      xv[j][e] = 0.0f;
-    if (r < a.m) {
-      const OutT* src = xin + (size_t)r * a.k + (size_t)(kb0 + (pr >> 3)) * 256 + 4 * lane;
+    for (int j = 0; j < PPW; ++j) {
+      const int pr = wave + W * j, r = pr & 7;
+      const OutT* src = xin + (size_t)r * a.k + (size_t)(kb0 + (pr >> 3)) * 256;
+      const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr(stage + (size_t)pr * 1024));
       if (sizeof(OutT) == 4) {
-        const f4_t t4 = *reinterpret_cast<const f4_t*>(src);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          xv[j][e] = t4[e];
+        lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
       } else {
-        const h4_t t4 = *reinterpret_cast<const h4_t*>(src);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          xv[j][e] = (float)t4[e];
+        lds_dma4<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff4, l);
+        lds_dma4<256>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff4, l);
       }
     }
   }
-  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_s_barrier();  // the workgroup's x requests ahead of its weight requests
 #pragma unroll
   for (int i = 0; i < DP; ++i)
     issue(i);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PW * DP) : "memory");
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < PPW; ++j) {
     const int pr = wave + W * j, i = pr >> 3, r = pr & 7;
-    const float (&v)[4] = xv[j];
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+      if (sizeof(OutT) == 4) {
+        const f4_t t4 = *reinterpret_cast<const f4_t*>(stage + (size_t)pr * 1024 + 16 * lane);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = t4[e];
+      } else {
+        const h4_t t4 = *reinterpret_cast<const h4_t*>(stage + (size_t)pr * 1024 + 8 * lane);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (float)t4[e];
+      }
+    }
     pack_block_row(v, r, lane, xf + (size_t)i * 8 * 64, reinterpret_cast<h4_t*>(xs) + (size_t)i * 64, const_cast<float*>(dscl) + (size_t)i * 8);
   }
   __syncthreads();
