@@ -2199,12 +2199,14 @@ __device__ __forceinline__ void q6_triple(uint32_t A, uint32_t B, uint32_t C, h2
   b1 = __builtin_bit_cast(h8_t, u4_t{f(o4), f(o5), f(o6), f(o7)});
 }
 
-// Each policy also names the column tiles per item of its persistent form
-// (kPT: the most that stays within the register file without spilling).
+// Each policy also names the shape of its persistent form: kPW waves (16:
+// one block of x each, within 128 VGPRs, four waves per SIMD; 8: two blocks
+// each, two waves per SIMD) and kPT column tiles per item, the measured best
+// that does not spill.
 struct FmtQ6K {
   static constexpr int kTB = kQ6TileBlockBytes;
   static constexpr bool kMin = false;
-  static constexpr int kPT = 4;
+  static constexpr int kPW = 16, kPT = 2;
   struct U {
     u4_t s0, s1, s2;
     uint32_t sc, d;
@@ -2245,7 +2247,7 @@ struct FmtQ6K {
 struct FmtQ8_0 {
   static constexpr int kTB = kTileN * kQ8BlockBytes;
   static constexpr bool kMin = false;
-  static constexpr int kPT = 4;
+  static constexpr int kPW = 16, kPT = 2;
   struct U {
     u4_t s[4];
     uint32_t d;
@@ -2282,7 +2284,7 @@ struct FmtQ8_0 {
 struct FmtQ5K {
   static constexpr int kTB = kTileN * kQ5BlockBytes;
   static constexpr bool kMin = true;
-  static constexpr int kPT = 2;
+  static constexpr int kPW = 8, kPT = 2;
   struct U {
     u4_t q0, q1, hd;
     uint32_t h0, h1;
@@ -2330,7 +2332,7 @@ struct FmtQ5K {
 struct FmtIQ4XS {
   static constexpr int kTB = kTileN * kIQ4BlockBytes;
   static constexpr bool kMin = false;
-  static constexpr int kPT = 4;
+  static constexpr int kPW = 16, kPT = 2;
   struct U {
     u4_t q0, q1;
     uint2 hd;
@@ -2381,18 +2383,18 @@ struct FmtIQ4XS {
   }
 };
 
-template <typename OutT>
+template <typename OutT, int W = 8>
 __device__ __forceinline__ void typed_epilogue(const GemvArgs& a, const float* part, int t_count, int tile0, int ntiles) {
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   const int tid = threadIdx.x;
-  for (int o = tid; o < a.m * 16 * t_count; o += 512) {
+  for (int o = tid; o < a.m * 16 * t_count; o += 64 * W) {
     const int row = o / (16 * t_count), c = o % (16 * t_count), t = c >> 4, cc = c & 15;
     if (tile0 + t >= ntiles)
       continue;
     float acc_v = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 8; ++w)
+    for (int w = 0; w < W; ++w)
       acc_v += part[((w * t_count + t) * 8 + row) * 16 + cc];
     if (sizeof(OutT) == 2)
       acc_v = round_half(acc_v);
@@ -2462,9 +2464,10 @@ __global__ __launch_bounds__(512) void typed_gemv_kernel(GemvArgs a) {
   typed_epilogue<OutT>(a, &part[0][0][0][0], T, tile0, ntiles);
 }
 
-template <class F, int T, typename OutT>
-__global__ __launch_bounds__(512) void typed_gemv_persistent_kernel(GemvArgs a, int items) {
-  constexpr int W = 8, BPW = 2, DQ = 2, U = BPW * T;
+template <class F, int T, int DQ, int W, typename OutT>
+__global__ __launch_bounds__(64 * W) void typed_gemv_persistent_kernel(GemvArgs a, int items) {
+  constexpr int BPW = 16 / W, U = BPW * T;
+  static_assert(W * BPW == 16 && DQ <= U, "16 blocks; window");
   __shared__ float part[2][W][T][8][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2514,7 +2517,7 @@ __global__ __launch_bounds__(512) void typed_gemv_persistent_kernel(GemvArgs a, 
           pb[wave][t][4 * g + v][col] = tot;
       }
     __syncthreads();
-    typed_epilogue<OutT>(a, &pb[0][0][0][0], T, item * T, ntiles);
+    typed_epilogue<OutT, W>(a, &pb[0][0][0][0], T, item * T, ntiles);
   }
 }
 
@@ -2915,26 +2918,27 @@ hipError_t typed_gemv_launch(hipStream_t s, const GemvArgs& a, int dtype) {
   return hipGetLastError();
 }
 
-template <class F, int T>
+template <class F, int T, int DQ, int W = 8>
 hipError_t typed_persistent_launch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
   const int items = (a.n / 16 + T - 1) / T;
-  const dim3 grid((unsigned)(items < cus ? items : cus)), block(512);
+  const dim3 grid((unsigned)(items < cus ? items : cus)), block(64 * W);
   if (dtype == kF32)
-    (void)dispatch(typed_gemv_persistent_kernel<F, T, float>, grid, block, s, a, items);
+    (void)dispatch(typed_gemv_persistent_kernel<F, T, DQ, W, float>, grid, block, s, a, items);
   else
-    (void)dispatch(typed_gemv_persistent_kernel<F, T, _Float16>, grid, block, s, a, items);
+    (void)dispatch(typed_gemv_persistent_kernel<F, T, DQ, W, _Float16>, grid, block, s, a, items);
   return hipGetLastError();
 }
 
-// K = 4096 with at least 16 column tiles per CU: the persistent form (F::kPT
-// tiles per item).  Otherwise column tiles per workgroup: the most (of 4, 2,
-// 1) that still gives every CU at least two workgroups.
+// K = 4096 with at least 16 column tiles per CU: the persistent form
+// (F::kPW waves, F::kPT tiles per item).  Otherwise column tiles per
+// workgroup: the most (of 4, 2, 1) that still gives every CU at least two
+// workgroups.
 template <class F>
 hipError_t typed_gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
   const int ntiles = a.n / 16;
-  static const int persistent = env_int("Q6K_GEMV_PERSISTENT", -1);  // -1 auto, 0 off, 2: two tiles per item
+  static const int persistent = env_int("Q6K_GEMV_PERSISTENT", -1);  // -1 auto, 0 off, 1 on
   if (a.nb == 16 && persistent != 0 && (persistent > 0 || ntiles >= 16 * cus))
-    return persistent == 2 ? typed_persistent_launch<F, 2>(s, a, dtype, cus) : typed_persistent_launch<F, F::kPT>(s, a, dtype, cus);
+    return typed_persistent_launch<F, F::kPT, 2, F::kPW>(s, a, dtype, cus);
   static const int forced = env_int("Q6K_GEMV_TILES", 0);
   const int t = forced == 1 || forced == 2 || forced == 4 ? forced : ntiles >= 8 * cus ? 4 : ntiles >= 4 * cus ? 2 : 1;
   if (t == 4)

@@ -53,7 +53,7 @@ def _linear(q4k, oracle, gpu, seed, m, n, k, post=0, dtype=torch.float32, counts
 # (m, n, k): K = 256 (waves 1..7 idle), 2304 (waves with 2 and 1 blocks),
 # 4096, 12288 (6 blocks per wave); N = 16 * 2049 (4 tiles per workgroup, one
 # in the last) and 16 * 1025 (2 per workgroup, one in the last); N = 16 * 4401
-# at K = 4096 takes the persistent form (1101 items of 4 tiles, one in the last).
+# at K = 4096 takes the persistent form (2201 items of 2 tiles, one in the last).
 SHAPES = [(1, 16, 256), (8, 16, 256), (3, 48, 768), (2, 80, 2304), (5, 4096, 4096), (8, 1024, 12288),
           (2, 16 * 2049, 512), (1, 16 * 1025, 256), (4, 592, 1024), (3, 16 * 4401, 4096)]
 
