@@ -416,7 +416,7 @@ int ensure_pack_workspace(Workspace& ws, int device, size_t bytes) {
   return Q4K_OK;
 }
 
-// Packs x (m <= 8 rows) for the streaming and split-K GEMVs.
+// Packs x (m <= 8 rows) for the per-item and persistent GEMVs.
 int stage_pack(hipStream_t stream, Workspace& ws, int device, const void* x, uint32_t dtype, uint32_t m, uint32_t k, DecodePack* pk) {
   const size_t nb = k / 256;
   int rc = ensure_pack_workspace(ws, device, nb * kPackBytesPerBlock);
@@ -612,13 +612,14 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     Q4K_TRY_HIP(launch_gemv_gate_up(stream, a, (int)dtype, device_cus(w->device)), "gemv gate/up launch");
     return Q4K_OK;
   }
-  if (gemv && split && gemv_stream_supported(rows, (int)(w->k / 256), (int)w->n, wu != nullptr, device_cus(w->device))) {
+  if (gemv && !wu && q4k_persistent_supported((int)m, (int)(w->k / 256), (int)w->n, device_cus(w->device))) {
+    // Wide plain projections (the LM head): the persistent GEMV, x fragments
+    // resident in registers.
     GemvArgs a{};
     int rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);
     if (rc)
       return rc;
     a.w = w->data;
-    a.wu = wu ? wu->data : w->data;
     a.x = x;
     a.y = y;
     a.aux = aux;
@@ -627,10 +628,10 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.k = (int)w->k;
     a.nb = (int)(w->k / 256);
     a.post = (int)post;
-    a.rows = rows;
+    a.rows = 2 * (int)m;
     a.split = 1;
-    LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    Q4K_TRY_HIP(launch_gemv_stream(stream, a, (int)dtype, wu != nullptr, device_cus(w->device)), "gemv stream launch");
+    LaunchTimer timer(stream, Q4K_KERNEL_GEMV);
+    Q4K_TRY_HIP(launch_q4k_persistent(stream, a, (int)dtype, device_cus(w->device)), "gemv persistent launch");
     return Q4K_OK;
   }
   const bool gemm2 = !gemv && gemm2_supported((int)m, (int)w->n);

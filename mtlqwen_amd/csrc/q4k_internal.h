@@ -301,8 +301,8 @@ constexpr int kGemvMaxRowTiles = 3;
 
 enum Dtype : int { kF32 = 0, kF16 = 1 };
 
-// Decode pack: the MFMA operands of x (m <= 8 rows) for the streaming and
-// split-K GEMVs (layout in q4k_kernels.hip, stage_pack_kernel).
+// Decode pack: the MFMA operands of x (m <= 8 rows) for the per-item and
+// persistent GEMVs (layout in q4k_kernels.hip, stage_pack_kernel).
 struct DecodePack {
   u4_t* frag = nullptr;  // [nb][8][64] x 16 B
   h4_t* xs = nullptr;    // [nb][64] x 8 B
@@ -317,7 +317,7 @@ struct GemvArgs {
   const _Float16* xs;     // staged sub-block sums / 32, min-term fragment order
   const float* rowscale;  // per-row power-of-two unscale factor
   const void* x;          // caller's activations [m, k]
-  DecodePack pack;        // packed operands of x (streaming and split-K GEMVs)
+  DecodePack pack;        // packed operands of x (per-item and persistent GEMVs)
   void* y;
   const void* aux;
   int m, n, k, nb, post;
@@ -382,11 +382,6 @@ struct GemvShape {
 // column tiles and waves per workgroup, for tuning.
 GemvShape gemv_shape(int rows, int n, int nb, bool gated);
 
-// Streaming GEMV (LDS ring, persistent workgroups) for one row tile and the
-// block counts it is instantiated for; `cus` = compute units of the device.
-bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus);
-hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus);
-
 // Fused gate/up GEMV for m <= 8 rows and K = 4096 that packs x itself (no
 // staging launch); reads a.x, a.w, a.wu (and a.norm_w when set) and writes a.y.
 bool gemv_gate_up_supported(int m, int nb, int n);
@@ -429,6 +424,12 @@ hipError_t launch_rms_norm(hipStream_t s, const void* x, const float* w, void* y
 
 // Device-side GGUF -> tiled re-layout (src and dst are device buffers).
 hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k);
+
+// Q4_K on the persistent GEMV of the other types (16 waves, x fragments in
+// registers): K = 4096, at least 16 column tiles per CU (the LM head), m <= 8,
+// a.pack = the decode pack of x.
+bool q4k_persistent_supported(int m, int nb, int n, int cus);
+hipError_t launch_q4k_persistent(hipStream_t s, const GemvArgs& a, int dtype, int cus);
 
 // GEMV of the other GGUF types for m <= 8 rows: a.w = tiled weights of ggml
 // type `type` (Q6_K, Q8_0, Q5_K or IQ4_XS), a.pack = the decode pack of x

@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
 
 // ----------------------------------------------------------------------------
 // Decode pack (m <= 8): x converted once into the MFMA operands of the
-// streaming and split-K GEMVs, per 256-element block b:
+// persistent and per-item GEMVs, per 256-element block b:
 //   frag[b][s][l]  16 B: A fragment s (v_mfma_f32_16x16x32_f16) of lane l =
 //                  16g + i: elements 64g + 32 (s / 4) + 8 (s % 4) + [0, 8)
 //                  of row i (i < 8: high fp16 parts, i >= 8: low parts of
@@ -666,21 +666,7 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// Streaming GEMV (m <= 8 rows split hi/lo into one 16-row activation tile,
-// nb == W * BPW).
-//
-// Persistent workgroups (at most one per CU) loop over items of T column
-// tiles.  Wave w owns blocks [w*BPW, (w+1)*BPW) of every item, so it stages
-// its activation fragments once, from the caller's x, and keeps them in
-// registers (no separate staging launch).  Each wave scales its own K range
-// of a row by a power of two and unscales its partial sums, so no pass over
-// the whole row is needed.  Its weight
-// tile-blocks ("units": block j, matrix mi, tile t) stream through a private
-// LDS ring of D+1 slots with global_load_lds_dwordx4 (16 bytes per lane, lane
-// order = slab order), D units ahead of the one being computed, so about
-// D * 2.3 KB per wave is always in flight without holding VGPRs.  Every
-// iteration issues exactly three loads (units past the end re-load the last
-// unit, an L2 hit), so a constant vmcnt(3*D) marks the current unit complete.
+// Load helpers of the GEMVs that stream weights through LDS.
 // ----------------------------------------------------------------------------
 // LDS-DMA loads are issued as asm: the compiler would otherwise guard every
 // later LDS read with vmcnt(0) (it cannot tell the ring slots apart).  Their
@@ -740,222 +726,15 @@ __device__ __forceinline__ void asm_load16_into(u4_t& r, const void* p) {
   asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(r) : "v"(p));
 }
 
-__device__ __forceinline__ void asm_load8_into(h4_t& r, const void* p) {
-  asm volatile("global_load_dwordx2 %0, %1, off" : "+v"(r) : "v"(p));
-}
-
 __device__ __forceinline__ h4_t asm_load8(const void* p) {
   h4_t r;
   asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
   return r;
 }
 
-__device__ __forceinline__ float asm_load4(const void* p) {
-  float r;
-  asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(p));
-  return r;
-}
-
 template <typename V>
 __device__ __forceinline__ void hold(V& v) {
   asm volatile("" : "+v"(v));
-}
-
-template <int T, int NM, int W, int DP, typename OutT>
-__global__ __launch_bounds__(64 * W) void q4k_gemv_stream_kernel(GemvArgs a, int items) {
-  constexpr int BPW = 2;       // blocks per wave
-  constexpr int MT = NM * T;   // (matrix, tile) pairs of an item
-  static_assert(MT % 2 == 0, "unit pairs share one block");
-  constexpr int PB = MT / 2;   // unit pairs per block per item
-  constexpr int PI = BPW * PB; // unit pairs per item
-  constexpr int R = 2 * DP;    // ring slots per wave: DP pairs in flight
-  // LDS: the per-wave rings, then the per-wave partial sums of an item,
-  // [wave][mi*T+t][row][col], summed in wave order by the epilogue.
-  constexpr int kRingBytes = W * R * kTileBlockBytes;
-  constexpr int kRedBytes = W * MT * 16 * 16 * 4;
-  static_assert(kRingBytes + kRedBytes <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kRingBytes + kRedBytes];
-  float* red = reinterpret_cast<float*>(lds + kRingBytes);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, col = lane & 15;
-  const int first = blockIdx.x, stride = gridDim.x;
-  // The wave -> K-range assignment rotates with the workgroup, so that the
-  // workgroups of one L2 do not all read the same part of x at once.
-  const int nb = a.nb, bw = ((wave + first) % W) * BPW;
-  const int n_items = first < items ? (items - 1 - first) / stride + 1 : 0;
-  if (n_items == 0)
-    return;
-  uint8_t* const ring = lds + (size_t)wave * R * kTileBlockBytes;
-  const uint32_t ring0 = lds_addr(ring);
-  const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
-  const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
-
-  // Pair p of this wave's stream: item p / PI, block j, (matrix, tile) pairs
-  // 2q and 2q + 1 of that block, into ring slots 2*ps, 2*ps + 1.  Pairs past
-  // the end re-load the last pair (L2 hits), so every pair issues six loads.
-  auto issue = [&](int p, int ps) {
-    __builtin_amdgcn_sched_barrier(0);
-    int it = p / PI;
-    int r = p - it * PI;
-    if (it >= n_items) {
-      it = n_items - 1;
-      r = PI - 1;
-    }
-    const int j = r / PB, q = r - j * PB;
-    const uint32_t l = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)(2 * ps) * kTileBlockBytes);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int mt = 2 * q + h, mi = mt / T, t = mt - mi * T;
-      const size_t ct = (size_t)(first + it * stride) * T + t;
-      const uint8_t* src = uniform_ptr((mi ? a.wu : a.w) + ct * tile_bytes + (size_t)(bw + j) * kTileBlockBytes);
-      // (The immediate offset applies to both addresses: LDS = M0 + offset + lane * size.)
-      const uint32_t lh = l + (uint32_t)h * kTileBlockBytes;
-      lds_dma16<0>(src, voff16, lh);
-      lds_dma16<kSlabBytes>(src, voff16, lh);
-      lds_dma4<kHeaderOffset>(src, voff4, lh);
-    }
-  };
-
-  // Resident activations: the decode pack of the wave's two blocks (A
-  // fragments, min-term operands, per-(row, block) unscale factors of this
-  // lane's four C rows 4g + v, i.e. rows (4g + v) & 7), loaded with
-  // coalesced 16-byte loads.  The vector L1 returns data in request order:
-  // one wait covers pair 0 and the activations, with the next DP - 1 pairs
-  // still outstanding.
-  // The first pair goes out before the activations so that HBM starts
-  // streaming at once; the activations then land right behind it.
-  issue(0, 0);
-  u4_t xw[BPW][8], dw[BPW];
-#pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-#pragma unroll
-    for (int f = 0; f < 8; ++f)
-      xw[j][f] = asm_load16(a.pack.frag + ((size_t)(bw + j) * 8 + f) * 64 + lane);
-    dw[j] = asm_load16(a.pack.dsc + (size_t)(bw + j) * 8 + 4 * (g & 1));
-  }
-  h4_t xsa[BPW];
-#pragma unroll
-  for (int j = 0; j < BPW; ++j)
-    xsa[j] = asm_load8(a.pack.xs + (size_t)(bw + j) * 64 + lane);
-#pragma unroll
-  for (int p = 1; p < DP; ++p)
-    issue(p, p);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * (DP - 1)) : "memory");
-  h8_t xa[BPW][8];
-  float dsc[BPW][4];
-#pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-#pragma unroll
-    for (int f = 0; f < 8; ++f) {
-      hold(xw[j][f]);
-      xa[j][f] = __builtin_bit_cast(h8_t, xw[j][f]);
-    }
-    hold(dw[j]);
-    const f4_t dv = __builtin_bit_cast(f4_t, dw[j]);
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      dsc[j][v] = dv[v];
-    hold(xsa[j]);
-  }
-
-  constexpr int EPI = 16 * T;  // outputs per row of an item
-  OutT* y = reinterpret_cast<OutT*>(a.y);
-  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
-  int ps = 0;  // ring pair-slot of the pair being computed
-  int p = 0;   // stream index of the pair being computed
-  for (int it = 0; it < n_items; ++it) {
-#pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-#pragma unroll
-      for (int q = 0; q < PB; ++q, ++p) {
-        // Six loads per pair: with DP pairs outstanding, vmcnt(6*(DP-1))
-        // marks the oldest complete.  The memory clobber keeps the LDS
-        // reads below the wait.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * (DP - 1)) : "memory");
-        const u4_t* sl = reinterpret_cast<const u4_t*>(ring + (2 * ps) * kTileBlockBytes);
-        u4_t q0[2], q1[2], hd[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const u4_t* su = sl + h * (kTileBlockBytes / 16);
-          q0[h] = su[lane];
-          q1[h] = su[kSlabBytes / 16 + lane];
-          hd[h] = su[kHeaderOffset / 16 + col];
-        }
-        // The pair is in registers once the reads are done: its slots take
-        // the pair DP ahead while this one is computed.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        issue(p + DP, ps);
-        ps = ps == DP - 1 ? 0 : ps + 1;
-        // Two independent chains, one per (matrix, tile).
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const BlockConsts kc = block_consts(hd[h], g);
-          f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const u4_t qq = u < 2 ? q0[h] : q1[h];
-            const uint32_t wa = qq[2 * (u & 1)], wb = qq[2 * (u & 1) + 1];
-            const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
-            const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
-            cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][u], blo, cl, 0, 0, 0);
-            ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j][4 + u], bhi, ch, 0, 0, 0);
-          }
-          const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[j], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-          // This wave's partial sums of (matrix, tile) 2q + h over block j,
-          // unscaled to x's range; block 1 adds to block 0's.
-          float* r = red + ((wave * MT + 2 * q + h) * 16 + 4 * g) * 16 + col;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float part = fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * dsc[j][v];
-            r[16 * v] = j == 0 ? part : r[16 * v] + part;
-          }
-        }
-      }
-    }
-
-    // Item complete: sum the W partial slots and run the epilogue.
-    __syncthreads();
-    const int ct0 = (first + it * stride) * T;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int o = tid + k * 64 * W;
-      if (o < a.m * EPI) {
-        const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
-        float sm[NM];
-#pragma unroll
-        for (int mi = 0; mi < NM; ++mi) {
-          float v = 0.0f;
-#pragma unroll
-          for (int w = 0; w < W; ++w)
-            v += red[((w * MT + mi * T + t) * 16 + row) * 16 + cc];
-#pragma unroll
-          for (int w = 0; w < W; ++w)
-            v += red[((w * MT + mi * T + t) * 16 + 8 + row) * 16 + cc];
-          sm[mi] = v;
-        }
-        const size_t off = (size_t)row * a.n + (size_t)(ct0 + t) * 16 + cc;
-        float out;
-        if (NM == 2) {
-          float gv = sm[0], uv = sm[NM - 1];
-          if (sizeof(OutT) == 2) {
-            gv = round_half(gv);
-            uv = round_half(uv);
-          }
-          out = silu(gv) * uv;
-        } else {
-          float acc_v = sm[0];
-          if (sizeof(OutT) == 2)
-            acc_v = round_half(acc_v);
-          out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
-        }
-        store_elem(y, off, out);
-      }
-    }
-    __syncthreads();
-  }
-  // Drain the trailing (re-load) units before the ring is released.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // ----------------------------------------------------------------------------
@@ -1275,8 +1054,7 @@ __global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// Split-K GEMV (m <= 8 rows, split hi/lo into one 16-row activation tile as
-// in the streaming GEMV).
+// Split-K GEMV (m <= 8 rows, split hi/lo into one 16-row activation tile).
 //
 // Each CU of a persistent launch would otherwise pull all of x from L2 (32 MB
 // across the chip for m = 8, K = 4096, fp32) before its first MFMA.  Here
@@ -2329,6 +2107,39 @@ struct FmtQ5K {
   }
 };
 
+// Q4_K itself in the same form (the tiled layout of q4k_internal.h), for the
+// wide decode projections (the LM head) the persistent form serves best.
+struct FmtQ4K {
+  static constexpr int kTB = kTileBlockBytes;
+  static constexpr bool kMin = true;
+  static constexpr int kPW = 16, kPT = 2;
+  struct U {
+    u4_t q0, q1, hd;
+  };
+  static __device__ __forceinline__ void load(U& u, const uint8_t* src, int lane) {
+    u.q0 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    u.q1 = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
+    u.hd = *(reinterpret_cast<const u4_t*>(src + kHeaderOffset) + (lane & 15));
+  }
+  static __device__ __forceinline__ void mac(const U& u, const XF& x, int lane, f4_t& acc) {
+    const BlockConsts kc = block_consts(u.hd, lane >> 4);
+    f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u4_t qq = s < 2 ? u.q0 : u.q1;
+      const uint32_t wa = qq[2 * (s & 1)], wb = qq[2 * (s & 1) + 1];
+      const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+      const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+      cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[s], blo, cl, 0, 0, 0);
+      ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(x.f[4 + s], bhi, ch, 0, 0, 0);
+    }
+    const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(x.xs, kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      acc[v] += fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * x.dv[v];
+  }
+};
+
 struct FmtIQ4XS {
   static constexpr int kTB = kTileN * kIQ4BlockBytes;
   static constexpr bool kMin = false;
@@ -2630,15 +2441,6 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const Gemv
   return gemv_multi_row_tile<3, GATED>(s, a, dtype, shape.waves);
 }
 
-template <int T, int NM, int W, int DP>
-hipError_t stream_launch(hipStream_t s, const GemvArgs& a, int dtype, int grid, int items) {
-  if (dtype == kF32)
-    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, DP, float>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
-  else
-    (void)dispatch(q4k_gemv_stream_kernel<T, NM, W, DP, _Float16>, dim3((unsigned)grid), dim3(64 * W), s, a, items);
-  return hipGetLastError();
-}
-
 }  // namespace
 
 namespace {
@@ -2729,36 +2531,6 @@ hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int 
   if (a.norm_w)
     return t3 ? gate_up_launch<3, true>(s, a, dtype, grid) : gate_up_launch<1, true>(s, a, dtype, grid);
   return t3 ? gate_up_launch<3, false>(s, a, dtype, grid) : gate_up_launch<1, false>(s, a, dtype, grid);
-}
-
-bool gemv_stream_supported(int rows, int nb, int n, bool gated, int cus) {
-  // Gated pairs (K = 4096) and wide outputs (4 tiles per item, at least 4
-  // items per CU); narrower plain projections measure faster on the
-  // register-buffered GEMV.
-  static const bool enabled = env_int("Q4K_GEMV_STREAM", 1) != 0;
-  if (!enabled || rows > 16 || nb != 16 || n % 16 != 0)
-    return false;
-  const int ctiles = n / 16;
-  return gated || (ctiles % 4 == 0 && ctiles / 4 >= 4 * cus);
-}
-
-hipError_t launch_gemv_stream(hipStream_t s, const GemvArgs& a, int dtype, bool gated, int cus) {
-  // K = 4096 (nb = 16): 8 waves x 2 blocks.  Items of T column tiles (an
-  // even number of (matrix, tile) pairs): T = 3 makes gated N = 12288
-  // exactly one item per CU; other gated outputs take 1; wide plain outputs 4.
-  // LDS holds the rings (2 * DP slots of 2304 B per wave) next to the
-  // partial sums (W * 2T KB gated, W * T KB otherwise).
-  const int ctiles = a.n / 16;
-  int tiles;
-  if (gated)
-    tiles = ctiles % 3 == 0 && ctiles / 3 == cus ? 3 : 1;
-  else
-    tiles = 4;
-  const int items = ctiles / tiles;
-  const int grid = items < cus ? items : cus;
-  if (gated)
-    return tiles == 3 ? stream_launch<3, 2, 8, 3>(s, a, dtype, grid, items) : stream_launch<1, 2, 8, 3>(s, a, dtype, grid, items);
-  return stream_launch<4, 1, 8, 3>(s, a, dtype, grid, items);
 }
 
 template <typename InT>
@@ -2946,6 +2718,17 @@ hipError_t typed_gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, int 
   if (t == 2)
     return typed_gemv_launch<F, 2, 2>(s, a, dtype);
   return typed_gemv_launch<F, 1, 2>(s, a, dtype);
+}
+
+// The Q4_K LM-head shape (K = 4096, at least 16 column tiles per CU, m <= 8)
+// on the persistent form.
+bool q4k_persistent_supported(int m, int nb, int n, int cus) {
+  static const int on = env_int("Q4K_GEMV_PERSISTENT", 1);
+  return on && m >= 1 && m <= 8 && nb == 16 && n % 16 == 0 && n / 16 >= 16 * cus;
+}
+
+hipError_t launch_q4k_persistent(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+  return typed_persistent_launch<FmtQ4K, FmtQ4K::kPT, 2, FmtQ4K::kPW>(s, a, dtype, cus);
 }
 
 hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus) {

@@ -6,7 +6,7 @@ decode pass.  Shapes are chosen to reach each kernel:
   gated, K=4096, N=12288   fused gate/up GEMV, 3 column tiles per workgroup
   gated, K=4096, N=512     fused gate/up GEMV, 1 column tile per workgroup
   plain, K=12288, N=1024   split-K GEMV (8 tiles x 8 K-slices of 6 blocks)
-  plain, K=4096, N=65536   decode pack + streaming GEMV, 4 column tiles per item
+  plain, K=4096, N=65536   decode pack + persistent GEMV (16 waves, x in registers)
 
 Bar: max row-relative error 1e-3 against the fp32-accumulated oracle.
 """
@@ -101,16 +101,24 @@ def test_splitk_f16_and_repeat(q4k, oracle, gpu):
         assert row_rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
-def test_wide_stream(q4k, oracle, gpu):
-    m, n, k = 3, 65536, 4096
-    rng = np.random.default_rng(1400)
+@pytest.mark.parametrize("m,n,post,dtype", [(3, 65536, 0, torch.float32), (8, 16 * 4401, 1, torch.float32),
+                                             (1, 16 * 4401, 2, torch.float32), (8, 65536, 1, torch.float16)])
+def test_wide_persistent(q4k, oracle, gpu, m, n, post, dtype):
+    """Wide plain projections (the LM head's shape class): the persistent
+    GEMV, 2 column tiles per item (16 * 4401 columns: one tile in the last)."""
+    k = 4096
+    rng = np.random.default_rng(1400 + m + post)
     w = make_q4k(rng, n, k)
-    x = make_x(rng, m, k)
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    x = make_x(rng, m, k).astype(npdt)
+    aux = make_x(rng, m, n, 2.0).astype(npdt) if post else None
     W = q4k.Weight(w, n, k)
-    y = torch.empty((m, n), device=gpu)
-    q4k.linear(_t(x, gpu), W, m, y, query_counts=[m])
+    y = torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+    if post:
+        y.copy_(_t(aux, gpu).to(dtype))
+    q4k.linear(_t(x, gpu).to(dtype), W, m, y, auxiliary=y if post else None, gated=post == 2, query_counts=[1] * m)
     torch.cuda.synchronize()
-    assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k)) <= TOL
+    assert row_rel_err(y.float().cpu().numpy(), oracle.linear(x, w, n, k, aux=aux, post=post)) <= TOL
 
 
 def test_decode_rows_of_extreme_magnitude(q4k, oracle, gpu):
