@@ -80,6 +80,21 @@ __device__ __forceinline__ void scale_min_pair(u4_t hd, int g, uint32_t& sc0, ui
   m1 = ((xb >> 8) & 15u) | ((yb >> 8) & 0x30u);
 }
 
+// The same pairs as 16-bit lanes: p0 = sc(2g) | m(2g) << 16, p1 = sc(2g + 1) |
+// m(2g + 1) << 16.  Bytes 0 / 1 of the selected words are gathered with one
+// v_perm_b32 per word pair.
+__device__ __forceinline__ void scale_min_packed(u4_t hd, int g, uint32_t& p0, uint32_t& p1) {
+  const uint32_t sh = 16u * (uint32_t)(g & 1);
+  const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
+  const bool low = g < 2;
+  const uint32_t ysh = low ? 0u : 2u, xsh = low ? 0u : 4u;
+  const uint32_t xa = low ? a : c, xb = (low ? b : c) >> xsh, ya = a >> ysh, yb = b >> ysh;
+  const uint32_t x0 = __builtin_amdgcn_perm(xb, xa, 0x0C040C00u), x1 = __builtin_amdgcn_perm(xb, xa, 0x0C050C01u);
+  const uint32_t y0 = __builtin_amdgcn_perm(yb, ya, 0x0C040C00u), y1 = __builtin_amdgcn_perm(yb, ya, 0x0C050C01u);
+  p0 = (x0 & 0x000F000Fu) | (y0 & 0x00300030u);
+  p1 = (x1 & 0x000F000Fu) | (y1 & 0x00300030u);
+}
+
 // (a & mask) | bits in one v_and_or_b32.  Written as asm because gfx9 VOP3
 // encodings cannot take the two literal constants the compiler would
 // otherwise need, so it splits the expression into v_and + v_or.
@@ -1549,23 +1564,26 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   // Block constants of the 4 column tiles: h(d * sc), -h(dmin * m) of
   // sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles), from the 4
   // headers (this lane's column) of one block.
-  h2_t dslo[4], dmlo[4], dshi[4], dmhi[4];
-  auto block_consts_from = [&](const u4_t* hd) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t sc0, mn0, sc1, mn1;
-      scale_min_pair(hd[c], g, sc0, mn0, sc1, mn1);
-      const float d = half_bits_to_float(hd[c].x & 0xffffu), dmin = half_bits_to_float(hd[c].x >> 16);
-      const _Float16 a0 = (_Float16)(d * (float)sc0), b0 = (_Float16)(dmin * (float)mn0);
-      const _Float16 a1 = (_Float16)(d * (float)sc1), b1 = (_Float16)(dmin * (float)mn1);
-      dslo[c] = h2_t{a0, a0};
-      dmlo[c] = h2_t{-b0, -b0};
-      dshi[c] = h2_t{a1, a1};
-      dmhi[c] = h2_t{-b1, -b1};
-    }
+  // Kept as packed pairs (h(d * sc), h(dmin * m)): the 6-bit fields become
+  // exact fp16 through the 1024 bias, and one v_pk_mul_f16 by the header's
+  // (d, dmin) word rounds each product once, as the fp32 product (exact for
+  // 11 x 6 bits) converted to fp16 would.
+  h2_t pclo[4], pchi[4];
+  auto block_const = [&](int c, const u4_t& hd) {
+    uint32_t p0, p1;
+    scale_min_packed(hd, g, p0, p1);
+    const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2_t dd = as_h2(hd.x);
+    pclo[c] = (as_h2(p0 | 0x64006400u) + k1024) * dd;
+    pchi[c] = (as_h2(p1 | 0x64006400u) + k1024) * dd;
   };
   // B fragments of column tile c from its two raw words (words 2(u & 1),
   // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants.
+  // The nibble masks and the fp16 bias live in registers (VOP3 takes no
+  // literal on this target), as plain values so that the scheduler sees the
+  // v_and_or_b32 it selects as vector ALU work and interleaves it.
+  uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, m_bias = 0x64006400u;
+  asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(m_bias));
   auto dequant_words = [&](int c, uint2 wv, h8_t& blo, h8_t& bhi) {
     const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const h2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
@@ -1573,10 +1591,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     u4_t lo, hi;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const h2_t ql = as_h2(and_or(lw[e], 0x000F000Fu, 0x64006400u)) + k1024;
-      const h2_t qh = __builtin_elementwise_fma(as_h2(and_or(lw[e], 0x00F000F0u, 0x64006400u)), k16, k64);
-      lo[e] = as_u32(__builtin_elementwise_fma(ql, dslo[c], dmlo[c]));
-      hi[e] = as_u32(__builtin_elementwise_fma(qh, dshi[c], dmhi[c]));
+      const h2_t ql = as_h2((lw[e] & m_lo) | m_bias) + k1024;
+      const h2_t qh = __builtin_elementwise_fma(as_h2((lw[e] & m_hi) | m_bias), k16, k64);
+      lo[e] = as_u32(__builtin_elementwise_fma(ql, h2_t{pclo[c][0], pclo[c][0]}, h2_t{-pclo[c][1], -pclo[c][1]}));
+      hi[e] = as_u32(__builtin_elementwise_fma(qh, h2_t{pchi[c][0], pchi[c][0]}, h2_t{-pchi[c][1], -pchi[c][1]}));
     }
     blo = __builtin_bit_cast(h8_t, lo);
     bhi = __builtin_bit_cast(h8_t, hi);
@@ -1603,16 +1621,26 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
       issue_a(t, i);
   // B(0) and A(0) landed: A(1..3) (12 loads) were issued after them.
   asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  // Dequantisation runs one column behind the MFMAs: column c of u-step
+  // t + 1 is dequantised under the MFMAs of column c + 1 of u-step t, and
+  // column 3 under those of column 0 of u-step t + 1 (from words kept in
+  // wv3), so that every column's MFMAs have vector work to cover.  At the
+  // last u-step of a block the next block's constants of column c are
+  // computed under column c's MFMAs, after column 3 of the current u-step
+  // (old constants) was dequantised and before column c's first use.
   h8_t bclo[4], bchi[4];  // dequantised B fragments of the current u-step
+  uint2 wv3;              // raw words of column 3 for the current u-step
   {
     u4_t hd[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 4; ++c) {
       hd[c] = *reinterpret_cast<const u4_t*>(bring + c * kTileBlockBytes + kHeaderOffset + 16 * col);
-    block_consts_from(hd);
+      block_const(c, hd[c]);
+    }
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 3; ++c)
       dequant_words(c, *reinterpret_cast<const uint2*>(bring + c * kTileBlockBytes + 16 * lane), bclo[c], bchi[c]);
+    wv3 = *reinterpret_cast<const uint2*>(bring + 3 * kTileBlockBytes + 16 * lane);
   }
   for (int blk = 0; blk < nb; ++blk) {
 #pragma unroll
@@ -1658,13 +1686,18 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
       // column c runs under the MFMAs of column c + 1.
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
+        if (c == 0)
+          dequant_words(3, wv3, bclo[3], bchi[3]);  // column 3 of this u-step
+        // Low-nibble fragments over the 8 row tiles, then the high ones:
+        // neighbouring MFMAs are independent.
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt) {
+        for (int rt = 0; rt < 8; ++rt)
           acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt], bclo[c], acc[rt][c], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
           acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt + 1], bchi[c], acc[rt][c], 0, 0, 0);
-        }
-        if (c == 0 && u == 3)
-          block_consts_from(hd);
+        if (u == 3)
+          block_const(c, hd[c]);
         if (c > 0)
           dequant_words(c - 1, wv[c - 1], bclo[c - 1], bchi[c - 1]);
         // The loads of the column group, spread over the step: fragment c
@@ -1673,7 +1706,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
         if (u == 0)
           issue_b(blk + 1, c);
       }
-      dequant_words(3, wv[3], bclo[3], bchi[3]);
+      wv3 = wv[3];
       // Schedule of the step: the LDS reads first, then each MFMA followed
       // by a share of the vector work (the next step's dequantisation, and
       // at u = 3 the next block's constants), so that no vector work is
