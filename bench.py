@@ -260,10 +260,11 @@ def neighbours_bench(args, dev):
     return out
 
 
-def q6k_bench(args, dev):
-    """The Q6_K LM head of real Qwen3.5 GGUF files (output.weight, K = 4096 ->
-    N = 248,320, 834 MB; quant_linear.metal:644-650) on 8 gathered rows, as
-    config 3's LM-head pass runs it: the decode pack of x, then the Q6_K GEMV.
+def lm_head_bench(dev, ggml_type):
+    """The LM head (K = 4096 -> N = 248,320) on 8 gathered rows, as config 3's
+    LM-head pass runs it: the decode pack of x, then the persistent GEMV.
+    Q4_K (572 MB) is the configuration's own type; Q6_K (834 MB) is what real
+    Qwen3.5 GGUF files store as output.weight (quant_linear.metal:644-650).
     Timed per launch with dispatch-attached events (GEMV and pack), and as a
     whole from a graph of both launches."""
     import torch
@@ -271,11 +272,18 @@ def q6k_bench(args, dev):
 
     n, k, m = 248320, 4096, 8
     nb = k // 256
-    g = torch.Generator(device=dev).manual_seed(0x51A70006)
-    raw = torch.randint(0, 256, (n, nb, 210), dtype=torch.uint8, device=dev, generator=g)
-    dd = (torch.rand((n, nb, 1), device=dev, generator=g) * 0.01).half().view(torch.uint8)
-    raw[:, :, 208:210] = dd.view(n, nb, 2)
-    W = q4k.Weight(raw.reshape(-1), n, k, ggml_type=q4k.GGML_TYPE_Q6_K)
+    g = torch.Generator(device=dev).manual_seed(0x51A70006 + ggml_type)
+    if ggml_type == q4k.GGML_TYPE_Q6_K:
+        bb, name = 210, "Q6_K"
+        raw = torch.randint(0, 256, (n, nb, bb), dtype=torch.uint8, device=dev, generator=g)
+        dd = (torch.rand((n, nb, 1), device=dev, generator=g) * 0.01).half().view(torch.uint8)
+        raw[:, :, 208:210] = dd.view(n, nb, 2)
+    else:  # Q4_K: d, dmin ~ U(0, 0.01), as in config 0
+        bb, name = 144, "Q4_K"
+        raw = torch.randint(0, 256, (n, nb, bb), dtype=torch.uint8, device=dev, generator=g)
+        dd = (torch.rand((n, nb, 2), device=dev, generator=g) * 0.01).half().view(torch.uint8)
+        raw[:, :, 0:4] = dd.view(n, nb, 4)
+    W = q4k.Weight(raw.reshape(-1), n, k, ggml_type=ggml_type)
     del raw, dd
     x = torch.randn((m, k), device=dev, generator=g)
     y = torch.empty((m, n), device=dev)
@@ -299,10 +307,10 @@ def q6k_bench(args, dev):
     graph.replay()
     torch.cuda.synchronize()
     step_ms = timed_graph(graph, 3) / (3 * reps) * 1e3
-    weight_bytes = n * nb * 210
+    weight_bytes = n * nb * bb
     nbytes = weight_bytes + m * k * 4 + m * n * 4
     gemv_us = tg / ng * 1e3
-    return {"shape": f"Q6_K N={n} K={k} m={m}", "gemv_avg_us": round(gemv_us, 2), "gemv_min_us": round(lg * 1e3, 2),
+    return {"shape": f"{name} N={n} K={k} m={m}", "kernel": W.kernel_name(0), "gemv_avg_us": round(gemv_us, 2), "gemv_min_us": round(lg * 1e3, 2),
             "pack_avg_us": round(ts / ns * 1e3, 2), "step_us": round(step_ms * 1e3, 2), "bytes": nbytes,
             "gemv_gbs": round(nbytes / (gemv_us * 1e-6) / 1e9, 1), "gemv_frac_of_8tbs": round(nbytes / (gemv_us * 1e-6) / 8e12, 3),
             "step_gbs": round(nbytes / (step_ms * 1e-3) / 1e9, 1)}
@@ -494,7 +502,8 @@ def main():
     pre = None if args.no_prefill else prefill_bench(args, dev)
     shard = shard_bench(args, dev)
     neighbours = neighbours_bench(args, dev)
-    q6k = q6k_bench(args, dev)
+    q4k_head = lm_head_bench(dev, 12)
+    q6k = lm_head_bench(dev, 14)
     types = None if args.no_types else types_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
@@ -543,6 +552,7 @@ def main():
         },
         "shard_1of8": shard,
         "neighbours": neighbours,
+        "q4k_lm_head": q4k_head,
         "q6k_lm_head": q6k,
         "types_lm_head": types,
         "copy_ceiling_gbs": round(copy_gbs, 1),
