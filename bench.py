@@ -260,6 +260,100 @@ def neighbours_bench(args, dev):
     return out
 
 
+def configs_bench(dev):
+    """The two remaining BASELINE configurations, each as one HIP graph of
+    its projections (random Q4_K weights as in config 0, seeded fp32
+    activations), timed over replays:
+      config 2: speculative verify, 8 sequences x 5 tokens = 40 rows, query
+        counts 5 (the decode phase, forward.cpp:190): QKV 4096 -> 6144, O
+        4096 -> 4096 with the residual, and the config-1 MLP (q4k_mlp);
+      config 3: ragged prefill of lengths {512,37,1,1,200,5,1,64} = 821 rows
+        (the prefill phase): QKV, O with the residual, gate (post 0), up with
+        in-place SiLU gating (post 2), down with the residual, then
+        rms_norm_gather of each sequence's last row and the Q4_K LM head
+        4096 -> 248,320 on those 8 rows (forward.cpp:72-75, 115-119).
+    Reports the time per pass and its algorithmic rate: weight + activation
+    bytes for config 2 (HBM-bound), 2 M N K FLOP of the projections for
+    config 3 (its prefill GEMMs dominate)."""
+    import torch
+    import mtlqwen_amd as q4k
+
+    g = torch.Generator(device=dev).manual_seed(0x51A70009)
+
+    def weight(n, k):
+        nb = k // 256
+        raw = torch.randint(0, 256, (n, nb, 144), dtype=torch.uint8, device=dev, generator=g)
+        raw[:, :, 0:4] = (torch.rand((n, nb, 2), device=dev, generator=g) * 0.01).half().view(torch.uint8).view(n, nb, 4)
+        return q4k.Weight(raw.reshape(-1), n, k)
+
+    K, F = 4096, 12288
+    qkv, o, gw, uw, dw = weight(6144, K), weight(K, K), weight(F, K), weight(F, K), weight(K, F)
+    head = weight(248320, K)
+    norm_w = torch.rand(K, device=dev, generator=g) + 0.5
+    out = {}
+    reps = 20
+
+    def run(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        return timed_graph(graph, 5) / (5 * reps)
+
+    # config 2
+    M = 40
+    counts = [5] * 8
+    x = torch.randn((M, K), device=dev, generator=g)
+    hidden = torch.randn((M, K), device=dev, generator=g)
+    yq = torch.empty((M, 6144), device=dev)
+    gate = torch.empty((M, F), device=dev)
+
+    def pass2():
+        q4k.linear(x, qkv, M, yq, query_counts=counts)
+        q4k.linear(x, o, M, hidden, auxiliary=hidden, query_counts=counts)
+        q4k.mlp(x, gw, uw, dw, hidden, gate, M, query_counts=counts)
+
+    dt = run(pass2)
+    wbytes = (6144 + K + 2 * F) * (K // 256) * 144 + K * (F // 256) * 144
+    abytes = 4 * M * (3 * K + 6144 + 2 * K + 2 * F + 2 * K)
+    out["config2"] = {"workload": "M=40 (8 x 5 tokens, decode phase): QKV 4096->6144, O 4096->4096 + residual, MLP 4096->12288x2->4096 + residual",
+                      "us_per_pass": round(dt * 1e6, 2), "bytes": wbytes + abytes, "gbs": round((wbytes + abytes) / dt / 1e9, 1),
+                      "frac_of_8tbs": round((wbytes + abytes) / dt / 8e12, 3)}
+
+    # config 3
+    lengths = [512, 37, 1, 1, 200, 5, 1, 64]
+    M = sum(lengths)
+    x = torch.randn((M, K), device=dev, generator=g)
+    hidden = torch.randn((M, K), device=dev, generator=g)
+    yq = torch.empty((M, 6144), device=dev)
+    gate = torch.empty((M, F), device=dev)
+    lm_rows = torch.empty((8, K), device=dev)
+    logits = torch.empty((8, 248320), device=dev)
+
+    def pass3():
+        q4k.linear(x, qkv, M, yq, query_counts=lengths)
+        q4k.linear(x, o, M, hidden, auxiliary=hidden, query_counts=lengths)
+        q4k.linear(x, gw, M, gate, query_counts=lengths)
+        q4k.linear(x, uw, M, gate, auxiliary=gate, gated=True, query_counts=lengths)
+        q4k.linear(gate, dw, M, hidden, auxiliary=hidden, query_counts=lengths)
+        q4k.rms_norm_gather(hidden, norm_w, lm_rows, lengths, [1] * 8)
+        q4k.linear(lm_rows, head, 8, logits, query_counts=[8])
+
+    dt = run(pass3)
+    flops = 2 * M * K * (6144 + K + 2 * F + F)
+    head_flops = 2 * 8 * K * 248320
+    out["config3"] = {"workload": "M=821 ragged prefill {512,37,1,1,200,5,1,64}: QKV, O + residual, gate, up (SiLU gating in place), down + residual, rms_norm_gather, Q4_K LM head 4096->248320 on 8 rows",
+                      "us_per_pass": round(dt * 1e6, 2), "projection_flop": flops, "tflops_incl_lm_head": round((flops + head_flops) / dt / 1e12, 1),
+                      "kernels": {"prefill": qkv.kernel_name(1), "lm_head": head.kernel_name(2)}}
+    return out
+
+
 def lm_head_bench(dev, ggml_type):
     """The LM head (K = 4096 -> N = 248,320) on 8 gathered rows, as config 3's
     LM-head pass runs it: the decode pack of x, then the persistent GEMV.
@@ -502,6 +596,7 @@ def main():
     pre = None if args.no_prefill else prefill_bench(args, dev)
     shard = shard_bench(args, dev)
     neighbours = neighbours_bench(args, dev)
+    cfgs = configs_bench(dev)
     q4k_head = lm_head_bench(dev, 12)
     q6k = lm_head_bench(dev, 14)
     types = None if args.no_types else types_bench(args, dev)
@@ -552,6 +647,7 @@ def main():
         },
         "shard_1of8": shard,
         "neighbours": neighbours,
+        "configs_2_3": cfgs,
         "q4k_lm_head": q4k_head,
         "q6k_lm_head": q6k,
         "types_lm_head": types,
