@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X Q4_K linear() path (one JSON line on stdout).
 
-Headline (BASELINE.json metric, config 1): the ragged decode batch of 8
+Headline (the benchmark's metric, config 1): the ragged decode batch of 8
 sequences x 1 token through the Qwen3.5-9B-shaped MLP with Q4_K weights --
 fused gate/up (K=4096 -> N=12288, x2, SiLU(gate)*up into the gate buffer) then
 down (K=12288 -> N=4096, residual added in place).  A step is one such MLP
@@ -261,7 +261,7 @@ def neighbours_bench(args, dev):
 
 
 def configs_bench(dev):
-    """The two remaining BASELINE configurations, each as one HIP graph of
+    """Benchmark configurations 2 and 3, each as one HIP graph of
     its projections (random Q4_K weights as in config 0, seeded fp32
     activations), timed over replays:
       config 2: speculative verify, 8 sequences x 5 tokens = 40 rows, query
@@ -617,7 +617,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded Q4_K weights per BASELINE config 0 recipe, N(0,1)*0.5 activations)",
+        "data": "synthetic (seeded Q4_K weights per the config-0 recipe, N(0,1)*0.5 activations)",
         "config": {
             "workload": "config1: ragged decode M=8 (8 seqs x 1 token), Q4_K MLP: fused gate/up 4096->12288 x2 "
                         "+ down 12288->4096 with in-place residual (q4k_mlp: two launches); HIP-graph replay",

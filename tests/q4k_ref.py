@@ -20,7 +20,7 @@ TYPE_BLOCK_BYTES = {TYPE_Q4_K: BLOCK_BYTES, TYPE_Q6_K: Q6_BLOCK_BYTES, TYPE_Q8_0
 IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float64)
 
 # --------------------------------------------------------------------------
-# Synthetic data (the BASELINE config-0 recipe).
+# Synthetic data (the benchmark's config-0 recipe).
 # --------------------------------------------------------------------------
 
 
@@ -407,7 +407,7 @@ class Oracle:
 
 
 def row_rel_err(y, ref):
-    """Max over rows of ||y - ref|| / ||ref|| (the BASELINE tolerance metric)."""
+    """Max over rows of ||y - ref|| / ||ref|| (the tolerance metric of the parity bar)."""
     y = np.asarray(y, np.float64)
     ref = np.asarray(ref, np.float64)
     num = np.linalg.norm(y - ref, axis=-1)

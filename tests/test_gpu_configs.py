@@ -1,4 +1,4 @@
-"""The five BASELINE configurations at their full shapes, HIP path vs oracle.
+"""The five benchmark configurations at their full shapes, HIP path vs oracle.
 
 Config 4 (M=2048) is checked on a 64-row subset against the oracle (the GPU
 computes all rows; the oracle recomputes the subset) plus a size-independent

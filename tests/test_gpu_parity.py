@@ -1,6 +1,6 @@
 """HIP path vs the CPU oracle on identical seeded inputs (run on the GPU box).
 
-Bar (BASELINE north star): max over output rows of ||y - ref|| / ||ref|| <= 1e-3,
+Bar: max over output rows of ||y - ref|| / ||ref|| <= 1e-3,
 ref = the oracle's fp32-accumulated Q4_K dequant-dot on the same inputs.
 The GEMV rounds activations to fp16 (row-scaled, weights exact); the GEMM
 also rounds dequantised weights to fp16 as the reference's prefill tiles do
