@@ -472,12 +472,16 @@ def prefill_bench(args, dev):
 
     step()
     torch.cuda.synchronize()
+    # Four steps per graph, as the decode graph holds many: one replay's host
+    # launch boundary is then shared by four steps instead of charged to one.
+    per_graph = 4
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        step()
+        for _ in range(per_graph):
+            step()
     timed_graph(graph, 2)
     elapsed = timed_graph(graph, args.prefill_steps)
-    ms = elapsed / args.prefill_steps * 1e3
+    ms = elapsed / (args.prefill_steps * per_graph) * 1e3
     q4k.profile_enable(True)
     for _ in range(args.prefill_steps):
         step()
