@@ -401,15 +401,17 @@ __device__ __forceinline__ void pack_block_row(const float (&v)[4], int r, int l
 // rows' 16-byte pieces of one fragment lane group are one 128-byte line, so
 // every line is written whole by one workgroup (row-per-workgroup staging
 // leaves 8 workgroups, on different XCDs, writing 16 bytes of each line).
-// CPT > 0: the row's K / 256 <= CPT chunks per thread stay in registers
+// TPR threads per row (32, or 64 for long rows: 512 threads per workgroup).
+// CPT > 0: the row's K / (8 TPR) <= CPT chunks per thread stay in registers
 // between the maximum and the conversion; CPT == 0: x is read twice.
-template <typename InT, int CPT>
-__global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale, int m,
-                                                         int k) {
-  const int t = threadIdx.x, q = t & 31;
-  const int row = blockIdx.x * 8 + (t >> 5);
+template <typename InT, int CPT, int TPR = 32>
+__global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale,
+                                                             int m, int k) {
+  static_assert(TPR == 32 || TPR == 64, "one row per half wave or per wave");
+  const int t = threadIdx.x, q = t & (TPR - 1);
+  const int row = blockIdx.x * 8 + t / TPR;
   const bool live = row < m;
-  const int nb = k >> 8, cpt = k >> 8;
+  const int nb = k >> 8, cpt = (k >> 3) / TPR;
   const InT* xr = x + (size_t)(live ? row : 0) * k;
   float v[CPT > 0 ? CPT : 1][8];
   float mx = 0.0f;
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__
 #pragma unroll
     for (int j = 0; j < CPT; ++j)
       if (live && j < cpt)
-        load8(xr + (size_t)(q + 32 * j) * 8, v[j]);
+        load8(xr + (size_t)(q + TPR * j) * 8, v[j]);
 #pragma unroll
     for (int j = 0; j < CPT; ++j)
 #pragma unroll
@@ -431,13 +433,14 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__
   } else if (live) {
     for (int j = 0; j < cpt; ++j) {
       float w[8];
-      load8(xr + (size_t)(q + 32 * j) * 8, w);
+      load8(xr + (size_t)(q + TPR * j) * 8, w);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         mx = fmaxf(mx, fabsf(w[i]));
     }
   }
-  // Row maximum: lanes 0..31 and 32..63 of a wave are two rows.
+  // Row maximum: lanes 0..31 and 32..63 of a wave are two rows (TPR = 32),
+  // or the whole wave is one (TPR = 64).
   mx = fmaxf(mx, dpp_f<kDppQuadSwap1>(mx));
   mx = fmaxf(mx, dpp_f<kDppQuadSwap2>(mx));
   mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
@@ -446,7 +449,7 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__
     const int b = __builtin_bit_cast(int, mx);
     const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
     const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-    mx = (t & 63) < 32 ? fmaxf(r0, r1) : fmaxf(r2, r3);
+    mx = TPR == 64 ? fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)) : (t & 63) < 32 ? fmaxf(r0, r1) : fmaxf(r2, r3);
   }
   float up = 1.0f, down = 1.0f;
   if (mx > 0.0f && mx <= FLT_MAX) {
@@ -465,7 +468,7 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       h[i] = (_Float16)(w[i] * up);
-    *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, q + 32 * j, nb)) = h;
+    *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, q + TPR * j, nb)) = h;
   };
   if (CPT > 0) {
 #pragma unroll
@@ -475,7 +478,7 @@ __global__ __launch_bounds__(256) void stage_gemm_kernel(const InT* __restrict__
   } else {
     for (int j = 0; j < cpt; ++j) {
       float w[8];
-      load8(xr + (size_t)(q + 32 * j) * 8, w);
+      load8(xr + (size_t)(q + TPR * j) * 8, w);
       put(j, w);
     }
   }
@@ -2577,6 +2580,8 @@ hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs,
     (void)dispatch(stage_x_kernel<InT, kStageGemm>, grid, block, s, x, xo, xs, rowscale, m, k);
   else if (mode == kStageGemm && k / 256 <= 16)
     (void)dispatch(stage_gemm_kernel<InT, 16>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k);
+  else if (mode == kStageGemm && k % 512 == 0 && k / 512 <= 24)  // K <= 12288: one read of x, 64 threads per row
+    (void)dispatch(stage_gemm_kernel<InT, 24, 64>, dim3((unsigned)((m + 7) / 8)), dim3(512), s, x, xo, rowscale, m, k);
   else if (mode == kStageGemm)
     (void)dispatch(stage_gemm_kernel<InT, 0>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k);
   else

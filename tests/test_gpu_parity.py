@@ -244,11 +244,14 @@ def test_gather_rows(q4k, gpu):
     assert torch.equal(out, x[torch.as_tensor(last, device=gpu)])
 
 
-@pytest.mark.parametrize("m,k,dtype", [(2051, 4096, torch.float16), (2050, 12288, torch.float32)])
+@pytest.mark.parametrize("m,k,dtype", [(2051, 4096, torch.float16), (2050, 12288, torch.float32), (2051, 8192, torch.float16),
+                                       (2049, 4352, torch.float32)])
 def test_gemm_eight_row_staging(q4k, oracle, gpu, m, k, dtype):
-    """m >= 2048 stages x eight rows per workgroup: in registers for K <= 4096,
-    in two passes over x beyond.  A ragged last workgroup (rows past m) and
-    fp16 input; rows are checked on a subset that includes the last ones."""
+    """m >= 2048 stages x eight rows per workgroup: in registers with 32
+    threads per row for K <= 4096, with 64 threads per row for K a multiple
+    of 512 up to 12288, in two passes over x otherwise (K = 4352: 17 blocks).
+    A ragged last workgroup (rows past m) and fp16 input; rows are checked on
+    a subset that includes the last ones."""
     n = 256
     rng = np.random.default_rng(2000 + k)
     w = make_q4k(rng, n, k)
