@@ -528,9 +528,30 @@ def copy_ceiling(dev):
     return 2 * 4 * n * reps / (time.perf_counter() - t0) / 1e9
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may run on,
+    up to the share the GPU box allots one GPU (OMP_NUM_THREADS there: 16),
+    so the baseline does not oversubscribe the cores of other jobs."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(avail, share) if share > 0 else avail)
+
+
 def cpu_baseline(args):
     """The C oracle (a port of the reference's arithmetic; the reference itself
-    is Metal-only) on the config-1 MLP, on up to 16 host threads."""
+    is Metal-only) on the config-1 MLP, on every host core allotted to this
+    process (cpu_threads)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from q4k_ref import Oracle
@@ -541,7 +562,7 @@ def cpu_baseline(args):
     wg, wu, wd = make_q4k(rng, N, K), make_q4k(rng, N, K), make_q4k(rng, K, N)
     x = (rng.standard_normal((M, K)) * 0.5).astype(np.float32)
     hidden = rng.standard_normal((M, K)).astype(np.float32)
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     iters, t0 = 0, time.perf_counter()
     while True:
         g = oracle.mlp_gate_up(x, wg, wu, N, K, threads=threads)
@@ -574,6 +595,8 @@ def cpu_baseline(args):
     dt4, n4 = timed(mlp4, args.cpu_seconds / 4)
     flop_tok = 3 * 2.0 * N * K
     return {"value": step_bytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
+            "cores_note": "threads = the cores allotted to this process (OMP_NUM_THREADS share of the GPU box, within its CPU affinity)",
             "sample": f"{iters} config-1 MLP steps (M=8, gate/up 4096->12288 x2 + down 12288->4096) "
                       f"in {dt * iters:.1f} s, {dt * 1e3:.1f} ms/step",
             "configs": {

@@ -17,6 +17,12 @@
  *  - Calls on one device share that device's staging workspace: issue them
  *    from one submitter / one stream at a time, as the reference engine does
  *    (single worker thread, one command buffer per pass).
+ *  - The workspace grows (hipMalloc) on the first call of a larger shape and
+ *    is kept until the process ends.  A call made while its stream captures
+ *    a HIP graph must not need growth: the launch that would need it fails
+ *    with Q4K_ECAPTURE before allocating (q4k_mlp and the two-call form of
+ *    q4k_mlp_gate_up may have enqueued their earlier launches by then).  One
+ *    call of the same shapes before the capture avoids it.
  */
 #ifndef Q4K_H
 #define Q4K_H
@@ -37,6 +43,7 @@ extern "C" {
 #define Q4K_ENOMEM (-6)
 #define Q4K_EFORMAT (-7)   /* malformed or truncated GGUF file */
 #define Q4K_ENOTFOUND (-8) /* missing file, tensor or metadata key */
+#define Q4K_ECAPTURE (-9)  /* the call needs more workspace than the device holds, and its stream is capturing a graph */
 
 #define Q4K_GGML_TYPE_Q4_K 12u
 #define Q4K_GGML_TYPE_Q6_K 14u   /* the Q6_K LM head / mixed-type files (quant_linear.metal:69-86,437-497) */

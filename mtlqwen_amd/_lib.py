@@ -20,6 +20,7 @@ EHIP = -5
 ENOMEM = -6
 EFORMAT = -7
 ENOTFOUND = -8
+ECAPTURE = -9
 
 GGML_TYPE_Q4_K = 12
 GGML_TYPE_Q6_K = 14

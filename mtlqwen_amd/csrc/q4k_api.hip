@@ -81,7 +81,7 @@ struct Workspace {
   size_t counter_elems = 0;
   uint8_t* pack = nullptr;  // decode pack of x (m <= 8)
   size_t pack_bytes = 0;
-  void* normed = nullptr;  // q4k_mlp's RMS-normalised x when the norm is not fused
+  uint8_t* normed = nullptr;  // q4k_mlp's RMS-normalised x when the norm is not fused
   size_t normed_bytes = 0;
   _Float16* wdq = nullptr;  // prefill with the other types: dequantised fp16 weights [n, k]
   size_t wdq_elems = 0;
@@ -299,6 +299,14 @@ int check_counts(const uint32_t* counts, uint32_t nq, uint32_t m) {
   return Q4K_OK;
 }
 
+// Q4_K prefill with fewer output columns than this runs the GEMV per 8-row
+// group (hi/lo activations, weights exact) instead of the GEMM, whose fp16
+// activations and weights leave a per-row error near the 1e-3 bar when a row
+// has few outputs to average over.  Batches of up to 24 rows keep the staged
+// hi/lo GEMV.
+constexpr uint32_t kGemmMinColumns = 256;
+constexpr uint32_t kGemvSplitRows = 24;
+
 // The kernel family each phase resolves to.  Decode-shaped phases (0, 2, 3)
 // run the MFMA GEMV; prefill (1) runs the LDS-tiled MFMA GEMM, whose slot also
 // serves prefill batches small enough for the GEMV (<= 48 rows) with the GEMV
@@ -311,6 +319,8 @@ Kernel& resolve(q4k_weight* w, uint32_t phase) {
     const bool other = w->type != Q4K_GGML_TYPE_Q4_K;
     if (other && k.kind == kGemm)
       k.kind = kGemv;  // prefill of the other types: GEMV per 8-row group below 64 rows, dequantised fp16 GEMM from 64
+    if (k.kind == kGemm && w->n < kGemmMinColumns)
+      k.kind = kGemv;  // narrow Q4_K outputs: the GEMV per 8-row group at every row count
     k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + type_name(w->type) + "_k" + std::to_string(w->k) + "_n" +
              std::to_string(w->n) + "_" + suffix[phase] +
              (k.kind == kGemm ? "_mfma32x32x16" : other && phase == Q4K_PHASE_PREFILL ? "_fp16_gemm" : "_mfma16x16x32");
@@ -322,104 +332,76 @@ Workspace& workspace(int device) {
   return g_ws[device & 63];
 }
 
-// Grows the device's staging buffers to `halves` fp16 values plus `rows` row scales.
-int ensure_workspace(Workspace& ws, int device, size_t halves, size_t rows) {
-  const size_t need = halves, need_s = rows < 64 ? 64 : rows;
-  if (ws.x_elems >= need && ws.scale_elems >= need_s)
-    return Q4K_OK;
-  if (ws.x_elems < need) {
-    if (ws.x)
-      ws.retired.push_back(ws.x);
-    ws.x = nullptr;
-    ws.x_elems = 0;
-    if (hipMalloc(&ws.x, need * sizeof(_Float16)) != hipSuccess)
-      return fail(Q4K_ENOMEM, "cannot allocate %zu-byte activation workspace on device %d", need * sizeof(_Float16), device);
-    ws.x_elems = need;
-  }
-  if (ws.scale_elems < need_s) {
-    if (ws.scale)
-      ws.retired.push_back(ws.scale);
-    ws.scale = nullptr;
-    ws.scale_elems = 0;
-    if (hipMalloc(&ws.scale, need_s * sizeof(float)) != hipSuccess)
-      return fail(Q4K_ENOMEM, "cannot allocate row-scale workspace on device %d", device);
-    ws.scale_elems = need_s;
+// Device allocation for workspace growth.  hipMalloc is not allowed while a
+// stream captures a graph, and a failure there would look like a lack of
+// memory: a call on a capturing stream that needs more workspace than the
+// device already holds fails with Q4K_ECAPTURE instead, before allocating.
+int ws_alloc(hipStream_t stream, int device, void** p, size_t bytes, const char* what) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone)
+    return fail(Q4K_ECAPTURE,
+                "the %s must grow to %zu bytes on device %d, but the stream is capturing a graph and allocation is not allowed "
+                "there: make one call of this shape (or a larger one) before the capture",
+                what, bytes, device);
+  if (hipMalloc(p, bytes) != hipSuccess) {
+    *p = nullptr;
+    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte %s on device %d", bytes, what, device);
   }
   return Q4K_OK;
 }
 
-// Split-K buffers.  Counters are zeroed once when allocated; every launch
-// leaves them zero again.
-int ensure_splitk_workspace(Workspace& ws, int device, size_t part_floats, size_t groups) {
-  if (ws.part_elems < part_floats) {
-    if (ws.part)
-      ws.retired.push_back(ws.part);
-    ws.part = nullptr;
-    ws.part_elems = 0;
-    if (hipMalloc(&ws.part, part_floats * sizeof(float)) != hipSuccess)
-      return fail(Q4K_ENOMEM, "cannot allocate %zu-byte split-K workspace on device %d", part_floats * sizeof(float), device);
-    ws.part_elems = part_floats;
-  }
-  if (ws.counter_elems < groups) {
-    const size_t n = groups < 1024 ? 1024 : groups;
-    if (ws.counters)
-      ws.retired.push_back(ws.counters);
-    ws.counters = nullptr;
-    ws.counter_elems = 0;
-    if (hipMalloc(&ws.counters, n * sizeof(int)) != hipSuccess)
-      return fail(Q4K_ENOMEM, "cannot allocate split-K counters on device %d", device);
-    Q4K_TRY_HIP(hipMemset(ws.counters, 0, n * sizeof(int)), "hipMemset");
-    ws.counter_elems = n;
-  }
-  return Q4K_OK;
-}
-
-// Grow-only device buffer (retired buffers stay allocated: a captured graph
-// may still name them).
+// Grow-only device buffer (outgrown buffers are retired, not freed: a graph
+// captured earlier may still name them).
 template <typename T>
-int ensure_buffer(Workspace& ws, int device, T*& buf, size_t& have, size_t need, const char* what) {
+int ensure_buffer(hipStream_t stream, Workspace& ws, int device, T*& buf, size_t& have, size_t need, const char* what) {
   if (have >= need)
     return Q4K_OK;
+  void* p = nullptr;
+  int rc = ws_alloc(stream, device, &p, need * sizeof(T), what);
+  if (rc)
+    return rc;
   if (buf)
     ws.retired.push_back(buf);
-  buf = nullptr;
-  have = 0;
-  if (hipMalloc(&buf, need * sizeof(T)) != hipSuccess)
-    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte %s on device %d", need * sizeof(T), what, device);
+  buf = static_cast<T*>(p);
   have = need;
   return Q4K_OK;
 }
 
-int ensure_normed_workspace(Workspace& ws, int device, size_t bytes) {
-  if (ws.normed_bytes >= bytes)
-    return Q4K_OK;
-  if (ws.normed)
-    ws.retired.push_back(ws.normed);
-  ws.normed = nullptr;
-  ws.normed_bytes = 0;
-  if (hipMalloc(&ws.normed, bytes) != hipSuccess)
-    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte normalised-activation buffer on device %d", bytes, device);
-  ws.normed_bytes = bytes;
-  return Q4K_OK;
+// Grows the device's staging buffers to `halves` fp16 values plus `rows` row scales.
+int ensure_workspace(hipStream_t stream, Workspace& ws, int device, size_t halves, size_t rows) {
+  int rc = ensure_buffer(stream, ws, device, ws.x, ws.x_elems, halves, "activation workspace");
+  if (!rc)
+    rc = ensure_buffer(stream, ws, device, ws.scale, ws.scale_elems, rows < 64 ? 64 : rows, "row-scale workspace");
+  return rc;
 }
 
-int ensure_pack_workspace(Workspace& ws, int device, size_t bytes) {
-  if (ws.pack_bytes >= bytes)
-    return Q4K_OK;
-  if (ws.pack)
-    ws.retired.push_back(ws.pack);
-  ws.pack = nullptr;
-  ws.pack_bytes = 0;
-  if (hipMalloc(&ws.pack, bytes) != hipSuccess)
-    return fail(Q4K_ENOMEM, "cannot allocate %zu-byte decode pack on device %d", bytes, device);
-  ws.pack_bytes = bytes;
+// Split-K buffers.  New counters are zeroed once (synchronously, outside any
+// capture: growth is refused there); every launch leaves them zero again.
+int ensure_splitk_workspace(hipStream_t stream, Workspace& ws, int device, size_t part_floats, size_t groups) {
+  int rc = ensure_buffer(stream, ws, device, ws.part, ws.part_elems, part_floats, "split-K workspace");
+  if (rc || ws.counter_elems >= groups)
+    return rc;
+  const size_t n = groups < 1024 ? 1024 : groups;
+  int* c = nullptr;
+  rc = ws_alloc(stream, device, reinterpret_cast<void**>(&c), n * sizeof(int), "split-K counter array");
+  if (rc)
+    return rc;
+  hipError_t e = hipMemset(c, 0, n * sizeof(int));
+  if (e != hipSuccess) {
+    (void)hipFree(c);
+    return hip_fail(e, "hipMemset");
+  }
+  if (ws.counters)
+    ws.retired.push_back(ws.counters);
+  ws.counters = c;
+  ws.counter_elems = n;
   return Q4K_OK;
 }
 
 // Packs x (m <= 8 rows) for the per-item and persistent GEMVs.
 int stage_pack(hipStream_t stream, Workspace& ws, int device, const void* x, uint32_t dtype, uint32_t m, uint32_t k, DecodePack* pk) {
   const size_t nb = k / 256;
-  int rc = ensure_pack_workspace(ws, device, nb * kPackBytesPerBlock);
+  int rc = ensure_buffer(stream, ws, device, ws.pack, ws.pack_bytes, nb * kPackBytesPerBlock, "decode pack");
   if (rc)
     return rc;
   pk->frag = reinterpret_cast<u4_t*>(ws.pack);
@@ -483,8 +465,8 @@ int set_device(int device) {
 // same (m, k, n) under the same lock; the decode pack and split-K paths always
 // stage (they are not reached by such pairs).
 // Projection with weights of a type other than Q4_K (wu == nullptr): up to 63
-// rows, per group of up to 8 rows, the decode pack of the group's x, then the
-// type's GEMV over the group's rows of y and aux; from 64 rows the GEMM above.
+// rows the GEMV per 8-row group (run_gemv_groups_locked); from 64 rows the
+// GEMM below.
 constexpr uint32_t kTypedGemmRows = 64;
 // Prefill-sized batches with the other types (m >= 64): x staged as fp16 rows
 // with power-of-two row scales, the weights dequantised to fp16 [n, k] (the
@@ -493,13 +475,17 @@ constexpr uint32_t kTypedGemmRows = 64;
 int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
                           uint32_t dtype) {
   const size_t n = w->n, k = w->k;
-  int rc = ensure_workspace(ws, w->device, (size_t)m * k, m);
+  int rc = ensure_workspace(stream, ws, w->device, (size_t)m * k, m);
   if (!rc)
-    rc = ensure_buffer(ws, w->device, ws.wdq, ws.wdq_elems, n * k, "dequantised-weight workspace");
+    rc = ensure_buffer(stream, ws, w->device, ws.wdq, ws.wdq_elems, n * k, "dequantised-weight workspace");
   if (!rc)
-    rc = ensure_buffer(ws, w->device, ws.cbuf, ws.cbuf_elems, (size_t)m * n, "GEMM result workspace");
+    rc = ensure_buffer(stream, ws, w->device, ws.cbuf, ws.cbuf_elems, (size_t)m * n, "GEMM result workspace");
   if (rc)
     return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (!ws.blas && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+    return fail(Q4K_ECAPTURE, "the library GEMM handle of device %d is created on first use, which allocates: make one call before the capture",
+                w->device);
   if (!ws.blas && rocblas_create_handle(&ws.blas) != rocblas_status_success) {
     ws.blas = nullptr;
     return fail(Q4K_EHIP, "rocblas_create_handle failed on device %d", w->device);
@@ -528,10 +514,11 @@ int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, cons
   return Q4K_OK;
 }
 
-int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
-                   uint32_t dtype) {
-  if (m >= kTypedGemmRows)
-    return run_typed_gemm_locked(stream, ws, w, x, y, aux, m, post, dtype);
+// Per group of up to 8 rows: the decode pack of the group's x (hi/lo fp16,
+// per-(row, block) power-of-two scale), then the weight type's GEMV over the
+// group's rows of y and aux.
+int run_gemv_groups_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
+                           uint32_t dtype) {
   const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
   for (uint32_t r0 = 0; r0 < m; r0 += 8) {
     const uint32_t mg = m - r0 < 8u ? m - r0 : 8u;
@@ -557,6 +544,13 @@ int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const voi
   return Q4K_OK;
 }
 
+int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
+                     uint32_t dtype) {
+  if (m >= kTypedGemmRows)
+    return run_typed_gemm_locked(stream, ws, w, x, y, aux, m, post, dtype);
+  return run_gemv_groups_locked(stream, ws, w, x, y, aux, m, post, dtype);
+}
+
 int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m,
                       uint32_t post, uint32_t dtype, uint32_t phase, bool restage) {
   if (w->type != Q4K_GGML_TYPE_Q4_K) {
@@ -568,6 +562,8 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
   Kernel& kern = resolve(w, phase);
   if (wu)
     resolve(wu, phase);
+  if (!wu && w->n < kGemmMinColumns && m > kGemvSplitRows)
+    return run_gemv_groups_locked(stream, ws, w, x, y, aux, m, post, dtype);
   const bool gemv = kern.kind != kGemm || m <= 16u * kGemvMaxRowTiles;
   const bool split = gemv && gemv_split((int)m);
   const int rows = split ? 2 * (int)m : (int)m;
@@ -575,7 +571,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
   if (gemv && gemv_splitk_plan((int)m, (int)w->n, (int)(w->k / 256), wu != nullptr, device_cus(w->device), &plan)) {
     // Split-K GEMV: each workgroup packs its own K-slice of x; partials in
     // the workspace.
-    int rc = ensure_splitk_workspace(ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
+    int rc = ensure_splitk_workspace(stream, ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
     if (rc)
       return rc;
     GemvArgs a{};
@@ -638,7 +634,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
   const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : gemm2 ? (size_t)gemm2_rows((int)m) : m;
   // xs is read 32 lanes at a time from its start; +128 halves of slack.
   const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : 0;
-  int rc = ensure_workspace(ws, w->device, ws_rows * w->k + xs_halves, ws_rows);
+  int rc = ensure_workspace(stream, ws, w->device, ws_rows * w->k + xs_halves, ws_rows);
   if (rc)
     return rc;
   _Float16* xs = ws.x + ws_rows * w->k;
@@ -1019,7 +1015,7 @@ int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const 
     Workspace& ws = workspace(wg->device);
     {
       std::lock_guard<std::mutex> lock(ws.mu);
-      rc = ensure_normed_workspace(ws, wg->device, xb);
+      rc = ensure_buffer(s, ws, wg->device, ws.normed, ws.normed_bytes, xb, "normalised-activation buffer");
     }
     if (rc)
       return rc;

@@ -431,9 +431,9 @@ hipError_t launch_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint
 bool q4k_persistent_supported(int m, int nb, int n, int cus);
 hipError_t launch_q4k_persistent(hipStream_t s, const GemvArgs& a, int dtype, int cus);
 
-// GEMV of the other GGUF types for m <= 8 rows: a.w = tiled weights of ggml
-// type `type` (Q6_K, Q8_0, Q5_K or IQ4_XS), a.pack = the decode pack of x
-// (launch_stage_pack), post 0/1/2 on a.y / a.aux.
+// GEMV for m <= 8 rows over the decode pack of x (launch_stage_pack): a.w =
+// tiled weights of ggml type `type` (Q4_K, Q6_K, Q8_0, Q5_K or IQ4_XS),
+// post 0/1/2 on a.y / a.aux.
 hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus);
 
 // Prefill with the other types: their weights dequantised to fp16 [n, k]

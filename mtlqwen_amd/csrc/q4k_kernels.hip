@@ -1469,9 +1469,9 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
 //    one barrier per u-step.
 //  - B: each wave streams the tile-blocks of its 4 column tiles through a
 //    private 2-block LDS ring (one block ahead) and dequantises in
-//    registers to h(h(d*sc) * q - h(dmin*m)) (the reference's prefill tile
-//    value, quant_linear.metal:43,45, with the two products rounded first)
-//    with packed fp16 operations.
+//    registers to h(h(d*sc) * q - h(dmin*m)) with packed fp16 operations
+//    (the reference's prefill tile value, quant_linear.metal:43,45, rounds
+//    the fp32 expression once; here the two products are rounded first).
 // Loads: per u-step a wave issues its 4 fragments of A(t + 4) and, at the
 // first u-step of a block, the 4 tile-blocks (12 loads) of the next block,
 // one fragment (and one tile-block) per column group so that the load
@@ -1581,7 +1581,14 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     pchi[c] = (as_h2(p1 | 0x64006400u) + k1024) * dd;
   };
   // B fragments of column tile c from its two raw words (words 2(u & 1),
-  // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants.
+  // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants:
+  // h(h(d * sc) * q - h(dmin * m)), one v_pk_fma_f16 per pair of weights.
+  // (The reference rounds d * sc * q - dmin * m once, formed in fp32,
+  // quant_linear.metal:43,45.  Here that costs one v_fma_mix per weight
+  // instead of one v_pk_fma_f16 per pair: a third more vector work per MFMA
+  // for a wave that issues its dequantisation between its MFMAs, measured
+  // 12-15 % slower.  Rounding the two products first adds at most 2^-12
+  // relative error to each before the final rounding.)
   // The nibble masks and the fp16 bias live in registers (VOP3 takes no
   // literal on this target), as plain values so that the scheduler sees the
   // v_and_or_b32 it selects as vector ALU work and interleaves it.
@@ -2771,6 +2778,8 @@ hipError_t launch_q4k_persistent(hipStream_t s, const GemvArgs& a, int dtype, in
 
 hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus) {
   switch (type) {
+    case kTypeQ4_K:
+      return typed_gemv_dispatch<FmtQ4K>(s, a, dtype, cus);
     case kTypeQ6_K:
       return typed_gemv_dispatch<FmtQ6K>(s, a, dtype, cus);
     case kTypeQ8_0:

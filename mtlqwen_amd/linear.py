@@ -32,9 +32,12 @@ def _dtype_code(t):
     raise TypeError(f"activations must be float32 or float16, got {t.dtype}")
 
 
-def _stream(stream):
+def _stream(stream, device=None):
+    """The stream handle to launch on: ``stream`` if given, else the current
+    stream of ``device`` (the weight's device; the current device if None)."""
     if stream is None:
-        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        dev = None if device is None else torch.device("cuda", device)
+        return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     if isinstance(stream, torch.cuda.Stream):
         return ctypes.c_void_p(stream.cuda_stream)
     return ctypes.c_void_p(stream)
@@ -48,6 +51,21 @@ def _ptr(t):
     if not t.is_contiguous():
         raise ValueError("tensors passed to the Q4_K path must be contiguous")
     return ctypes.c_void_p(t.data_ptr())
+
+
+def _check_tensor(t, numel, what, device=None):
+    """The C ABI takes raw pointers: a tensor must hold at least ``numel``
+    elements (and sit on ``device``) before its address is handed over, so a
+    mis-sized buffer is a ValueError here rather than an out-of-bounds access
+    on the GPU."""
+    if t is None:
+        return
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{what} must be a GPU tensor")
+    if device is not None and t.device.index != device:
+        raise ValueError(f"{what} is on cuda:{t.device.index}, the weights on cuda:{device}")
+    if t.numel() < numel:
+        raise ValueError(f"{what} holds {t.numel()} elements, needs {numel}")
 
 
 class Weight:
@@ -64,7 +82,7 @@ class Weight:
             if data.dtype != torch.uint8 or not data.is_contiguous():
                 raise ValueError("device weight bytes must be a contiguous uint8 tensor")
             rc = lib.q4k_weight_create_from_device(ctypes.c_void_p(data.data_ptr()), data.numel(), n, k, ggml_type,
-                                                   device, _stream(None), ctypes.byref(handle))
+                                                   device, _stream(None, device), ctypes.byref(handle))
         else:
             buf = np.ascontiguousarray(np.frombuffer(memoryview(data).cast("B"), dtype=np.uint8)
                                        if not isinstance(data, np.ndarray) else data.view(np.uint8).reshape(-1))
@@ -147,17 +165,24 @@ def linear(x, w, count, output, auxiliary=None, gated=False, query_counts=None, 
     dt = _dtype_code(x)
     if output.dtype != x.dtype or (auxiliary is not None and auxiliary.dtype != x.dtype):
         raise TypeError("x, output and auxiliary must share a dtype")
+    _check_tensor(x, count * w.k, "x", w.device)
+    _check_tensor(output, count * w.n, "output", w.device)
+    _check_tensor(auxiliary, count * w.n, "auxiliary", w.device)
     post = POST_GATE if gated else (POST_ADD if auxiliary is not None else POST_STORE)
     counts, nq = u32_array(query_counts if query_counts is not None else [count])
-    check(lib.q4k_linear(_stream(stream), w.handle, _ptr(x), _ptr(output), _ptr(auxiliary), count, counts, nq, post, dt))
+    check(lib.q4k_linear(_stream(stream, w.device), w.handle, _ptr(x), _ptr(output), _ptr(auxiliary), count, counts, nq, post, dt))
     return output
 
 
 def mlp_gate_up(x, gate, up, count, output, query_counts=None, stream=None):
     """silu(x . gate^T) * (x . up^T) into ``output`` (the gate buffer)."""
     dt = _dtype_code(x)
+    if output.dtype != x.dtype:
+        raise TypeError("x and output must share a dtype")
+    _check_tensor(x, count * gate.k, "x", gate.device)
+    _check_tensor(output, count * gate.n, "output", gate.device)
     counts, nq = u32_array(query_counts if query_counts is not None else [count])
-    check(lib.q4k_mlp_gate_up(_stream(stream), gate.handle, up.handle, _ptr(x), _ptr(output), count, counts, nq, dt))
+    check(lib.q4k_mlp_gate_up(_stream(stream, gate.device), gate.handle, up.handle, _ptr(x), _ptr(output), count, counts, nq, dt))
     return output
 
 
@@ -168,10 +193,16 @@ def mlp(x, gate, up, down, hidden, gate_buffer, count, query_counts=None, stream
     ``x`` may be ``hidden`` (the decoder passes the residual stream and
     the layer's ffn_norm)."""
     dt = _dtype_code(x)
+    if gate_buffer.dtype != x.dtype or hidden.dtype != x.dtype:
+        raise TypeError("x, gate_buffer and hidden must share a dtype")
+    _check_tensor(x, count * gate.k, "x", gate.device)
+    _check_tensor(gate_buffer, count * gate.n, "gate_buffer", gate.device)
+    _check_tensor(hidden, count * down.n, "hidden", gate.device)
     counts, nq = u32_array(query_counts if query_counts is not None else [count])
     if norm_weight is not None:
-        _check_norm_weight(norm_weight, x.shape[-1])
-    check(lib.q4k_mlp(_stream(stream), gate.handle, up.handle, down.handle, _ptr(norm_weight), float(eps), _ptr(x),
+        _check_norm_weight(norm_weight, gate.k)
+        _check_tensor(norm_weight, gate.k, "norm_weight", gate.device)
+    check(lib.q4k_mlp(_stream(stream, gate.device), gate.handle, up.handle, down.handle, _ptr(norm_weight), float(eps), _ptr(x),
                       _ptr(gate_buffer), _ptr(hidden), count, counts, nq, dt))
     return hidden
 
@@ -179,10 +210,15 @@ def mlp(x, gate, up, down, hidden, gate_buffer, count, query_counts=None, stream
 def gather_rows(x, out, counts, samples, stream=None):
     """LM-head row gather (native_ops.metal:12-15): returns the gathered row count."""
     dt = _dtype_code(x)
+    if out.dtype != x.dtype:
+        raise TypeError("x and out must share a dtype")
+    k = x.shape[-1]
+    _check_tensor(x, sum(counts) * k, "x")
+    _check_tensor(out, sum(samples) * k, "out", x.device.index)
     c, nq = u32_array(counts)
     s, _ = u32_array(samples)
     rows = ctypes.c_uint32()
-    check(lib.q4k_gather_rows(_stream(stream), _ptr(x), _ptr(out), x.shape[-1], c, s, nq, dt, ctypes.byref(rows)))
+    check(lib.q4k_gather_rows(_stream(stream, x.device.index), _ptr(x), _ptr(out), k, c, s, nq, dt, ctypes.byref(rows)))
     return rows.value
 
 
@@ -195,7 +231,9 @@ def embedding(table, ids, y, stream=None):
     rows = ids.numel()
     if y.shape[0] < rows or y.numel() < rows * table.k:
         raise ValueError("y must hold len(ids) rows of table.k values")
-    check(lib.q4k_embedding(_stream(stream), table.handle, _ptr(ids), rows, _ptr(y), _dtype_code(y)))
+    _check_tensor(ids, rows, "ids", table.device)
+    _check_tensor(y, rows * table.k, "y", table.device)
+    check(lib.q4k_embedding(_stream(stream, table.device), table.handle, _ptr(ids), rows, _ptr(y), _dtype_code(y)))
     return y
 
 
@@ -203,8 +241,12 @@ def rms_norm(x, weight, y, eps=1e-6, stream=None):
     """RMS norm of every row of ``x`` (native_ops.metal:6-40) with fp32
     ``weight`` [k]; ``y`` may be ``x``."""
     _check_norm_weight(weight, x.shape[-1])
+    if y.dtype != x.dtype:
+        raise TypeError("x and y must share a dtype")
     m = x.numel() // x.shape[-1]
-    check(lib.q4k_rms_norm(_stream(stream), _ptr(x), _ptr(weight), _ptr(y), m, x.shape[-1], float(eps), _dtype_code(x)))
+    _check_tensor(weight, x.shape[-1], "weight", x.device.index)
+    _check_tensor(y, x.numel(), "y", x.device.index)
+    check(lib.q4k_rms_norm(_stream(stream, x.device.index), _ptr(x), _ptr(weight), _ptr(y), m, x.shape[-1], float(eps), _dtype_code(x)))
     return y
 
 
@@ -212,10 +254,16 @@ def rms_norm_gather(x, weight, out, counts, samples, eps=1e-6, stream=None):
     """LM-head rms_norm_gather (native_ops.metal:6-40, forward.cpp:72-75):
     the rows gather_rows selects, RMS-normalised; returns their count."""
     _check_norm_weight(weight, x.shape[-1])
+    if out.dtype != x.dtype:
+        raise TypeError("x and out must share a dtype")
+    k = x.shape[-1]
+    _check_tensor(x, sum(counts) * k, "x")
+    _check_tensor(weight, k, "weight", x.device.index)
+    _check_tensor(out, sum(samples) * k, "out", x.device.index)
     c, nq = u32_array(counts)
     s, _ = u32_array(samples)
     rows = ctypes.c_uint32()
-    check(lib.q4k_rms_norm_gather(_stream(stream), _ptr(x), _ptr(weight), _ptr(out), x.shape[-1], c, s, nq, float(eps),
+    check(lib.q4k_rms_norm_gather(_stream(stream, x.device.index), _ptr(x), _ptr(weight), _ptr(out), k, c, s, nq, float(eps),
                                   _dtype_code(x), ctypes.byref(rows)))
     return rows.value
 
@@ -242,7 +290,7 @@ def mfma_ceiling(device=0, iters=20000, stream=None):
     """Measured fp16 MFMA rate of the device in TFLOP/s (a loop of the GEMM's
     MFMA instruction on every CU); synchronises the stream."""
     t = ctypes.c_double()
-    check(lib.q4k_mfma_ceiling(_stream(stream), int(device), int(iters), ctypes.byref(t)))
+    check(lib.q4k_mfma_ceiling(_stream(stream, int(device)), int(device), int(iters), ctypes.byref(t)))
     return t.value
 
 

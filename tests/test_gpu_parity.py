@@ -2,9 +2,13 @@
 
 Bar: max over output rows of ||y - ref|| / ||ref|| <= 1e-3,
 ref = the oracle's fp32-accumulated Q4_K dequant-dot on the same inputs.
-The GEMV rounds activations to fp16 (row-scaled, weights exact); the GEMM
-also rounds dequantised weights to fp16 as the reference's prefill tiles do
-(quant_linear.metal:43,45).  Expected error is ~3e-4 and ~4e-4 respectively.
+The GEMV carries activations as hi/lo fp16 pairs (row-scaled, weights exact:
+errors near 1e-6) up to 24 rows, and single fp16 rows from 25 to 48.  The
+GEMM (256 or more output columns) rounds activations to fp16 and the
+dequantised weights to h(h(d*sc)*q - h(dmin*m)) (the reference's prefill
+tiles round d*sc*q - dmin*m once, quant_linear.metal:43,45): a numpy model of
+these roundings puts the worst row near 7.5e-4 at these shapes (6.8e-4 with
+the reference's rounding).  Narrower prefill outputs take the GEMV.
 """
 import numpy as np
 import pytest
@@ -66,8 +70,10 @@ def test_gemv_f16(q4k, oracle, gpu, m, post):
     _run(q4k, oracle, gpu, 300 + m, m, 256, 1024, post=post, dtype=torch.float16, xscale=0.25)
 
 
-GEMM_SHAPES = [(49, 64, 256), (64, 128, 512), (65, 144, 768), (128, 256, 1024), (129, 80, 512), (300, 4096, 4096),
-               (821, 6144, 4096), (257, 4096, 12288)]
+# (49, 64, 256) .. (129, 80, 512): narrow outputs (the GEMV per 8-row group);
+# (130, 272, 1024), (77, 400, 512): the 128 x 128 GEMM (N not a multiple of 256).
+GEMM_SHAPES = [(49, 64, 256), (64, 128, 512), (65, 144, 768), (128, 256, 1024), (129, 80, 512), (130, 272, 1024), (77, 400, 512),
+               (300, 4096, 4096), (821, 6144, 4096), (257, 4096, 12288)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
@@ -75,21 +81,16 @@ def test_gemm_store(q4k, oracle, gpu, m, n, k):
     _run(q4k, oracle, gpu, 400 + m, m, n, k)
 
 
-def test_gemm_tiny_outputs(q4k, oracle, gpu):
-    """N=16, K=256: with 16 outputs per row the per-row norm ratio of the
-    GEMM's fp16 operand rounding (~4e-4 on average) fluctuates past 1e-3 on
-    some rows (a numpy model of the same roundings gives 1.3e-3 here), so this
-    shape is held to the bar over the whole output instead."""
-    rng = np.random.default_rng(429)
-    m, n, k = 129, 16, 256
-    w = make_q4k(rng, n, k)
-    x = make_x(rng, m, k)
-    W = q4k.Weight(w, n, k)
-    y = torch.empty((m, n), device=gpu)
-    q4k.linear(_t(x, gpu), W, m, y)
-    torch.cuda.synchronize()
-    ref = oracle.linear(x, w, n, k)
-    assert row_rel_err(y.cpu().numpy().reshape(1, -1), ref.reshape(1, -1)) <= TOL
+@pytest.mark.parametrize("seed", [429, 430, 431])
+@pytest.mark.parametrize("m,n,k", [(129, 16, 256), (300, 128, 512), (49, 240, 1024)])
+def test_gemm_tiny_outputs(q4k, oracle, gpu, seed, m, n, k):
+    """Prefill with fewer than 256 output columns, per-row bar.  With 16
+    outputs a row's error has little to average over: fp16 activations and
+    weights (the GEMM's operands) put a numpy model of seed 429 at 1.4e-3, so
+    these shapes run the hi/lo GEMV per 8-row group, whose weights are exact."""
+    W, err = _run(q4k, oracle, gpu, seed, m, n, k)
+    assert "mfma16x16x32" in W.kernel_name(1)
+    assert err <= 1e-5
 
 
 @pytest.mark.parametrize("post", [1, 2])
@@ -250,8 +251,8 @@ def test_gemm_eight_row_staging(q4k, oracle, gpu, m, k, dtype):
     """m >= 2048 stages x eight rows per workgroup: in registers with 32
     threads per row for K <= 4096, with 64 threads per row for K a multiple
     of 512 up to 12288, in two passes over x otherwise (K = 4352: 17 blocks).
-    A ragged last workgroup (rows past m) and fp16 input; rows are checked on
-    a subset that includes the last ones."""
+    A ragged last workgroup (rows past m) and fp16 input; every row is
+    compared with the oracle and the whole output must be finite."""
     n = 256
     rng = np.random.default_rng(2000 + k)
     w = make_q4k(rng, n, k)
@@ -262,10 +263,9 @@ def test_gemm_eight_row_staging(q4k, oracle, gpu, m, k, dtype):
     y = torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
     q4k.linear(_t(x, gpu, dtype), W, m, y, query_counts=[m])
     torch.cuda.synchronize()
-    rows = np.concatenate([np.arange(8), np.random.default_rng(3).choice(m, 40, replace=False), np.arange(m - 8, m)])
-    got = y.float().cpu().numpy()[rows]
+    got = y.float().cpu().numpy()
     assert np.all(np.isfinite(got))
-    assert row_rel_err(got, oracle.linear(x[rows], w, n, k)) <= TOL
+    assert row_rel_err(got, oracle.linear(x, w, n, k)) <= TOL
 
 
 def test_mfma_ceiling(q4k, gpu):
