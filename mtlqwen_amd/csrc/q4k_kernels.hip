@@ -1469,9 +1469,8 @@ __global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
 //    one barrier per u-step.
 //  - B: each wave streams the tile-blocks of its 4 column tiles through a
 //    private 2-block LDS ring (one block ahead) and dequantises in
-//    registers to h(h(d*sc) * q - h(dmin*m)) with packed fp16 operations
-//    (the reference's prefill tile value, quant_linear.metal:43,45, rounds
-//    the fp32 expression once; here the two products are rounded first).
+//    registers to h(d*sc*q - dmin*m), the fp32 expression rounded to fp16
+//    once (the reference's prefill tile value, quant_linear.metal:43,45).
 // Loads: per u-step a wave issues its 4 fragments of A(t + 4) and, at the
 // first u-step of a block, the 4 tile-blocks (12 loads) of the next block,
 // one fragment (and one tile-block) per column group so that the load
@@ -1564,47 +1563,53 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     lds_dma4<kHeaderOffset>(src, voff4, l);
   };
 
-  // Block constants of the 4 column tiles: h(d * sc), -h(dmin * m) of
-  // sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles), from the 4
-  // headers (this lane's column) of one block.
-  // Kept as packed pairs (h(d * sc), h(dmin * m)): the 6-bit fields become
-  // exact fp16 through the 1024 bias, and one v_pk_mul_f16 by the header's
-  // (d, dmin) word rounds each product once, as the fp32 product (exact for
-  // 11 x 6 bits) converted to fp16 would.
-  h2_t pclo[4], pchi[4];
+  // Block constants of the 4 column tiles, in fp32, from the 4 headers (this
+  // lane's column) of one block: for sub-block 2g (low nibbles) d * sc and
+  // -(1024 d * sc + dmin * m), for sub-block 2g + 1 (high nibbles) d * sc and
+  // -(64 d * sc + dmin * m).  d * sc and dmin * m are exact in fp32 (11-bit d
+  // times a 6-bit field).
+  float dsl[4], csl[4], dsh[4], csh[4];
   auto block_const = [&](int c, const u4_t& hd) {
     uint32_t p0, p1;
     scale_min_packed(hd, g, p0, p1);
-    const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const h2_t dd = as_h2(hd.x);
-    pclo[c] = (as_h2(p0 | 0x64006400u) + k1024) * dd;
-    pchi[c] = (as_h2(p1 | 0x64006400u) + k1024) * dd;
+    const float d = half_bits_to_float(hd.x & 0xffffu), dmin = half_bits_to_float(hd.x >> 16);
+    dsl[c] = d * (float)(p0 & 0xffu);
+    csl[c] = __builtin_fmaf(-1024.0f, dsl[c], -dmin * (float)((p0 >> 16) & 0xffu));
+    dsh[c] = d * (float)(p1 & 0xffu);
+    csh[c] = __builtin_fmaf(-64.0f, dsh[c], -dmin * (float)((p1 >> 16) & 0xffu));
   };
   // B fragments of column tile c from its two raw words (words 2(u & 1),
-  // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants:
-  // h(h(d * sc) * q - h(dmin * m)), one v_pk_fma_f16 per pair of weights.
-  // (The reference rounds d * sc * q - dmin * m once, formed in fp32,
-  // quant_linear.metal:43,45.  Here that costs one v_fma_mix per weight
-  // instead of one v_pk_fma_f16 per pair: a third more vector work per MFMA
-  // for a wave that issues its dequantisation between its MFMAs, measured
-  // 12-15 % slower.  Rounding the two products first adds at most 2^-12
-  // relative error to each before the final rounding.)
-  // The nibble masks and the fp16 bias live in registers (VOP3 takes no
-  // literal on this target), as plain values so that the scheduler sees the
+  // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants: the
+  // reference's prefill tile value h(d * sc * q - dmin * m), formed in fp32
+  // and rounded to fp16 once (quant_linear.metal:43,45).  (w & 0x000F000F) |
+  // 0x6400 is the fp16 value 1024 + q of two low nibbles, (w & 0x00F000F0) |
+  // 0x5400 the value 64 + q of two high nibbles; one v_fma_mix_f32 per weight
+  // then forms (B + q) * d * sc - (B d * sc + dmin * m) with the product exact
+  // and one rounding to fp32, and one v_cvt_pk_f16_f32 per pair rounds to
+  // fp16.  The bias B rides in the fp32 constant, so no instruction removes
+  // it; the constant itself is rounded to fp32 when B d * sc and dmin * m
+  // span more than 24 bits, which moves about 0.8 % of the weights by one
+  // fp16 ulp against the reference's value (numpy model of the benchmark's
+  // weights).  The empty asm keeps the fp32 results apart from the
+  // conversion: fused, they become v_fma_mixlo/mixhi_f16 pairs writing the
+  // two halves of one register, a dependent chain that measured 6 % slower.
+  // The nibble masks and biases live in registers (VOP3 takes no literal on
+  // this target), as plain values so that the scheduler sees the
   // v_and_or_b32 it selects as vector ALU work and interleaves it.
-  uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, m_bias = 0x64006400u;
-  asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(m_bias));
+  uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, b_lo = 0x64006400u, b_hi = 0x54005400u;
+  asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(b_lo), "+v"(b_hi));
   auto dequant_words = [&](int c, uint2 wv, h8_t& blo, h8_t& bhi) {
-    const h2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const h2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f}, k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
     const uint32_t lw[4] = {wv.x, wv.x >> 8, wv.y, wv.y >> 8};
     u4_t lo, hi;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const h2_t ql = as_h2((lw[e] & m_lo) | m_bias) + k1024;
-      const h2_t qh = __builtin_elementwise_fma(as_h2((lw[e] & m_hi) | m_bias), k16, k64);
-      lo[e] = as_u32(__builtin_elementwise_fma(ql, h2_t{pclo[c][0], pclo[c][0]}, h2_t{-pclo[c][1], -pclo[c][1]}));
-      hi[e] = as_u32(__builtin_elementwise_fma(qh, h2_t{pchi[c][0], pchi[c][0]}, h2_t{-pchi[c][1], -pchi[c][1]}));
+      const h2_t ql = as_h2((lw[e] & m_lo) | b_lo);
+      const h2_t qh = as_h2((lw[e] & m_hi) | b_hi);
+      float a0 = __builtin_fmaf((float)ql[0], dsl[c], csl[c]), a1 = __builtin_fmaf((float)ql[1], dsl[c], csl[c]);
+      float b0 = __builtin_fmaf((float)qh[0], dsh[c], csh[c]), b1 = __builtin_fmaf((float)qh[1], dsh[c], csh[c]);
+      asm("" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
+      lo[e] = as_u32(h2_t{(_Float16)a0, (_Float16)a1});
+      hi[e] = as_u32(h2_t{(_Float16)b0, (_Float16)b1});
     }
     blo = __builtin_bit_cast(h8_t, lo);
     bhi = __builtin_bit_cast(h8_t, hi);

@@ -124,8 +124,10 @@ def test_config4_long_prefill(q4k, oracle, gpu):
     rows = np.unique(np.concatenate([16 * tiles + tiles % 16, np.arange(0, m, 128), np.arange(127, m, 128), np.arange(m - 8, m)]))
     g_gpu = gate.cpu().numpy()
     assert np.all(np.isfinite(g_gpu)) and np.all(np.isfinite(out.cpu().numpy()))
-    assert row_rel_err(g_gpu[rows], oracle.mlp_gate_up(x[rows], wg, wu, 12288, 4096)) <= TOL
-    assert row_rel_err(out.cpu().numpy()[rows], oracle.linear(g_gpu[rows], wd, 4096, 12288)) <= TOL
+    err_g = row_rel_err(g_gpu[rows], oracle.mlp_gate_up(x[rows], wg, wu, 12288, 4096))
+    err_d = row_rel_err(out.cpu().numpy()[rows], oracle.linear(g_gpu[rows], wd, 4096, 12288))
+    print(f"config4: gated {err_g:.3e} down {err_d:.3e} over {len(rows)} rows")
+    assert err_g <= TOL and err_d <= TOL
     # Linearity over every row of the full-size gate projection.
     xa = acts(44, m, 4096)
     xb = x - xa

@@ -5,10 +5,9 @@ ref = the oracle's fp32-accumulated Q4_K dequant-dot on the same inputs.
 The GEMV carries activations as hi/lo fp16 pairs (row-scaled, weights exact:
 errors near 1e-6) up to 24 rows, and single fp16 rows from 25 to 48.  The
 GEMM (256 or more output columns) rounds activations to fp16 and the
-dequantised weights to h(h(d*sc)*q - h(dmin*m)) (the reference's prefill
-tiles round d*sc*q - dmin*m once, quant_linear.metal:43,45): a numpy model of
-these roundings puts the worst row near 7.5e-4 at these shapes (6.8e-4 with
-the reference's rounding).  Narrower prefill outputs take the GEMV.
+dequantised weights to h(d*sc*q - dmin*m) as the reference's prefill tiles do
+(quant_linear.metal:43,45): a numpy model of these roundings puts the worst
+row near 7e-4 at these shapes.  Narrower prefill outputs take the GEMV.
 """
 import numpy as np
 import pytest
