@@ -115,6 +115,25 @@ int q4k_weight_prepare(q4k_weight* w, uint32_t phase);
 int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts,
                uint32_t nqueries, uint32_t post, uint32_t dtype);
 
+/* q4k_linear for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference, whose kernels allocate nothing; here the
+ * staging, split-K partials and counters of q4k_linear normally live in a
+ * workspace that grows on demand.  Same arguments, selection, kernels and
+ * results as q4k_linear, but the workspace is a fixed 64 MiB device array
+ * that each GPU the library runs on holds until the process ends: 2 MiB of
+ * decode pack (m <= 8, k <= 61440), 8 MiB of split-K partials, 4096 split-K
+ * counters, 65536 row scales, and about 54 MiB of staged activations (e.g.
+ * m * k <= 28.1 million for prefill, rows padded to 128).  A call needing
+ * more fails with Q4K_ESHAPE and a message naming the buffer; prefill of 64
+ * or more rows with weights other than Q4_K (a library GEMM) fails with
+ * Q4K_ETYPE.  Calls allocate nothing (no hipMalloc, hipFree or allocating
+ * library routine).  Every call on a GPU shares that GPU's array and leaves
+ * its contents behind: calls that overlap on one GPU (other streams or
+ * threads) race; issue them in one stream order. */
+int q4k_linear_noalloc(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts,
+                       uint32_t nqueries, uint32_t post, uint32_t dtype);
+
 /* Gated MLP projection (model/qwen35/forward.cpp:115-118).
  * Decode passes: one fused gate/up kernel, y = silu(x.Wg^T) * (x.Wu^T)
  * (fused_kernels.metal:44-78).  Other passes: the reference's two calls,

@@ -89,6 +89,9 @@ struct Workspace {
   size_t cbuf_elems = 0;
   rocblas_handle blas = nullptr;
   std::vector<void*> retired;
+  // Fixed-size buffers in the no-allocation scratch: never grown; a call
+  // that needs more fails (ensure_buffer).
+  bool fixed = false;
 };
 
 Workspace g_ws[64];
@@ -356,6 +359,9 @@ template <typename T>
 int ensure_buffer(hipStream_t stream, Workspace& ws, int device, T*& buf, size_t& have, size_t need, const char* what) {
   if (have >= need)
     return Q4K_OK;
+  if (ws.fixed)
+    return fail(Q4K_ESHAPE, "this call needs %zu bytes of %s; the no-allocation scratch of device %d holds %zu (q4k_linear_noalloc)",
+                need * sizeof(T), what, device, have * sizeof(T));
   void* p = nullptr;
   int rc = ws_alloc(stream, device, &p, need * sizeof(T), what);
   if (rc)
@@ -381,6 +387,9 @@ int ensure_splitk_workspace(hipStream_t stream, Workspace& ws, int device, size_
   int rc = ensure_buffer(stream, ws, device, ws.part, ws.part_elems, part_floats, "split-K workspace");
   if (rc || ws.counter_elems >= groups)
     return rc;
+  if (ws.fixed)
+    return fail(Q4K_ESHAPE, "this call needs %zu split-K counters; the no-allocation scratch of device %d holds %zu", groups, device,
+                ws.counter_elems);
   const size_t n = groups < 1024 ? 1024 : groups;
   int* c = nullptr;
   rc = ws_alloc(stream, device, reinterpret_cast<void**>(&c), n * sizeof(int), "split-K counter array");
@@ -475,6 +484,9 @@ constexpr uint32_t kTypedGemmRows = 64;
 int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
                           uint32_t dtype) {
   const size_t n = w->n, k = w->k;
+  if (ws.fixed)
+    return fail(Q4K_ETYPE, "q4k_linear_noalloc does not serve %u-row prefill with %s weights (their prefill GEMM is a library call that may allocate)",
+                m, type_name(w->type));
   int rc = ensure_workspace(stream, ws, w->device, (size_t)m * k, m);
   if (!rc)
     rc = ensure_buffer(stream, ws, w->device, ws.wdq, ws.wdq_elems, n * k, "dequantised-weight workspace");
@@ -574,6 +586,8 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     int rc = ensure_splitk_workspace(stream, ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
     if (rc)
       return rc;
+    if (ws.fixed)  // the scratch's counters start at zero for this launch (a fill kernel: capture-safe)
+      Q4K_TRY_HIP(launch_fill_u32(stream, reinterpret_cast<uint32_t*>(ws.counters), 0u, (uint32_t)plan.groups), "counter fill launch");
     GemvArgs a{};
     a.w = w->data;
     a.wu = wu ? wu->data : w->data;
@@ -884,8 +898,14 @@ int q4k_select_phase(const uint32_t* query_counts, uint32_t nqueries, uint32_t m
   return Q4K_OK;
 }
 
-int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts, uint32_t nqueries,
-               uint32_t post, uint32_t dtype) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks of q4k_linear / q4k_linear_noalloc; *phase receives the
+// batch's phase.
+int check_linear(const q4k_weight* w, const void* x, const void* y, const void* aux, uint32_t m, const uint32_t* query_counts,
+                 uint32_t nqueries, uint32_t post, uint32_t dtype, uint32_t* phase) {
   if (!w)
     return fail(Q4K_EINVAL, "weight is NULL");
   if (dtype > Q4K_DTYPE_F16)
@@ -906,9 +926,98 @@ int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* 
     return fail(Q4K_EALIAS, "x must not overlap y");
   if (aux && aux != y && overlaps(aux, (size_t)m * w->n * es, y, (size_t)m * w->n * es))
     return fail(Q4K_EALIAS, "aux must be y itself or disjoint from it");
-  const uint32_t phase = phase_of(query_counts, nqueries, m, false);
-  if (phase != Q4K_PHASE_PREFILL && m > 16u * kGemvMaxRowTiles)
+  *phase = phase_of(query_counts, nqueries, m, false);
+  if (*phase != Q4K_PHASE_PREFILL && m > 16u * kGemvMaxRowTiles)
     return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
+  return Q4K_OK;
+}
+
+// ---- the no-allocation entry point (q4k_linear_noalloc) -------------------
+// Its workspace lives in `scratch`, a file-scope device array that every GPU
+// the library runs on holds until the process ends.  In host code the name
+// `scratch` is a host-side stand-in, not a device address: the device
+// address of each GPU's copy comes from hipGetSymbolAddress, taken once per
+// device at that device's first call (with the device current), and only
+// that address is used (kernel arguments, fills).
+constexpr size_t kScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Fixed regions of the scratch: decode pack, split-K partials and counters,
+// row scales; the rest holds the staged activations.
+constexpr size_t kScrPackBytes = 2ull << 20;
+constexpr size_t kScrPartBytes = 8ull << 20;
+constexpr size_t kScrCounterBytes = 16ull << 10;
+constexpr size_t kScrScaleBytes = 256ull << 10;
+constexpr size_t kScrXBytes = kScratchBytes - kScrPackBytes - kScrPartBytes - kScrCounterBytes - kScrScaleBytes;
+
+struct ScratchWorkspace {
+  Workspace ws;
+  bool ready = false;
+};
+ScratchWorkspace g_scratch[64];
+std::mutex g_scratch_setup;
+
+// The device's scratch workspace, set up on first use (device current).
+int scratch_workspace(int device, Workspace** out) {
+  ScratchWorkspace& sw = g_scratch[device & 63];
+  std::lock_guard<std::mutex> lock(g_scratch_setup);
+  if (!sw.ready) {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+      return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr)
+      return fail(Q4K_EHIP, "hipGetSymbolAddress(scratch) returned no address on device %d", device);
+    uint8_t* b = static_cast<uint8_t*>(ptr);
+    Workspace& ws = sw.ws;
+    ws.fixed = true;
+    ws.pack = b;
+    ws.pack_bytes = kScrPackBytes;
+    b += kScrPackBytes;
+    ws.part = reinterpret_cast<float*>(b);
+    ws.part_elems = kScrPartBytes / sizeof(float);
+    b += kScrPartBytes;
+    ws.counters = reinterpret_cast<int*>(b);
+    ws.counter_elems = kScrCounterBytes / sizeof(int);
+    b += kScrCounterBytes;
+    ws.scale = reinterpret_cast<float*>(b);
+    ws.scale_elems = kScrScaleBytes / sizeof(float);
+    b += kScrScaleBytes;
+    ws.x = reinterpret_cast<_Float16*>(b);
+    ws.x_elems = kScrXBytes / sizeof(_Float16);
+    sw.ready = true;
+  }
+  *out = &sw.ws;
+  return Q4K_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q4k_linear_noalloc(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts,
+                       uint32_t nqueries, uint32_t post, uint32_t dtype) {
+  uint32_t phase = 0;
+  int rc = check_linear(w, x, y, aux, m, query_counts, nqueries, post, dtype, &phase);
+  if (rc)
+    return rc;
+  rc = set_device(w->device);
+  if (rc)
+    return rc;
+  Workspace* ws = nullptr;
+  rc = scratch_workspace(w->device, &ws);
+  if (rc)
+    return rc;
+  std::lock_guard<std::mutex> lock(ws->mu);
+  return run_linear_locked(static_cast<hipStream_t>(stream), *ws, w, nullptr, x, y, aux, m, post, dtype, phase, true);
+}
+
+int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts, uint32_t nqueries,
+               uint32_t post, uint32_t dtype) {
+  uint32_t phase = 0;
+  int rc = check_linear(w, x, y, aux, m, query_counts, nqueries, post, dtype, &phase);
+  if (rc)
+    return rc;
   rc = set_device(w->device);
   if (rc)
     return rc;

@@ -415,6 +415,10 @@ hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters)
 
 hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx);
 
+// p[0, n) = v on stream s (a kernel, so that graph capture records a kernel
+// node rather than a memset).
+hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t v, uint32_t n);
+
 // Token embedding from a tiled Q4_K table (n rows of k): y[t] = row ids[t].
 hipError_t launch_embedding(hipStream_t s, const uint8_t* w, const int32_t* ids, void* y, int rows, int n, int k, int dtype);
 

@@ -1814,6 +1814,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   out[(size_t)blockIdx.x * 256 + threadIdx.x] = sum;
 }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, uint32_t n) {
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256)
+    p[i] = v;
+}
+
 // ----------------------------------------------------------------------------
 // Row gather and device re-layout.
 // ----------------------------------------------------------------------------
@@ -2680,6 +2685,14 @@ hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype) {
     (void)dispatch(q4k_gemm_kernel<float>, grid, block, s, a);
   else
     (void)dispatch(q4k_gemm_kernel<_Float16>, grid, block, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t v, uint32_t n) {
+  if (n == 0)
+    return hipSuccess;
+  const unsigned grid = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  (void)dispatch(fill_u32_kernel, dim3(grid), dim3(256), s, p, v, n);
   return hipGetLastError();
 }
 

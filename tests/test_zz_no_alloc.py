@@ -1,0 +1,68 @@
+"""q4k_linear_noalloc (the entry point that allocates nothing) against
+q4k_linear through the C ABI: the same kernels on the same inputs, so the
+outputs must be identical, on two calls in a row (the second smaller) for
+every kernel family the entry point reaches; and its refusals."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from q4k_ref import make_q4k, make_weight, make_x, TYPE_Q6_K
+
+pytestmark = pytest.mark.gpu
+
+
+def _noalloc(q4k, x, w, m, y, aux=None, post=0, counts=None):
+    counts = counts if counts is not None else [m]
+    arr = (ctypes.c_uint32 * len(counts))(*counts)
+    dt = q4k.DTYPE_F16 if x.dtype == torch.float16 else q4k.DTYPE_F32
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return q4k.lib.q4k_linear_noalloc(stream, w.handle, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
+                                      None if aux is None else ctypes.c_void_p(aux.data_ptr()), m, arr, len(counts), post, dt)
+
+
+# (label, n, k, first (m, counts), second (m, counts), post, dtype)
+CASES = [
+    ("split-K down (K=12288)", 4096, 12288, (8, [1] * 8), (3, [1] * 3), 1, torch.float32),
+    ("persistent GEMV (wide N)", 65536, 4096, (8, [1] * 8), (2, [1] * 2), 0, torch.float32),
+    ("staged GEMV (40 rows)", 4096, 4096, (40, [5] * 8), (20, [5] * 4), 0, torch.float32),
+    ("prefill GEMM", 4096, 4096, (300, [300]), (129, [129]), 2, torch.float32),
+    ("narrow prefill (GEMV groups)", 128, 1024, (100, [100]), (30, [30]), 0, torch.float32),
+    ("fp16 prefill GEMM", 512, 2048, (200, [200]), (70, [70]), 1, torch.float16),
+    ("fp16 decode GEMV", 1024, 2048, (8, [1] * 8), (5, [1] * 5), 0, torch.float16),
+]
+
+
+@pytest.mark.parametrize("label,n,k,first,second,post,dtype", CASES, ids=[c[0] for c in CASES])
+def test_noalloc_matches_linear(q4k, gpu, label, n, k, first, second, post, dtype):
+    rng = np.random.default_rng(1300 + n % 97 + k % 89)
+    W = q4k.Weight(make_q4k(rng, n, k), n, k)
+    for m, counts in (first, second):
+        x = torch.from_numpy(make_x(rng, m, k, 0.25)).to(gpu).to(dtype)
+        aux0 = torch.from_numpy(make_x(rng, m, n, 0.5)).to(gpu).to(dtype) if post else None
+        y_ref = aux0.clone() if post else torch.empty((m, n), device=gpu, dtype=dtype)
+        q4k.linear(x, W, m, y_ref, auxiliary=y_ref if post else None, gated=(post == 2), query_counts=counts)
+        y = aux0.clone() if post else torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+        rc = _noalloc(q4k, x, W, m, y, aux=y if post else None, post=post, counts=counts)
+        assert rc == 0, q4k.lib.q4k_last_error().decode()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"{label} m={m}"
+
+
+def test_noalloc_refusals(q4k, gpu):
+    rng = np.random.default_rng(1310)
+    # Staging 8192 x 8192 activations exceeds the scratch.
+    n, k, m = 256, 8192, 8192
+    W = q4k.Weight(make_q4k(rng, n, k), n, k)
+    x = torch.zeros((m, k), device=gpu)
+    y = torch.zeros((m, n), device=gpu)
+    rc = _noalloc(q4k, x, W, m, y)
+    assert rc == -3
+    assert "no-allocation scratch" in q4k.lib.q4k_last_error().decode()
+    # Prefill of 64+ rows with another type is a library GEMM: refused.
+    n, k, m = 256, 1024, 64
+    W6 = q4k.Weight(make_weight(rng, n, k, TYPE_Q6_K), n, k, ggml_type=TYPE_Q6_K)
+    rc = _noalloc(q4k, torch.zeros((m, k), device=gpu), W6, m, torch.zeros((m, n), device=gpu))
+    assert rc == -2 and "noalloc" in q4k.lib.q4k_last_error().decode()
+    torch.cuda.synchronize()
