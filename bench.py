@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-types", action="store_true", help="skip the Q8_0 / Q5_K / IQ4_XS LM-head timings")
+    ap.add_argument("--part", default="all",
+                    choices=["all", "decode", "prefill", "config2", "config3", "lm_head", "types", "shard", "neighbours"],
+                    help="run one workload alone (for profiling runs that attribute kernel statistics to one configuration)")
     return ap.parse_args()
 
 
@@ -260,7 +263,7 @@ def neighbours_bench(args, dev):
     return out
 
 
-def configs_bench(dev):
+def configs_bench(dev, parts=("config2", "config3"), sets=3):
     """Benchmark configurations 2 and 3, each as one HIP graph of
     its projections (random Q4_K weights as in config 0, seeded fp32
     activations), timed over replays:
@@ -287,9 +290,6 @@ def configs_bench(dev):
         return q4k.Weight(raw.reshape(-1), n, k)
 
     K, F = 4096, 12288
-    qkv, o, gw, uw, dw = weight(6144, K), weight(K, K), weight(F, K), weight(F, K), weight(K, F)
-    head = weight(248320, K)
-    norm_w = torch.rand(K, device=dev, generator=g) + 0.5
     out = {}
     reps = 20
 
@@ -306,27 +306,41 @@ def configs_bench(dev):
         torch.cuda.synchronize()
         return timed_graph(graph, 5) / (5 * reps)
 
-    # config 2
-    M = 40
-    counts = [5] * 8
-    x = torch.randn((M, K), device=dev, generator=g)
-    hidden = torch.randn((M, K), device=dev, generator=g)
-    yq = torch.empty((M, 6144), device=dev)
-    gate = torch.empty((M, F), device=dev)
+    if "config2" in parts:
+        # config 2, weights rotating over `sets` copies (118 MB each: more
+        # than the 256 MB memory-side cache for sets >= 3)
+        wsets = [(weight(6144, K), weight(K, K), weight(F, K), weight(F, K), weight(K, F)) for _ in range(sets)]
+        M = 40
+        counts = [5] * 8
+        x = torch.randn((M, K), device=dev, generator=g)
+        hidden = torch.randn((M, K), device=dev, generator=g)
+        yq = torch.empty((M, 6144), device=dev)
+        gate = torch.empty((M, F), device=dev)
+        turn = [0]
 
-    def pass2():
-        q4k.linear(x, qkv, M, yq, query_counts=counts)
-        q4k.linear(x, o, M, hidden, auxiliary=hidden, query_counts=counts)
-        q4k.mlp(x, gw, uw, dw, hidden, gate, M, query_counts=counts)
+        def pass2():
+            qkv, o, gw, uw, dw = wsets[turn[0] % len(wsets)]
+            turn[0] += 1
+            q4k.linear(x, qkv, M, yq, query_counts=counts)
+            q4k.linear(x, o, M, hidden, auxiliary=hidden, query_counts=counts)
+            q4k.mlp(x, gw, uw, dw, hidden, gate, M, query_counts=counts)
 
-    dt = run(pass2)
-    wbytes = (6144 + K + 2 * F) * (K // 256) * 144 + K * (F // 256) * 144
-    abytes = 4 * M * (3 * K + 6144 + 2 * K + 2 * F + 2 * K)
-    out["config2"] = {"workload": "M=40 (8 x 5 tokens, decode phase): QKV 4096->6144, O 4096->4096 + residual, MLP 4096->12288x2->4096 + residual",
-                      "us_per_pass": round(dt * 1e6, 2), "bytes": wbytes + abytes, "gbs": round((wbytes + abytes) / dt / 1e9, 1),
-                      "frac_of_8tbs": round((wbytes + abytes) / dt / 8e12, 3)}
+        dt = run(pass2)
+        wbytes = (6144 + K + 2 * F) * (K // 256) * 144 + K * (F // 256) * 144
+        abytes = 4 * M * (3 * K + 6144 + 2 * K + 2 * F + 2 * K)
+        out["config2"] = {"workload": "M=40 (8 x 5 tokens, decode phase): QKV 4096->6144, O 4096->4096 + residual, MLP 4096->12288x2->4096 + residual",
+                          "weight_sets": len(wsets), "us_per_pass": round(dt * 1e6, 2), "bytes": wbytes + abytes,
+                          "gbs": round((wbytes + abytes) / dt / 1e9, 1), "frac_of_8tbs": round((wbytes + abytes) / dt / 8e12, 3),
+                          "kernels": {"qkv": wsets[0][0].kernel_name(0), "gate_up": wsets[0][2].kernel_name(3), "down": wsets[0][4].kernel_name(0)}}
+        del wsets
+        torch.cuda.empty_cache()
+    if "config3" not in parts:
+        return out
 
     # config 3
+    qkv, o, gw, uw, dw = weight(6144, K), weight(K, K), weight(F, K), weight(F, K), weight(K, F)
+    head = weight(248320, K)
+    norm_w = torch.rand(K, device=dev, generator=g) + 0.5
     lengths = [512, 37, 1, 1, 200, 5, 1, 64]
     M = sum(lengths)
     x = torch.randn((M, K), device=dev, generator=g)
@@ -619,14 +633,33 @@ def main():
     import mtlqwen_amd  # fails loudly if libq4k.so is missing
     dev = torch.device("cuda:0")
 
+    want = (lambda p: args.part in ("all", p))
+    if args.part != "all" and args.part != "decode":
+        # one workload alone (profiling runs); printed as its own JSON line
+        res = {"part": args.part}
+        if args.part == "prefill":
+            res["prefill"] = prefill_bench(args, dev)
+        elif args.part in ("config2", "config3"):
+            res.update(configs_bench(dev, parts=(args.part,), sets=args.sets if args.part == "config2" else 1))
+        elif args.part == "lm_head":
+            res["q4k_lm_head"], res["q6k_lm_head"] = lm_head_bench(dev, 12), lm_head_bench(dev, 14)
+        elif args.part == "types":
+            res["types_lm_head"] = types_bench(args, dev)
+        elif args.part == "shard":
+            res["shard_1of8"] = shard_bench(args, dev)
+        elif args.part == "neighbours":
+            res["neighbours"] = neighbours_bench(args, dev)
+        print(json.dumps(res), flush=True)
+        return
+
     dec = decode_bench(args, dev)
-    pre = None if args.no_prefill else prefill_bench(args, dev)
-    shard = shard_bench(args, dev)
-    neighbours = neighbours_bench(args, dev)
-    cfgs = configs_bench(dev)
-    q4k_head = lm_head_bench(dev, 12)
-    q6k = lm_head_bench(dev, 14)
-    types = None if args.no_types else types_bench(args, dev)
+    pre = None if args.no_prefill or not want("prefill") else prefill_bench(args, dev)
+    shard = shard_bench(args, dev) if want("shard") else None
+    neighbours = neighbours_bench(args, dev) if want("neighbours") else None
+    cfgs = configs_bench(dev, sets=min(args.sets, 3)) if want("config2") else None
+    q4k_head = lm_head_bench(dev, 12) if want("lm_head") else None
+    q6k = lm_head_bench(dev, 14) if want("lm_head") else None
+    types = None if args.no_types or not want("types") else types_bench(args, dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
@@ -695,6 +728,7 @@ def main():
                 "peak": FP16_DENSE_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(pre["gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4),
+                "traffic": profiled_traffic("gemm2_config4_traffic.txt"),
                 "avg_us": round(pre["gemm_avg_us"], 2),
             },
         }

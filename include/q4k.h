@@ -115,6 +115,17 @@ int q4k_weight_prepare(q4k_weight* w, uint32_t phase);
 int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts,
                uint32_t nqueries, uint32_t post, uint32_t dtype);
 
+/* The projection of an RMS-normalised input: y = post(rms_norm(x, norm_w,
+ * eps) . W^T, aux), rms_norm as native_ops.metal:6-40 (x * rsqrt(sum(x^2) /
+ * k + eps) * norm_w, norm_w k fp32 values), the pair the decoder runs for the
+ * attention input (forward.cpp:82 attn_norm, then the QKV projections
+ * :86-87, :99).  The norm is folded into the activation staging of the
+ * selected kernel (decode GEMV, prefill GEMM); paths that pack x inside the
+ * GEMV (split-K, the wide persistent GEMV) normalise into the workspace
+ * first.  Arguments otherwise as q4k_linear; aux must not be x. */
+int q4k_linear_norm(void* stream, q4k_weight* w, const float* norm_w, float eps, const void* x, void* y, const void* aux, uint32_t m,
+                    const uint32_t* query_counts, uint32_t nqueries, uint32_t post, uint32_t dtype);
+
 /* q4k_linear for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference, whose kernels allocate nothing; here the
@@ -147,10 +158,12 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
  *   gate = silu(xn.Wg^T) * (xn.Wu^T)        [m, n]  (the gate buffer)
  *   hidden = hidden + gate.Wd^T              [m, k]  (post 1, in place)
  * with wg, wu n x k, wd k x n and norm_w k fp32 values (or NULL).  The
- * decoder passes x = hidden with the layer's ffn_norm; for decode passes
- * that the fused gate/up GEMV takes (m <= 8, k = 4096) the norm runs inside
- * it, otherwise into a workspace buffer first.  The gate buffer must not
- * overlap x or hidden; x may equal hidden. */
+ * decoder passes x = hidden with the layer's ffn_norm; the norm runs inside
+ * the fused gate/up GEMV (decode, m <= 8, k = 4096) or inside the activation
+ * staging that the gate and up projections share (prefill GEMM, other
+ * decode GEMVs); only paths that pack x inside the GEMV normalise into a
+ * workspace buffer first.  The gate buffer must not overlap x or hidden; x
+ * may equal hidden. */
 int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const float* norm_w, float eps, const void* x, void* gate, void* hidden,
             uint32_t m, const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype);
 

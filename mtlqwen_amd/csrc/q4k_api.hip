@@ -482,7 +482,7 @@ constexpr uint32_t kTypedGemmRows = 64;
 // reference's prefill tile values), one rocBLAS GEMM with fp32 accumulation
 // and output, then the epilogue (row unscale, post 0/1/2, fp16 rounding).
 int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
-                          uint32_t dtype) {
+                          uint32_t dtype, const float* norm_w, float eps) {
   const size_t n = w->n, k = w->k;
   if (ws.fixed)
     return fail(Q4K_ETYPE, "q4k_linear_noalloc does not serve %u-row prefill with %s weights (their prefill GEMM is a library call that may allocate)",
@@ -504,7 +504,7 @@ int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, cons
   }
   {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
-    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, nullptr, ws.scale, (int)m, (int)k, kStageRowMajor), "stage_x launch");
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, nullptr, ws.scale, (int)m, (int)k, kStageRowMajor, norm_w, eps), "stage_x launch");
   }
   {
     LaunchTimer timer(stream, Q4K_KERNEL_AUX);
@@ -523,6 +523,25 @@ int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, cons
     return fail(Q4K_EHIP, "rocblas_gemm_ex failed (%d)", (int)st);
   LaunchTimer timer(stream, Q4K_KERNEL_AUX);
   Q4K_TRY_HIP(launch_gemm_post(stream, ws.cbuf, ws.scale, y, aux, (int)m, (int)n, (int)post, (int)dtype), "gemm epilogue launch");
+  return Q4K_OK;
+}
+
+// A path that packs x itself (split-K, decode pack) cannot fold a row's RMS
+// norm into its staging: with a norm weight, x is normalised into the
+// workspace first (one rms_norm launch, native_ops.metal:6-40) and the path
+// reads that copy.
+int prenorm(hipStream_t stream, Workspace& ws, int device, const void*& x, const float*& norm_w, float eps, uint32_t m, uint32_t k,
+            uint32_t dtype) {
+  if (!norm_w)
+    return Q4K_OK;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  int rc = ensure_buffer(stream, ws, device, ws.normed, ws.normed_bytes, (size_t)m * k * es, "normalised-activation buffer");
+  if (rc)
+    return rc;
+  LaunchTimer timer(stream, Q4K_KERNEL_AUX);
+  Q4K_TRY_HIP(launch_rms_norm(stream, x, norm_w, ws.normed, (int)m, (int)k, eps, (int)dtype, nullptr), "rms_norm launch");
+  x = ws.normed;
+  norm_w = nullptr;
   return Q4K_OK;
 }
 
@@ -557,25 +576,34 @@ int run_gemv_groups_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, con
 }
 
 int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
-                     uint32_t dtype) {
+                     uint32_t dtype, const float* norm_w, float eps) {
   if (m >= kTypedGemmRows)
-    return run_typed_gemm_locked(stream, ws, w, x, y, aux, m, post, dtype);
+    return run_typed_gemm_locked(stream, ws, w, x, y, aux, m, post, dtype, norm_w, eps);
+  int rc = prenorm(stream, ws, w->device, x, norm_w, eps, m, w->k, dtype);
+  if (rc)
+    return rc;
   return run_gemv_groups_locked(stream, ws, w, x, y, aux, m, post, dtype);
 }
 
+// norm_w != nullptr: the projection of rms_norm(x, norm_w) (forward.cpp:82,
+// 114), folded into the activation staging where the path stages x.
 int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m,
-                      uint32_t post, uint32_t dtype, uint32_t phase, bool restage) {
+                      uint32_t post, uint32_t dtype, uint32_t phase, bool restage, const float* norm_w = nullptr, float eps = 0.0f) {
   if (w->type != Q4K_GGML_TYPE_Q4_K) {
     if (wu)
       return fail(Q4K_ETYPE, "the fused gate/up kernel takes Q4_K weights");
     resolve(w, phase);
-    return run_typed_locked(stream, ws, w, x, y, aux, m, post, dtype);
+    return run_typed_locked(stream, ws, w, x, y, aux, m, post, dtype, norm_w, eps);
   }
   Kernel& kern = resolve(w, phase);
   if (wu)
     resolve(wu, phase);
-  if (!wu && w->n < kGemmMinColumns && m > kGemvSplitRows)
+  if (!wu && w->n < kGemmMinColumns && m > kGemvSplitRows) {
+    int rc = prenorm(stream, ws, w->device, x, norm_w, eps, m, w->k, dtype);
+    if (rc)
+      return rc;
     return run_gemv_groups_locked(stream, ws, w, x, y, aux, m, post, dtype);
+  }
   const bool gemv = kern.kind != kGemm || m <= 16u * kGemvMaxRowTiles;
   const bool split = gemv && gemv_split((int)m);
   const int rows = split ? 2 * (int)m : (int)m;
@@ -583,7 +611,9 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
   if (gemv && gemv_splitk_plan((int)m, (int)w->n, (int)(w->k / 256), wu != nullptr, device_cus(w->device), &plan)) {
     // Split-K GEMV: each workgroup packs its own K-slice of x; partials in
     // the workspace.
-    int rc = ensure_splitk_workspace(stream, ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
+    int rc = prenorm(stream, ws, w->device, x, norm_w, eps, m, w->k, dtype);
+    if (!rc)
+      rc = ensure_splitk_workspace(stream, ws, w->device, gemv_splitk_part_floats(plan), (size_t)plan.groups);
     if (rc)
       return rc;
     if (ws.fixed)  // the scratch's counters start at zero for this launch (a fill kernel: capture-safe)
@@ -618,6 +648,8 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.nb = (int)(w->k / 256);
     a.rows = 2 * (int)m;
     a.split = 1;
+    a.norm_w = norm_w;
+    a.eps = eps;
     LaunchTimer timer(stream, Q4K_KERNEL_GEMV_GATED);
     Q4K_TRY_HIP(launch_gemv_gate_up(stream, a, (int)dtype, device_cus(w->device)), "gemv gate/up launch");
     return Q4K_OK;
@@ -626,7 +658,9 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     // Wide plain projections (the LM head): the persistent GEMV, x fragments
     // resident in registers.
     GemvArgs a{};
-    int rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);
+    int rc = prenorm(stream, ws, w->device, x, norm_w, eps, m, w->k, dtype);
+    if (!rc)
+      rc = stage_pack(stream, ws, w->device, x, dtype, m, w->k, &a.pack);
     if (rc)
       return rc;
     a.w = w->data;
@@ -655,7 +689,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
   if (restage) {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
     const int mode = gemm2 ? kStageGemm : !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
-    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode), "stage_x launch");
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode, norm_w, eps), "stage_x launch");
   }
   if (gemv) {
     GemvArgs a;
@@ -697,10 +731,10 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
 }
 
 int run_linear(hipStream_t stream, q4k_weight* w, q4k_weight* wu, const void* x, void* y, const void* aux, uint32_t m, uint32_t post, uint32_t dtype,
-               uint32_t phase) {
+               uint32_t phase, const float* norm_w = nullptr, float eps = 0.0f) {
   Workspace& ws = workspace(w->device);
   std::lock_guard<std::mutex> lock(ws.mu);
-  return run_linear_locked(stream, ws, w, wu, x, y, aux, m, post, dtype, phase, true);
+  return run_linear_locked(stream, ws, w, wu, x, y, aux, m, post, dtype, phase, true, norm_w, eps);
 }
 
 }  // namespace
@@ -1024,8 +1058,47 @@ int q4k_linear(void* stream, q4k_weight* w, const void* x, void* y, const void* 
   return run_linear(static_cast<hipStream_t>(stream), w, nullptr, x, y, aux, m, post, dtype, phase);
 }
 
+int q4k_linear_norm(void* stream, q4k_weight* w, const float* norm_w, float eps, const void* x, void* y, const void* aux, uint32_t m,
+                    const uint32_t* query_counts, uint32_t nqueries, uint32_t post, uint32_t dtype) {
+  if (!norm_w)
+    return fail(Q4K_EINVAL, "norm_w is NULL");
+  if (!(eps >= 0.0f))
+    return fail(Q4K_EINVAL, "eps must be a non-negative number");
+  uint32_t phase = 0;
+  int rc = check_linear(w, x, y, aux, m, query_counts, nqueries, post, dtype, &phase);
+  if (rc)
+    return rc;
+  if (aux && aux == x)
+    return fail(Q4K_EALIAS, "aux must not be x");
+  rc = set_device(w->device);
+  if (rc)
+    return rc;
+  return run_linear(static_cast<hipStream_t>(stream), w, nullptr, x, y, aux, m, post, dtype, phase, norm_w, eps);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The gated projection with an optional RMS norm of x (q4k_mlp's ffn_norm).
+int mlp_gate_up_impl(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x, void* y, uint32_t m, const uint32_t* query_counts,
+                     uint32_t nqueries, uint32_t dtype, const float* norm_w, float eps);
+
+}  // namespace
+
+extern "C" {
+
 int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x, void* y, uint32_t m, const uint32_t* query_counts,
                     uint32_t nqueries, uint32_t dtype) {
+  return mlp_gate_up_impl(stream, wg, wu, x, y, m, query_counts, nqueries, dtype, nullptr, 0.0f);
+}
+
+}  // extern "C"
+
+namespace {
+
+int mlp_gate_up_impl(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x, void* y, uint32_t m, const uint32_t* query_counts,
+                     uint32_t nqueries, uint32_t dtype, const float* norm_w, float eps) {
   if (!wg || !wu)
     return fail(Q4K_EINVAL, "gate and up weights must be non-NULL");
   if (wg->n != wu->n || wg->k != wu->k || wg->device != wu->device)
@@ -1051,18 +1124,22 @@ int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x,
   if (phase == Q4K_PHASE_GATED_DECODE && m > 16u * kGemvMaxRowTiles)
     return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
   if (phase == Q4K_PHASE_GATED_DECODE && q4)
-    return run_linear(s, wg, wu, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase);
+    return run_linear(s, wg, wu, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, norm_w, eps);
   // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in
-  // place.  Both read the same x: it is staged once, under one hold of the
-  // workspace lock.
+  // place.  Both read the same x: it is staged once (with the norm, if any),
+  // under one hold of the workspace lock.
   Workspace& ws = workspace(wg->device);
   std::lock_guard<std::mutex> lock(ws.mu);
-  rc = run_linear_locked(s, ws, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, true);
+  rc = run_linear_locked(s, ws, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, true, norm_w, eps);
   if (rc)
     return rc;
   // The Q4_K projection of a Q4_K pair reuses the staged x; other types pack their own.
-  return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, !q4);
+  return run_linear_locked(s, ws, wu, nullptr, x, y, y, m, Q4K_POST_GATE, dtype, phase, !q4, norm_w, eps);
 }
+
+}  // namespace
+
+extern "C" {
 
 int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const float* norm_w, float eps, const void* x, void* gate, void* hidden,
             uint32_t m, const uint32_t* query_counts, uint32_t nqueries, uint32_t dtype) {
@@ -1092,51 +1169,13 @@ int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const 
   rc = set_device(wg->device);
   if (rc)
     return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const uint32_t phase = phase_of(query_counts, nqueries, m, true);
-  const void* xin = x;
-  if (norm_w) {
-    if (phase == Q4K_PHASE_GATED_DECODE && wg->type == Q4K_GGML_TYPE_Q4_K && wu->type == Q4K_GGML_TYPE_Q4_K &&
-        gemv_gate_up_supported((int)m, (int)(wg->k / 256), (int)wg->n)) {
-      // The norm runs inside the fused gate/up GEMV (forward.cpp:114-118 in one launch).
-      resolve(wg, phase);
-      resolve(wu, phase);
-      GemvArgs a{};
-      a.w = wg->data;
-      a.wu = wu->data;
-      a.x = x;
-      a.y = gate;
-      a.m = (int)m;
-      a.n = (int)wg->n;
-      a.k = (int)wg->k;
-      a.nb = (int)(wg->k / 256);
-      a.rows = 2 * (int)m;
-      a.split = 1;
-      a.norm_w = norm_w;
-      a.eps = eps;
-      {
-        LaunchTimer timer(s, Q4K_KERNEL_GEMV_GATED);
-        Q4K_TRY_HIP(launch_gemv_gate_up(s, a, (int)dtype, device_cus(wg->device)), "gemv gate/up launch");
-      }
-      return q4k_linear(stream, wd, gate, hidden, hidden, m, query_counts, nqueries, Q4K_POST_ADD, dtype);
-    }
-    // Otherwise rms_norm (forward.cpp:114) into the workspace first.
-    Workspace& ws = workspace(wg->device);
-    {
-      std::lock_guard<std::mutex> lock(ws.mu);
-      rc = ensure_buffer(s, ws, wg->device, ws.normed, ws.normed_bytes, xb, "normalised-activation buffer");
-    }
-    if (rc)
-      return rc;
-    rc = q4k_rms_norm(stream, x, norm_w, ws.normed, m, wg->k, eps, dtype);
-    if (rc)
-      return rc;
-    xin = ws.normed;
-  }
-  // forward.cpp:115-119 as two calls: gate/up into the gate buffer, then down
-  // with the residual added in place.  (Stream order: the gate/up kernel has
-  // read all of x before the down projection writes hidden, so x may be hidden.)
-  rc = q4k_mlp_gate_up(stream, wg, wu, xin, gate, m, query_counts, nqueries, dtype);
+  // forward.cpp:114-119 as two calls: the ffn_norm (inside the fused gate/up
+  // GEMV for decode passes, folded into the activation staging of the
+  // gate/up projections otherwise) and gate/up into the gate buffer, then
+  // down with the residual added in place.  (Stream order: the gate/up
+  // launches have read all of x before the down projection writes hidden, so
+  // x may be hidden.)
+  rc = mlp_gate_up_impl(stream, wg, wu, x, gate, m, query_counts, nqueries, dtype, norm_w, eps);
   if (rc)
     return rc;
   return q4k_linear(stream, wd, gate, hidden, hidden, m, query_counts, nqueries, Q4K_POST_ADD, dtype);

@@ -357,7 +357,10 @@ enum StageMode : int {
 // is carried as hi = fp16(v) plus lo = fp16(v - hi), about 22 significant bits.
 // The fragment modes also write xs: each 32-element sub-block's sum of the
 // scaled values, divided by 32 (so it stays within fp16), hi/lo like x.
-hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode);
+// norm_w != nullptr: x is RMS-normalised on the way in, x * rsqrt(sum(x^2) /
+// k + eps) * norm_w (native_ops.metal:6-40), before the conversion.
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode,
+                          const float* norm_w = nullptr, float eps = 0.0f);
 hipError_t launch_stage_pack(hipStream_t s, const void* x, int dtype, const DecodePack& pk, int m, int k);
 
 // Halves of the sub-block-sum fragments for `rows` staged rows: per 16-row

@@ -181,6 +181,32 @@ __device__ __forceinline__ float block_max_256(float mx) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// Maximum of mx and sum of ss over the 256 threads (one barrier).
+__device__ __forceinline__ void block_max_sum_256(float& mx, float& ss) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off));
+    ss += __shfl_xor(ss, off);
+  }
+  __shared__ float red[2][4];
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = mx;
+    red[1][threadIdx.x >> 6] = ss;
+  }
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  ss = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+}
+
+// Fused RMS norm of a staged row (native_ops.metal:6-40): the staging
+// kernels multiply each element by its weight w[k] as it is read, sum the
+// squares of the unweighted elements, and fold rsqrt(sum / k + eps) into the
+// power-of-two conversion scale.
+struct RowNorm {
+  const float* w = nullptr;
+  float eps = 0.0f;
+};
+
 // Element offset of (row, 8-element chunk c) in the GEMV fragment layout:
 // fragment ((row / 16) * nb + b) * 8 + s holds, for lane 16g + (row % 16),
 // elements b*256 + 64g + 32*(s/4) + 8*(s%4) + [0, 8).
@@ -250,21 +276,51 @@ __device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row,
   }
 }
 
-template <typename InT, int MODE>
+// Loads chunk c (8 elements) of row xr; with NORM, multiplies each element by
+// its norm weight and adds the squares of the unweighted elements to ss.
+template <bool NORM, typename InT>
+__device__ __forceinline__ void load8_norm(const InT* xr, const float* nw, int c, float* v, float& ss) {
+  load8(xr + (size_t)c * 8, v);
+  if (NORM) {
+    float w8[8];
+    load8(nw + (size_t)c * 8, w8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ss = fmaf(v[i], v[i], ss);
+      v[i] *= w8[i];
+    }
+  }
+}
+
+// Power-of-two scale that puts a row's largest magnitude mx in [2^14, 2^15):
+// finite in fp16 with the full 11-bit significand for every large element.
+__device__ __forceinline__ void pow2_scale(float mx, float& up, float& down) {
+  up = 1.0f;
+  down = 1.0f;
+  if (mx > 0.0f && mx <= FLT_MAX) {
+    int e;
+    frexpf(mx, &e);
+    e = e < -80 ? -80 : e;
+    up = ldexpf(1.0f, 15 - e);
+    down = ldexpf(1.0f, e - 15);
+  }
+}
+
+template <typename InT, int MODE, bool NORM>
 __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, _Float16* __restrict__ xs,
-                                                      float* __restrict__ rowscale, int m, int k) {
+                                                      float* __restrict__ rowscale, int m, int k, RowNorm nrm) {
   const int row = blockIdx.x;
   const InT* xr = x + (size_t)row * k;
   const int chunks = k >> 3, nb = k >> 8;
   const bool in_regs = chunks <= 256 * kStageRegChunks;
   float v[kStageRegChunks][8] = {};
-  float mx = 0.0f;
+  float mx = 0.0f, ss = 0.0f;
   if (in_regs) {
 #pragma unroll
     for (int j = 0; j < kStageRegChunks; ++j) {
       const int c = threadIdx.x + 256 * j;
       if (c < chunks) {
-        load8(xr + c * 8, v[j]);
+        load8_norm<NORM>(xr, nrm.w, c, v[j], ss);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           mx = fmaxf(mx, fabsf(v[j][i]));
@@ -273,39 +329,40 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
   } else {
     for (int c = threadIdx.x; c < chunks; c += 256) {
       float t[8];
-      load8(xr + c * 8, t);
+      load8_norm<NORM>(xr, nrm.w, c, t, ss);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         mx = fmaxf(mx, fabsf(t[i]));
     }
   }
-  mx = block_max_256(mx);
-  // Scale the row so its largest magnitude lands in [2^14, 2^15): finite in
-  // fp16 with the full 11-bit significand for every large element.
-  float up = 1.0f, down = 1.0f;
-  if (mx > 0.0f && mx <= FLT_MAX) {
-    int e;
-    frexpf(mx, &e);
-    e = e < -80 ? -80 : e;
-    up = ldexpf(1.0f, 15 - e);
-    down = ldexpf(1.0f, e - 15);
+  float r = 1.0f;
+  if (NORM) {
+    block_max_sum_256(mx, ss);
+    r = 1.0f / sqrtf(ss / (float)k + nrm.eps);
+    mx *= r;
+  } else {
+    mx = block_max_256(mx);
   }
+  float up, down;
+  pow2_scale(mx, up, down);
   if (threadIdx.x == 0)
     rowscale[row] = down;
+  const float cs = NORM ? up * r : up;
   if (in_regs) {
 #pragma unroll
     for (int j = 0; j < kStageRegChunks; ++j) {
       const int c = threadIdx.x + 256 * j;
       if (256 * j < chunks)  // uniform: whole groups of 4 lanes take part
-        stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, v[j], up);
+        stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, v[j], cs);
     }
   } else {
     for (int c0 = 0; c0 < chunks; c0 += 256) {
       const int c = c0 + threadIdx.x;
       float t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float unused = 0.0f;
       if (c < chunks)
-        load8(xr + c * 8, t);
-      stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, t, up);
+        load8_norm<NORM>(xr, nrm.w, c, t, unused);
+      stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, t, cs);
     }
   }
 }
@@ -404,9 +461,24 @@ __device__ __forceinline__ void pack_block_row(const float (&v)[4], int r, int l
 // TPR threads per row (32, or 64 for long rows: 512 threads per workgroup).
 // CPT > 0: the row's K / (8 TPR) <= CPT chunks per thread stay in registers
 // between the maximum and the conversion; CPT == 0: x is read twice.
-template <typename InT, int CPT, int TPR = 32>
+// Reduction over the lanes of one staged row: lanes 0..31 and 32..63 of a
+// wave are two rows (TPR = 32), or the whole wave is one (TPR = 64).
+template <int TPR, bool MAX>
+__device__ __forceinline__ float row_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, dpp_f<kDppQuadSwap1>(v));
+  v = op(v, dpp_f<kDppQuadSwap2>(v));
+  v = op(v, dpp_f<kDppHalfMirror>(v));
+  v = op(v, dpp_f<kDppRowMirror>(v));
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return TPR == 64 ? op(op(r0, r1), op(r2, r3)) : (threadIdx.x & 63) < 32 ? op(r0, r1) : op(r2, r3);
+}
+
+template <typename InT, int CPT, int TPR, bool NORM>
 __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restrict__ x, _Float16* __restrict__ xo, float* __restrict__ rowscale,
-                                                             int m, int k) {
+                                                             int m, int k, RowNorm nrm) {
   static_assert(TPR == 32 || TPR == 64, "one row per half wave or per wave");
   const int t = threadIdx.x, q = t & (TPR - 1);
   const int row = blockIdx.x * 8 + t / TPR;
@@ -414,7 +486,7 @@ __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restri
   const int nb = k >> 8, cpt = (k >> 3) / TPR;
   const InT* xr = x + (size_t)(live ? row : 0) * k;
   float v[CPT > 0 ? CPT : 1][8];
-  float mx = 0.0f;
+  float mx = 0.0f, ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < (CPT > 0 ? CPT : 1); ++j)
 #pragma unroll
@@ -424,7 +496,7 @@ __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restri
 #pragma unroll
     for (int j = 0; j < CPT; ++j)
       if (live && j < cpt)
-        load8(xr + (size_t)(q + TPR * j) * 8, v[j]);
+        load8_norm<NORM>(xr, nrm.w, q + TPR * j, v[j], ss);
 #pragma unroll
     for (int j = 0; j < CPT; ++j)
 #pragma unroll
@@ -433,41 +505,30 @@ __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restri
   } else if (live) {
     for (int j = 0; j < cpt; ++j) {
       float w[8];
-      load8(xr + (size_t)(q + TPR * j) * 8, w);
+      load8_norm<NORM>(xr, nrm.w, q + TPR * j, w, ss);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         mx = fmaxf(mx, fabsf(w[i]));
     }
   }
-  // Row maximum: lanes 0..31 and 32..63 of a wave are two rows (TPR = 32),
-  // or the whole wave is one (TPR = 64).
-  mx = fmaxf(mx, dpp_f<kDppQuadSwap1>(mx));
-  mx = fmaxf(mx, dpp_f<kDppQuadSwap2>(mx));
-  mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
-  mx = fmaxf(mx, dpp_f<kDppRowMirror>(mx));
-  {
-    const int b = __builtin_bit_cast(int, mx);
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-    mx = TPR == 64 ? fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)) : (t & 63) < 32 ? fmaxf(r0, r1) : fmaxf(r2, r3);
+  mx = row_reduce<TPR, true>(mx);
+  float r = 1.0f;
+  if (NORM) {
+    r = 1.0f / sqrtf(row_reduce<TPR, false>(ss) / (float)k + nrm.eps);
+    mx *= r;
   }
-  float up = 1.0f, down = 1.0f;
-  if (mx > 0.0f && mx <= FLT_MAX) {
-    int e;
-    frexpf(mx, &e);
-    e = e < -80 ? -80 : e;
-    up = ldexpf(1.0f, 15 - e);
-    down = ldexpf(1.0f, e - 15);
-  }
+  float up, down;
+  pow2_scale(mx, up, down);
   if (!live)
     return;
   if (q == 0)
     rowscale[row] = down;
+  const float cs = NORM ? up * r : up;
   auto put = [&](int j, const float* w) {
     h8_t h;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      h[i] = (_Float16)(w[i] * up);
+      h[i] = (_Float16)(w[i] * cs);
     *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, q + TPR * j, nb)) = h;
   };
   if (CPT > 0) {
@@ -478,7 +539,8 @@ __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restri
   } else {
     for (int j = 0; j < cpt; ++j) {
       float w[8];
-      load8(xr + (size_t)(q + TPR * j) * 8, w);
+      float unused = 0.0f;
+      load8_norm<NORM>(xr, nrm.w, q + TPR * j, w, unused);
       put(j, w);
     }
   }
@@ -2586,23 +2648,23 @@ hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int 
   return t3 ? gate_up_launch<3, false>(s, a, dtype, grid) : gate_up_launch<1, false>(s, a, dtype, grid);
 }
 
-template <typename InT>
-hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode) {
+template <typename InT, bool NORM>
+hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode, RowNorm nrm) {
   const dim3 grid((unsigned)m), block(256);
   if (mode == kStageRowMajor)
-    (void)dispatch(stage_x_kernel<InT, kStageRowMajor>, grid, block, s, x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageRowMajor, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
   else if (mode == kStageFrag)
-    (void)dispatch(stage_x_kernel<InT, kStageFrag>, grid, block, s, x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageFrag, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
   else if (mode == kStageGemm && m < 2048)  // fewer than 256 workgroups of 8 rows: one row each
-    (void)dispatch(stage_x_kernel<InT, kStageGemm>, grid, block, s, x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageGemm, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
   else if (mode == kStageGemm && k / 256 <= 16)
-    (void)dispatch(stage_gemm_kernel<InT, 16>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k);
+    (void)dispatch(stage_gemm_kernel<InT, 16, 32, NORM>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k, nrm);
   else if (mode == kStageGemm && k % 512 == 0 && k / 512 <= 24)  // K <= 12288: one read of x, 64 threads per row
-    (void)dispatch(stage_gemm_kernel<InT, 24, 64>, dim3((unsigned)((m + 7) / 8)), dim3(512), s, x, xo, rowscale, m, k);
+    (void)dispatch(stage_gemm_kernel<InT, 24, 64, NORM>, dim3((unsigned)((m + 7) / 8)), dim3(512), s, x, xo, rowscale, m, k, nrm);
   else if (mode == kStageGemm)
-    (void)dispatch(stage_gemm_kernel<InT, 0>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k);
+    (void)dispatch(stage_gemm_kernel<InT, 0, 32, NORM>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k, nrm);
   else
-    (void)dispatch(stage_x_kernel<InT, kStageFragSplit>, grid, block, s, x, xo, xs, rowscale, m, k);
+    (void)dispatch(stage_x_kernel<InT, kStageFragSplit, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
   return hipGetLastError();
 }
 
@@ -2615,12 +2677,18 @@ hipError_t launch_stage_pack(hipStream_t s, const void* x, int dtype, const Deco
   return hipGetLastError();
 }
 
-hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode) {
+hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode,
+                          const float* norm_w, float eps) {
   if (m <= 0)
     return hipSuccess;
+  RowNorm nrm;
+  nrm.w = norm_w;
+  nrm.eps = eps;
   if (dtype == kF32)
-    return stage_launch(s, static_cast<const float*>(x), xo, xs, rowscale, m, k, mode);
-  return stage_launch(s, static_cast<const _Float16*>(x), xo, xs, rowscale, m, k, mode);
+    return norm_w ? stage_launch<float, true>(s, static_cast<const float*>(x), xo, xs, rowscale, m, k, mode, nrm)
+                  : stage_launch<float, false>(s, static_cast<const float*>(x), xo, xs, rowscale, m, k, mode, nrm);
+  return norm_w ? stage_launch<_Float16, true>(s, static_cast<const _Float16*>(x), xo, xs, rowscale, m, k, mode, nrm)
+                : stage_launch<_Float16, false>(s, static_cast<const _Float16*>(x), xo, xs, rowscale, m, k, mode, nrm);
 }
 
 GemvShape gemv_shape(int rows, int n, int nb, bool gated) {

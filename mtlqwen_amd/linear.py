@@ -174,6 +174,26 @@ def linear(x, w, count, output, auxiliary=None, gated=False, query_counts=None, 
     return output
 
 
+def linear_norm(x, w, norm_weight, count, output, auxiliary=None, gated=False, query_counts=None, stream=None, eps=1e-6):
+    """linear() of rms_norm(x, norm_weight, eps) (native_ops.metal:6-40): the
+    decoder's attention input, attn_norm then the QKV projection
+    (forward.cpp:82, 86-87), with the norm folded into the projection's
+    activation staging (q4k_linear_norm)."""
+    dt = _dtype_code(x)
+    if output.dtype != x.dtype or (auxiliary is not None and auxiliary.dtype != x.dtype):
+        raise TypeError("x, output and auxiliary must share a dtype")
+    _check_norm_weight(norm_weight, w.k)
+    _check_tensor(norm_weight, w.k, "norm_weight", w.device)
+    _check_tensor(x, count * w.k, "x", w.device)
+    _check_tensor(output, count * w.n, "output", w.device)
+    _check_tensor(auxiliary, count * w.n, "auxiliary", w.device)
+    post = POST_GATE if gated else (POST_ADD if auxiliary is not None else POST_STORE)
+    counts, nq = u32_array(query_counts if query_counts is not None else [count])
+    check(lib.q4k_linear_norm(_stream(stream, w.device), w.handle, _ptr(norm_weight), float(eps), _ptr(x), _ptr(output), _ptr(auxiliary),
+                              count, counts, nq, post, dt))
+    return output
+
+
 def mlp_gate_up(x, gate, up, count, output, query_counts=None, stream=None):
     """silu(x . gate^T) * (x . up^T) into ``output`` (the gate buffer)."""
     dt = _dtype_code(x)
@@ -311,7 +331,7 @@ def unrelayout_host(tiled, n, k, ggml_type=GGML_TYPE_Q4_K):
     return dst
 
 
-__all__ = ["Weight", "linear", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "embedding", "rms_norm",
+__all__ = ["Weight", "linear", "linear_norm", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "embedding", "rms_norm",
            "rms_norm_gather", "relayout_host",
            "profile_enable", "profile_query", "mfma_ceiling",
            "unrelayout_host", "q4k_nbytes", "Q4KError", "PHASE_NAMES"]
