@@ -323,7 +323,7 @@ struct GemvArgs {
   int m, n, k, nb, post;
   int rows;  // staged fragment rows: 2m when split (rows m.. hold the low parts), else m
   int split;
-  // Fused gate/up GEMV only: when non-null, x is RMS-normalised first,
+  // Fused gate/up and rows GEMVs: when non-null, x is RMS-normalised first,
   // x * rsqrt(sum(x^2) / k + eps) * norm_w (native_ops.metal:6-40).
   const float* norm_w = nullptr;
   float eps = 0.0f;

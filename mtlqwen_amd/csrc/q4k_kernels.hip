@@ -15,153 +15,10 @@
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
-#include "q4k_internal.h"
+#include "q4k_device.h"
 
 namespace q4k {
 namespace {
-
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef float f16_t __attribute__((ext_vector_type(16)));
-
-// g * sigmoid(g) with the hardware exponential and reciprocal (a few ulp;
-// 1 + exp(-g) >= 1, so the reciprocal never sees a denormal or zero).
-__device__ __forceinline__ float silu(float g) {
-  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-}
-
-__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-
-__device__ __forceinline__ float round_half(float v) {
-  return (float)(_Float16)v;
-}
-
-template <typename T>
-__device__ __forceinline__ float load_elem(const T* p, size_t i) {
-  return (float)p[i];
-}
-
-template <typename T>
-__device__ __forceinline__ void store_elem(T* p, size_t i, float v) {
-  p[i] = (T)v;
-}
-
-// Loads 8 consecutive activations as fp32.
-__device__ __forceinline__ void load8(const float* p, float* v) {
-  f4_t a = *reinterpret_cast<const f4_t*>(p), b = *reinterpret_cast<const f4_t*>(p + 4);
-  v[0] = a[0], v[1] = a[1], v[2] = a[2], v[3] = a[3], v[4] = b[0], v[5] = b[1], v[6] = b[2], v[7] = b[3];
-}
-
-__device__ __forceinline__ void load8(const _Float16* p, float* v) {
-  h8_t a = *reinterpret_cast<const h8_t*>(p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    v[i] = (float)a[i];
-}
-
-// Scales and mins of sub-blocks 2g and 2g+1 from the three packed words of a
-// block header (quant_linear.metal:12-20, taken four bytes at a time).
-__device__ __forceinline__ void scale_min_pair(u4_t hd, int g, uint32_t& sc0, uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
-  const uint32_t sh = 16u * (uint32_t)(g & 1);
-  const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
-  // Sub-blocks 0-3 keep 6 bits in a / b; sub-blocks 4-7 take the low 4 bits
-  // from c and the top 2 from a >> 2 / b >> 2.  Written as one formula with
-  // per-lane selects of plain values: a branch on g would split the caller's
-  // instruction schedule into divergent blocks.
-  const bool low = g < 2;
-  const uint32_t ysh = low ? 0u : 2u, xsh = low ? 0u : 4u;
-  const uint32_t xa = low ? a : c, xb = (low ? b : c) >> xsh, ya = a >> ysh, yb = b >> ysh;
-  sc0 = (xa & 15u) | (ya & 0x30u);
-  sc1 = ((xa >> 8) & 15u) | ((ya >> 8) & 0x30u);
-  m0 = (xb & 15u) | (yb & 0x30u);
-  m1 = ((xb >> 8) & 15u) | ((yb >> 8) & 0x30u);
-}
-
-// The same pairs as 16-bit lanes: p0 = sc(2g) | m(2g) << 16, p1 = sc(2g + 1) |
-// m(2g + 1) << 16.  Bytes 0 / 1 of the selected words are gathered with one
-// v_perm_b32 per word pair.
-__device__ __forceinline__ void scale_min_packed(u4_t hd, int g, uint32_t& p0, uint32_t& p1) {
-  const uint32_t sh = 16u * (uint32_t)(g & 1);
-  const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
-  const bool low = g < 2;
-  const uint32_t ysh = low ? 0u : 2u, xsh = low ? 0u : 4u;
-  const uint32_t xa = low ? a : c, xb = (low ? b : c) >> xsh, ya = a >> ysh, yb = b >> ysh;
-  const uint32_t x0 = __builtin_amdgcn_perm(xb, xa, 0x0C040C00u), x1 = __builtin_amdgcn_perm(xb, xa, 0x0C050C01u);
-  const uint32_t y0 = __builtin_amdgcn_perm(yb, ya, 0x0C040C00u), y1 = __builtin_amdgcn_perm(yb, ya, 0x0C050C01u);
-  p0 = (x0 & 0x000F000Fu) | (y0 & 0x00300030u);
-  p1 = (x1 & 0x000F000Fu) | (y1 & 0x00300030u);
-}
-
-// (a & mask) | bits in one v_and_or_b32.  Written as asm because gfx9 VOP3
-// encodings cannot take the two literal constants the compiler would
-// otherwise need, so it splits the expression into v_and + v_or.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
-  return r;
-}
-
-__device__ __forceinline__ h2_t as_h2(uint32_t v) {
-  return __builtin_bit_cast(h2_t, v);
-}
-
-__device__ __forceinline__ uint32_t as_u32(h2_t v) {
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// Eight quants of one slab pair as exact fp16 products q * sc.
-// (w & mask) | 0x6400 is the fp16 value 1024 + q (low nibble, mask 0x000F) or
-// 1024 + 16q (high nibble, mask 0x00F0); one fused multiply-add with
-// (sc, -1024 sc) or (sc/16, -64 sc) leaves q*sc <= 945, exact in fp16.
-__device__ __forceinline__ h8_t quant_times_scale(uint32_t wa, uint32_t wb, uint32_t mask, uint32_t bias, h2_t mul, h2_t add) {
-  const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-  const h2_t v0 = __builtin_elementwise_fma(as_h2(and_or(wa, mask, bias)), mul, add);
-  const h2_t v1 = __builtin_elementwise_fma(as_h2(and_or(wa8, mask, bias)), mul, add);
-  const h2_t v2 = __builtin_elementwise_fma(as_h2(and_or(wb, mask, bias)), mul, add);
-  const h2_t v3 = __builtin_elementwise_fma(as_h2(and_or(wb8, mask, bias)), mul, add);
-  return __builtin_bit_cast(h8_t, u4_t{as_u32(v0), as_u32(v1), as_u32(v2), as_u32(v3)});
-}
-
-// Per-lane constants of one tile-block header for lane group g: the fp16
-// multipliers of the low / high nibbles (sub-blocks 2g, 2g+1) and the min
-// fragment 32 * m_{4g..4g+3} (zero for g >= 2: k = 8..15 of the 16x16x16 MFMA
-// are unused).  quant_linear.metal:12-20 unpacking, two fields at a time.
-struct BlockConsts {
-  float d, dmin;
-  h2_t mul_lo, add_lo, mul_hi, add_hi;
-  h4_t bmin;
-};
-
-__device__ __forceinline__ BlockConsts block_consts(u4_t hd, int g) {
-  BlockConsts k;
-  k.d = half_bits_to_float(hd.x & 0xffffu);
-  k.dmin = half_bits_to_float(hd.x >> 16);
-  const uint32_t sh = 16u * (uint32_t)(g & 1);
-  const uint32_t a = hd.y >> sh, c = hd.w >> sh;
-  // bytes 0, 1 = sc_{2g}, sc_{2g+1} (both forms computed, then selected:
-  // lanes of one wave take both sides of the g < 2 split)
-  const uint32_t sc_direct = a & 0x3F3Fu, sc_packed = (c & 0x0F0Fu) | ((a >> 2) & 0x3030u);
-  const uint32_t scp = g < 2 ? sc_direct : sc_packed;
-  const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-  const h2_t kneg1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-  // perm(0x64646464, v, sel) interleaves bytes of v with 0x64: fp16 1024 + byte.
-  k.mul_lo = as_h2(__builtin_amdgcn_perm(0x64646464u, scp, 0x04000400u)) - k1024;
-  k.add_lo = k.mul_lo * kneg1024;
-  const h2_t p_hi = as_h2(__builtin_amdgcn_perm(0x64646464u, scp, 0x04010401u));
-  k.mul_hi = __builtin_elementwise_fma(p_hi, h2_t{(_Float16)0.0625f, (_Float16)0.0625f}, h2_t{(_Float16)-64.0f, (_Float16)-64.0f});
-  k.add_hi = k.mul_hi * kneg1024;
-  // bytes 0..3 = m_{4g}..m_{4g+3} for g < 2; zero for g >= 2 (k = 8..15 unused)
-  const uint32_t m03 = hd.z & 0x3F3F3F3Fu, m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-  const uint32_t mb = g >= 2 ? 0u : (g == 0 ? m03 : m47);
-  const h2_t k32 = {(_Float16)32.0f, (_Float16)32.0f}, kneg32768 = {(_Float16)-32768.0f, (_Float16)-32768.0f};
-  const h2_t m01 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04010400u)), k32, kneg32768);
-  const h2_t m23 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04030402u)), k32, kneg32768);
-  k.bmin = h4_t{m01[0], m01[1], m23[0], m23[1]};
-  return k;
-}
 
 // ----------------------------------------------------------------------------
 // Activation staging.  One workgroup per row.  Rows of up to 256 * 8 * kStageRegChunks
@@ -206,33 +63,6 @@ struct RowNorm {
   const float* w = nullptr;
   float eps = 0.0f;
 };
-
-// Element offset of (row, 8-element chunk c) in the GEMV fragment layout:
-// fragment ((row / 16) * nb + b) * 8 + s holds, for lane 16g + (row % 16),
-// elements b*256 + 64g + 32*(s/4) + 8*(s%4) + [0, 8).
-__device__ __forceinline__ size_t frag_offset(int row, int c, int nb) {
-  const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, sl = ((e >> 5) & 1) * 4 + ((e >> 3) & 3);
-  return ((((size_t)(row >> 4) * nb + b) * 8 + sl) * 64 + (g * 16 + (row & 15))) * 8;
-}
-
-// Element offset of (row, 8-element chunk c) in the pipelined GEMM's order:
-// per (128-row block R, 256-element block b, u-step u) one contiguous 16 KB
-// run of 16 fragments f = 2 * (row tile within R) + h, h = 0 for the low-
-// nibble half (elements 64g + 8u + [0, 8)) and 1 for the high-nibble half
-// (64g + 32 + 8u + [0, 8)); fragment lane 16g + row % 16.  One u-step of a
-// workgroup's A operand is then a single contiguous read.
-__device__ __forceinline__ size_t gemm_frag_offset(int row, int c, int nb) {
-  const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, h = (e >> 5) & 1, u = (e >> 3) & 3;
-  const int f = 2 * ((row >> 4) & 7) + h;
-  return (((((size_t)(row >> 7) * nb + b) * 4 + u) * 16 + f) * 64 + (g * 16 + (row & 15))) * 8;
-}
-
-// Half index of (row, sub-block j of block b) in the min-term fragments: per
-// (row tile, block), lane 16 * (j / 4) + row % 16 holds j % 4 of 4 halves --
-// the A operand of v_mfma_f32_16x16x16_f16 with k = sub-block (8 of 16 used).
-__device__ __forceinline__ size_t xs_offset(int row, int b, int j, int nb) {
-  return (((size_t)(row >> 4) * nb + b) * 32 + 16 * (j >> 2) + (row & 15)) * 4 + (j & 3);
-}
 
 // Converts and stores one 8-element chunk; all 256 threads of the workgroup
 // must call it together (the sub-block sum is reduced over 4 lanes).
@@ -289,20 +119,6 @@ __device__ __forceinline__ void load8_norm(const InT* xr, const float* nw, int c
       ss = fmaf(v[i], v[i], ss);
       v[i] *= w8[i];
     }
-  }
-}
-
-// Power-of-two scale that puts a row's largest magnitude mx in [2^14, 2^15):
-// finite in fp16 with the full 11-bit significand for every large element.
-__device__ __forceinline__ void pow2_scale(float mx, float& up, float& down) {
-  up = 1.0f;
-  down = 1.0f;
-  if (mx > 0.0f && mx <= FLT_MAX) {
-    int e;
-    frexpf(mx, &e);
-    e = e < -80 ? -80 : e;
-    up = ldexpf(1.0f, 15 - e);
-    down = ldexpf(1.0f, e - 15);
   }
 }
 
@@ -382,35 +198,6 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
 // magnitude in [2^14, 2^15); hi + lo carries about 22 significant bits.
 // One 64-thread workgroup per (block, row); lane l holds elements 4l..4l+3.
 // ----------------------------------------------------------------------------
-// Cross-lane steps on the VALU (DPP), without the LDS crossbar's latency.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm(1, 0, 3, 2)
-constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm(2, 3, 0, 1)
-constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8 lanes
-constexpr int kDppRowMirror = 0x140;  // lane i <-> 15 - i within 16 lanes
-
-// Sum over each aligned group of 8 lanes, in every lane of the group.
-__device__ __forceinline__ float sum8_lanes(float v) {
-  v += dpp_f<kDppQuadSwap1>(v);
-  v += dpp_f<kDppQuadSwap2>(v);
-  return v + dpp_f<kDppHalfMirror>(v);
-}
-
-// Maximum over the 64 lanes (uniform result).
-__device__ __forceinline__ float max64_lanes(float v) {
-  v = fmaxf(v, dpp_f<kDppQuadSwap1>(v));
-  v = fmaxf(v, dpp_f<kDppQuadSwap2>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_f<kDppRowMirror>(v));
-  const int b = __builtin_bit_cast(int, v);
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
 // Packs the four elements v of lane l (elements 4l..4l+3 of row r of one
 // block) into the block's fragments frag_b [8][64], min-term operands xs_b
 // [64] and unscale factors dsc_b [8]; the 64 lanes of one wave call it
@@ -748,74 +535,6 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 // ----------------------------------------------------------------------------
 // Load helpers of the GEMVs that stream weights through LDS.
 // ----------------------------------------------------------------------------
-// LDS-DMA loads are issued as asm: the compiler would otherwise guard every
-// later LDS read with vmcnt(0) (it cannot tell the ring slots apart).  Their
-// completion is covered by the explicit vmcnt waits below.  No memory
-// clobber: one makes the compiler treat the asm as an outstanding store and
-// wait vmcnt(0) before every later LDS read; ordering against the LDS reads
-// comes from the scheduling barrier in issue() and the clobbering wait.  The
-// address is a wave-uniform SGPR base plus a fixed per-lane VGPR offset, so
-// issuing costs no vector ALU work.  M0 is written here; nothing else in this
-// kernel uses it.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// Wave-uniform values the compiler cannot prove uniform are moved to SGPRs.
-__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
-template <int OFFSET>
-__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "s"(lds), "n"(OFFSET) : "m0");
-}
-
-template <int OFFSET>
-__device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "s"(lds), "n"(OFFSET) : "m0");
-}
-
-// Register loads issued as asm for the same reason: a compiler-visible load
-// makes its first use wait vmcnt(0), draining the ring.  Their results are
-// released to the compiler by hold() after an explicit wait.
-__device__ __forceinline__ u4_t asm_load16(const void* p) {
-  u4_t r;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
-  return r;
-}
-
-// Stores and loads that bypass every cache level (sc0 sc1: system
-// coherence), for data exchanged between workgroups on different XCDs.  The
-// loads return through vmcnt like the others: wait before use.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
-}
-
-__device__ __forceinline__ float load_coherent(const float* p) {
-  float r;
-  asm volatile("global_load_dword %0, %1, off sc0 sc1" : "=v"(r) : "v"(p));
-  return r;
-}
-
-// Same, into a register that keeps its value in lanes the load skips.
-__device__ __forceinline__ void asm_load16_into(u4_t& r, const void* p) {
-  asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(r) : "v"(p));
-}
-
-__device__ __forceinline__ h4_t asm_load8(const void* p) {
-  h4_t r;
-  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
-  return r;
-}
-
-template <typename V>
-__device__ __forceinline__ void hold(V& v) {
-  asm volatile("" : "+v"(v));
-}
 
 // ----------------------------------------------------------------------------
 // Fused gate/up GEMV with in-register activation packing (m <= 8 rows, K =
@@ -1154,16 +873,6 @@ __global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
 // Workgroups of one group are placed on one XCD (workgroup b runs on XCD
 // b % 8), so their partials meet in one L2.
 // ----------------------------------------------------------------------------
-// Count of arrivals at a counter shared by workgroups on any XCD: the atomic
-// is performed at system scope (past every XCD's L2).
-__device__ __forceinline__ int count_arrival(int* ctr) {
-  return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-__device__ __forceinline__ void reset_counter(int* ctr) {
-  __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
 // Bytes of LDS one split-K slice uses.
 template <int NM, int T, int BPS, int DP>
 constexpr int splitk_lds_bytes() {

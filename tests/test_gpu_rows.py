@@ -1,0 +1,77 @@
+"""The GEMV for decode-shaped batches of 9..48 activation rows (x staged
+once per call into fp16 MFMA fragments with per-(row, block) power-of-two
+scales; one 16-column tile per workgroup, K split over its waves) against
+the CPU oracle: several block counts (K = 768 .. 12288, odd ones
+included), partial and single column tiles, hi/lo rows (m <= 24) and single
+fp16 rows (25..48), gated pairs, fp16 activations, post 1 / 2; back-to-back
+calls of one shape give identical results.
+Bar: max row-relative error 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+from q4k_ref import make_q4k, make_x, row_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+# (m, n, k, counts): decode phase (counts <= 5 per query) unless noted
+SHAPES = [
+    (40, 4096, 12288, [5] * 8),   # down projection of config 2: several K-slices
+    (40, 12288, 4096, [5] * 8),   # wide N
+    (24, 2048, 4096, [3] * 8),    # hi/lo rows, three row tiles
+    (9, 1040, 1024, [5, 4]),      # partial last column group
+    (13, 48, 768, [5, 5, 3]),     # fewer tiles than one group
+    (48, 4096, 2048, [48]),       # prefill batch of 48 rows (GEMV side)
+    (30, 272, 3328, [30]),        # odd block count (13)
+]
+
+
+@pytest.mark.parametrize("m,n,k,counts", SHAPES)
+def test_rows_store(q4k, oracle, gpu, m, n, k, counts):
+    rng = np.random.default_rng(1500 + m + n % 97)
+    w = make_q4k(rng, n, k)
+    W = q4k.Weight(w, n, k)
+    x = make_x(rng, m, k)
+    y = torch.full((m, n), float("nan"), device=gpu)
+    xt = torch.from_numpy(x).to(gpu)
+    q4k.linear(xt, W, m, y, query_counts=counts)
+    # A second call of the same shape must give the same result.
+    y2 = torch.full((m, n), float("nan"), device=gpu)
+    q4k.linear(xt, W, m, y2, query_counts=counts)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert torch.equal(y, y2)
+    assert row_rel_err(got, oracle.linear(x, w, n, k)) <= TOL
+
+
+@pytest.mark.parametrize("m,post,dtype", [(40, 1, torch.float32), (17, 2, torch.float32), (33, 1, torch.float16),
+                                          (6, 0, torch.float16)])
+def test_rows_epilogues(q4k, oracle, gpu, m, post, dtype):
+    n, k = 1024, 4096
+    rng = np.random.default_rng(1550 + m)
+    w = make_q4k(rng, n, k)
+    W = q4k.Weight(w, n, k)
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    x = make_x(rng, m, k, 0.25).astype(npdt)
+    aux = make_x(rng, m, n, 2.0).astype(npdt) if post else None
+    y = torch.from_numpy(aux).to(gpu) if post else torch.empty((m, n), device=gpu, dtype=dtype)
+    q4k.linear(torch.from_numpy(x).to(gpu), W, m, y, auxiliary=y if post else None, gated=(post == 2), query_counts=[5] * (m // 5) + ([m % 5] if m % 5 else []))
+    torch.cuda.synchronize()
+    ref = oracle.linear(x, w, n, k, aux=aux, post=post)
+    assert row_rel_err(y.float().cpu().numpy(), ref.astype(np.float32)) <= TOL
+
+
+@pytest.mark.parametrize("m", [9, 24, 40])
+def test_rows_gated(q4k, oracle, gpu, m):
+    n, k = 3072, 4096
+    rng = np.random.default_rng(1560 + m)
+    wg, wu = make_q4k(rng, n, k), make_q4k(rng, n, k)
+    G, U = q4k.Weight(wg, n, k), q4k.Weight(wu, n, k)
+    x = make_x(rng, m, k, 0.5)
+    y = torch.empty((m, n), device=gpu)
+    counts = [5] * (m // 5) + ([m % 5] if m % 5 else [])
+    q4k.mlp_gate_up(torch.from_numpy(x).to(gpu), G, U, m, y, query_counts=counts)
+    torch.cuda.synchronize()
+    assert row_rel_err(y.cpu().numpy(), oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
