@@ -1125,6 +1125,30 @@ int mlp_gate_up_impl(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x
     return fail(Q4K_ESHAPE, "decode batch of %u rows exceeds %d", m, 16 * kGemvMaxRowTiles);
   if (phase == Q4K_PHASE_GATED_DECODE && q4)
     return run_linear(s, wg, wu, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, norm_w, eps);
+  if (phase == Q4K_PHASE_GATED_DECODE && wg->type == wu->type && typed_gate_up_supported(wg->type, (int)m, (int)(wg->k / 256), (int)wg->n)) {
+    // The fused gate/up GEMV of a type with one in the reference
+    // (fused_kernels.metal:80-200): one launch, x packed in registers.
+    Workspace& ws = workspace(wg->device);
+    std::lock_guard<std::mutex> lock(ws.mu);
+    resolve(wg, phase);
+    resolve(wu, phase);
+    GemvArgs a{};
+    a.w = wg->data;
+    a.wu = wu->data;
+    a.x = x;
+    a.y = y;
+    a.m = (int)m;
+    a.n = (int)wg->n;
+    a.k = (int)wg->k;
+    a.nb = (int)(wg->k / 256);
+    a.rows = 2 * (int)m;
+    a.split = 1;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    LaunchTimer timer(s, Q4K_KERNEL_GEMV_GATED);
+    Q4K_TRY_HIP(launch_typed_gate_up(s, a, wg->type, (int)dtype, device_cus(wg->device)), "typed gate/up launch");
+    return Q4K_OK;
+  }
   // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in
   // place.  Both read the same x: it is staged once (with the norm, if any),
   // under one hold of the workspace lock.

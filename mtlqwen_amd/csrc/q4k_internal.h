@@ -389,6 +389,10 @@ GemvShape gemv_shape(int rows, int n, int nb, bool gated);
 // staging launch); reads a.x, a.w, a.wu (and a.norm_w when set) and writes a.y.
 bool gemv_gate_up_supported(int m, int nb, int n);
 hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus);
+// The same for gate and up weights of one other type with a fused decode
+// kernel in the reference (Q5_K, IQ4_XS).
+bool typed_gate_up_supported(uint32_t type, int m, int nb, int n);
+hipError_t launch_typed_gate_up(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus);
 
 // Split-K GEMV for m <= 8 (see q4k_gemv_splitk_kernel): a plan picks an
 // instance for (n, nb); the launch needs `part` (gemv_splitk_part_floats

@@ -656,25 +656,23 @@ __device__ __forceinline__ void pack_x_regs(const float (&xv)[32], int lane, XBl
 constexpr int kGuXRow = 36;
 constexpr int kGuWaveFloats = 2 * 64 * kGuXRow;
 
-// One item (T column tiles of both matrices) of the fused gate/up GEMV, by the
-// 8 waves of the workgroup.  NORM: x is RMS-normalised on the way in
-// (native_ops.metal:6-40, the norm forward.cpp:114 applies before the MLP):
-// the 8 waves hold all of x between them, so each row's sum of squares is
-// their partial sums (ssq [wave][row]) added after one barrier, and every
-// element becomes (x * rsqrt(sum / k + eps)) * w before the pack.
-template <int T, typename OutT, bool NORM>
-__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int item) {
-  constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT;
+// The x of one item of the fused gate/up GEMV, packed: wave w loads K-blocks
+// bw, bw + 1 of all 8 rows (one coalesced load per (block, row), lane l
+// holding elements 4l..4l+3; rows >= m read row 0 and are zeroed), calls
+// issue_first() so that its first weight units queue behind x, and turns its
+// blocks into MFMA operands in registers (through its LDS region).  NORM: x
+// is RMS-normalised on the way in (native_ops.metal:6-40, the norm
+// forward.cpp:114 applies before the MLP): the 8 waves hold all of x between
+// them, so each row's sum of squares is their partial sums (ssq [wave][row])
+// added after one barrier, and every element becomes
+// (x * rsqrt(sum / k + eps)) * w before the pack.
+template <typename OutT, bool NORM, typename Issue>
+__device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int bw, XBlock (&xb)[2],
+                                               Issue&& issue_first) {
+  constexpr int W = 8, BPW = 2;
   constexpr int kXRow = kGuXRow;
-  static_assert(MT * 8 * 16 <= BPW * 64 * kXRow, "partials fit the x region");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, col = lane & 15;
-  const int nb = a.nb, bw = ((wave + item) % W) * BPW;
-  const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
-
-  // x: one coalesced load per (block, row), lane l holding elements
-  // 4l..4l+3 (rows >= m read row 0 and are zeroed below).
   float xv[BPW][8][4];
 #pragma unroll
   for (int j = 0; j < BPW; ++j)
@@ -699,27 +697,8 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
     for (int j = 0; j < BPW; ++j)
       nw[j] = *reinterpret_cast<const f4_t*>(a.norm_w + (size_t)(bw + j) * 256 + 4 * lane);
   }
-  // Units are loaded into registers DQ ahead of the one being computed
-  // (header dword, then the two quant slabs; the scheduling barriers keep
-  // the issue order: x first, then unit by unit).  A shallow window keeps
-  // the memory queues short, so x and each wave's next unit arrive early;
-  // issuing every unit at once measured slower (the whole item's requests
-  // queue ahead of x).
-  constexpr int DQ = 2;
   __builtin_amdgcn_sched_barrier(0);
-  uint32_t hw[U];
-  u4_t q0[U], q1[U];
-  auto issue_unit = [&](int u) {
-    const int j = u / MT, mt = u - j * MT, mi = mt / T, t = mt - mi * T;
-    const uint8_t* src = (mi ? a.wu : a.w) + ((size_t)item * T + t) * tile_bytes + (size_t)(bw + j) * kTileBlockBytes;
-    hw[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kHeaderOffset) + lane);
-    q0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
-    q1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-#pragma unroll
-  for (int u = 0; u < (DQ < U ? DQ : U); ++u)
-    issue_unit(u);
+  issue_first();
 
   if constexpr (NORM) {
     float ss[8];
@@ -771,7 +750,6 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
         v4[e] = r < a.m ? xv[j][r][e] : 0.0f;
       *reinterpret_cast<f4_t*>(xw + (j * 64 + dl + r) * kXRow + doff) = v4;
     }
-  XBlock xb[BPW];
 #pragma unroll
   for (int j = 0; j < BPW; ++j) {
     float t32[32];
@@ -784,6 +762,80 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
     }
     pack_x_regs(t32, lane, xb[j]);
   }
+}
+
+// The end of an item: C row 4g + v of each (matrix, tile) pair, lanes g < 2
+// adding the low part held 32 lanes up, goes to the wave's LDS region; the
+// eight waves' sums are added in wave order and SiLU(gate) * up is stored.
+template <int T, typename OutT>
+__device__ __forceinline__ void gate_up_finish(const GemvArgs& a, float (*xl)[kGuWaveFloats], const f4_t (&acc)[2 * T], int item) {
+  constexpr int W = 8, MT = 2 * T;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  float* const xw = xl[wave];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float tot = acc[mt][v] + __shfl_xor(acc[mt][v], 32);
+      if (g < 2)
+        xw[(mt * 8 + 4 * g + v) * 16 + col] = tot;
+    }
+  __syncthreads();
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  constexpr int EPI = 16 * T;
+  for (int o = tid; o < a.m * EPI; o += 64 * W) {
+    const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
+    float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      gv += xl[w][(t * 8 + row) * 16 + cc];
+      uv += xl[w][((T + t) * 8 + row) * 16 + cc];
+    }
+    if (sizeof(OutT) == 2) {
+      gv = round_half(gv);
+      uv = round_half(uv);
+    }
+    store_elem(y, (size_t)row * a.n + ((size_t)item * T + t) * 16 + cc, silu(gv) * uv);
+  }
+}
+
+// One item (T column tiles of both matrices) of the fused gate/up GEMV, by the
+// 8 waves of the workgroup.
+template <int T, typename OutT, bool NORM>
+__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int item) {
+  constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT;
+  static_assert(MT * 8 * 16 <= BPW * 64 * kGuXRow, "partials fit the x region");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int nb = a.nb, bw = ((wave + item) % W) * BPW;
+  const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
+
+  // Units are loaded into registers DQ ahead of the one being computed
+  // (header dword, then the two quant slabs; the scheduling barriers keep
+  // the issue order: x first, then unit by unit).  A shallow window keeps
+  // the memory queues short, so x and each wave's next unit arrive early;
+  // issuing more units ahead measured slower (they queue ahead of the x of
+  // later workgroups).
+  constexpr int DQ = 2;
+  uint32_t hw[U];
+  u4_t q0[U], q1[U];
+  auto issue_unit = [&](int u) {
+    const int j = u / MT, mt = u - j * MT, mi = mt / T, t = mt - mi * T;
+    const uint8_t* src = (mi ? a.wu : a.w) + ((size_t)item * T + t) * tile_bytes + (size_t)(bw + j) * kTileBlockBytes;
+    hw[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kHeaderOffset) + lane);
+    q0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    q1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  XBlock xb[BPW];
+  gate_up_pack_x<OutT, NORM>(a, xl, ssq, bw, xb, [&] {
+#pragma unroll
+    for (int u = 0; u < (DQ < U ? DQ : U); ++u)
+      issue_unit(u);
+  });
 
   f4_t acc[MT];
 #pragma unroll
@@ -815,34 +867,7 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
     for (int v = 0; v < 4; ++v)
       acc[mt][v] += fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * xb[j].dv[v];
   }
-
-  // C row 4g + v: lanes g < 2 add the low part held 32 lanes up; the
-  // wave's partials [mt][row][col] go to its own x region.
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float tot = acc[mt][v] + __shfl_xor(acc[mt][v], 32);
-      if (g < 2)
-        xw[(mt * 8 + 4 * g + v) * 16 + col] = tot;
-    }
-  __syncthreads();
-  OutT* y = reinterpret_cast<OutT*>(a.y);
-  constexpr int EPI = 16 * T;
-  for (int o = tid; o < a.m * EPI; o += 64 * W) {
-    const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
-    float gv = 0.0f, uv = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      gv += xl[w][(t * 8 + row) * 16 + cc];
-      uv += xl[w][((T + t) * 8 + row) * 16 + cc];
-    }
-    if (sizeof(OutT) == 2) {
-      gv = round_half(gv);
-      uv = round_half(uv);
-    }
-    store_elem(y, (size_t)row * a.n + ((size_t)item * T + t) * 16 + cc, silu(gv) * uv);
-  }
+  gate_up_finish<T, OutT>(a, xl, acc, item);
 }
 
 template <int T, typename OutT, bool NORM>
@@ -2039,6 +2064,63 @@ __device__ __forceinline__ void typed_epilogue(const GemvArgs& a, const float* p
   }
 }
 
+// Fused gate/up GEMV of a weight type with a fused decode kernel in the
+// reference (Q5_K, IQ4_XS: fused_kernels.metal:80-143, 145-200): the Q4_K
+// item's x packing and epilogue (gate_up_pack_x, gate_up_finish) around the
+// type's tile-block units (F::load, F::mac), two units in flight per wave.
+template <class F, int T, typename OutT, bool NORM>
+__device__ __forceinline__ void typed_gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int item) {
+  constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT, DQ = 2;
+  static_assert(MT * 8 * 16 <= BPW * 64 * kGuXRow, "partials fit the x region");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = a.nb, bw = ((wave + item) % W) * BPW;
+  const size_t tile_bytes = (size_t)nb * F::kTB;
+  typename F::U un[U];
+  auto issue_unit = [&](int u) {
+    const int j = u / MT, mt = u - j * MT, mi = mt / T, t = mt - mi * T;
+    F::load(un[u], (mi ? a.wu : a.w) + ((size_t)item * T + t) * tile_bytes + (size_t)(bw + j) * F::kTB, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  XBlock xb[BPW];
+  gate_up_pack_x<OutT, NORM>(a, xl, ssq, bw, xb, [&] {
+#pragma unroll
+    for (int u = 0; u < (DQ < U ? DQ : U); ++u)
+      issue_unit(u);
+  });
+  XF xf[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      xf[j].f[s] = xb[j].frag[s];
+    xf[j].xs = xb[j].xs;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      xf[j].dv[v] = xb[j].dv[v];
+  }
+  f4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    acc[mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = u / MT, mt = u - j * MT;
+    __builtin_amdgcn_sched_barrier(0);
+    if (u + DQ < U)
+      issue_unit(u + DQ);
+    F::mac(un[u], xf[j], lane, acc[mt]);
+  }
+  gate_up_finish<T, OutT>(a, xl, acc, item);
+}
+
+template <class F, int T, typename OutT, bool NORM>
+__global__ __launch_bounds__(512) void typed_gate_up_kernel(GemvArgs a) {
+  __shared__ __attribute__((aligned(16))) float xl[8][kGuWaveFloats];
+  __shared__ float ssq[8][8];
+  typed_gate_up_item<F, T, OutT, NORM>(a, xl, ssq, blockIdx.x);
+}
+
 template <class F, int T, int DQ, typename OutT>
 __global__ __launch_bounds__(512) void typed_gemv_kernel(GemvArgs a) {
   constexpr int W = 8;
@@ -2355,6 +2437,44 @@ hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int 
   if (a.norm_w)
     return t3 ? gate_up_launch<3, true>(s, a, dtype, grid) : gate_up_launch<1, true>(s, a, dtype, grid);
   return t3 ? gate_up_launch<3, false>(s, a, dtype, grid) : gate_up_launch<1, false>(s, a, dtype, grid);
+}
+
+bool typed_gate_up_supported(uint32_t type, int m, int nb, int n) {
+  static const bool enabled = env_int("Q4K_GEMV_GATE_UP", 1) != 0;
+  return enabled && (type == kTypeQ5_K || type == kTypeIQ4_XS) && m >= 1 && m <= 8 && nb == 16 && n % 16 == 0;
+}
+
+template <class F, int T, bool NORM>
+hipError_t typed_gate_up_launch(hipStream_t s, const GemvArgs& a, int dtype, unsigned grid) {
+  if (dtype == kF32)
+    (void)dispatch(typed_gate_up_kernel<F, T, float, NORM>, dim3(grid), dim3(512), s, a);
+  else
+    (void)dispatch(typed_gate_up_kernel<F, T, _Float16, NORM>, dim3(grid), dim3(512), s, a);
+  return hipGetLastError();
+}
+
+template <class F>
+hipError_t typed_gate_up_dispatch(hipStream_t s, const GemvArgs& a, int dtype, int cus) {
+  // Column tiles per workgroup as for Q4_K.
+  const int ctiles = a.n / 16;
+  const bool t3 = ctiles % 3 == 0 && ctiles / 3 >= cus;
+  const unsigned grid = (unsigned)(t3 ? ctiles / 3 : ctiles);
+  if (a.norm_w)
+    return t3 ? typed_gate_up_launch<F, 3, true>(s, a, dtype, grid) : typed_gate_up_launch<F, 1, true>(s, a, dtype, grid);
+  return t3 ? typed_gate_up_launch<F, 3, false>(s, a, dtype, grid) : typed_gate_up_launch<F, 1, false>(s, a, dtype, grid);
+}
+
+hipError_t launch_typed_gate_up(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus) {
+  if (a.m < 1 || a.m > 8 || a.nb != 16 || a.n % 16 != 0)
+    return hipErrorInvalidValue;
+  switch (type) {
+    case kTypeQ5_K:
+      return typed_gate_up_dispatch<FmtQ5K>(s, a, dtype, cus);
+    case kTypeIQ4_XS:
+      return typed_gate_up_dispatch<FmtIQ4XS>(s, a, dtype, cus);
+    default:
+      return hipErrorInvalidValue;
+  }
 }
 
 template <typename InT, bool NORM>

@@ -10,7 +10,9 @@ idle) to 48 blocks (six per wave) and 9 blocks (ragged per wave); ragged
 column tails of the 4- and 2-tile workgroups; the persistent form at K = 4096
 (16 * 4401 columns, one tile in the last item); post 1 / 2 in place in
 decode and prefill (per-8-row groups); fp16 activations; the device-side
-upload (bit-identical to the host one); the gated projection; a GGUF file;
+upload (bit-identical to the host one); the gated projection (one fused
+launch for Q5_K and IQ4_XS in the decode phase, with and without the
+ffn_norm); a GGUF file;
 and, for every non-Q4_K type, prefill batches of 64 rows and more (the
 dequantised fp16 GEMM) with post 0 / 1 / 2 and fp16 activations.
 """
@@ -96,6 +98,62 @@ def test_gate_up(q4k, oracle, gpu, t, m, counts):
     q4k.mlp_gate_up(_t(x, gpu), G, U, m, gate, query_counts=counts)
     torch.cuda.synchronize()
     assert row_rel_err(gate.cpu().numpy(), oracle.mlp_gate_up(x, wg, wu, n, k, ggml_type=t)) <= TOL
+
+
+FUSED_GATE_UP = [TYPE_Q5_K, TYPE_IQ4_XS]
+
+
+@pytest.mark.parametrize("m,n,dtype", [(8, 12288, torch.float32), (1, 512, torch.float32), (3, 1536, torch.float16)])
+@pytest.mark.parametrize("t", FUSED_GATE_UP)
+def test_gate_up_fused_decode(q4k, oracle, gpu, t, m, n, dtype):
+    """Q5_K / IQ4_XS gate and up in the decode phase run as one fused launch
+    (fused_kernels.metal:80-200): three column tiles per workgroup at
+    N = 12288, one at N = 512 and 1536; fp32 and fp16 activations."""
+    k = 4096
+    rng = np.random.default_rng(980 + m + t)
+    wg, wu = make_weight(rng, n, k, t), make_weight(rng, n, k, t)
+    # fp16: small enough that SiLU(gate) * up stays inside the fp16 range.
+    x = make_x(rng, m, k, 0.01 if dtype == torch.float16 else 0.5)
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    xq = x.astype(npdt)
+    G, U = q4k.Weight(wg, n, k, ggml_type=t), q4k.Weight(wu, n, k, ggml_type=t)
+    gate = torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+    xt = _t(xq, gpu, dtype)
+    torch.cuda.synchronize()
+    q4k.profile_enable(True)
+    q4k.mlp_gate_up(xt, G, U, m, gate, query_counts=[1] * m)
+    torch.cuda.synchronize()
+    launches = [q4k.profile_query(kind)[0] for kind in (q4k.KERNEL_STAGE, q4k.KERNEL_GEMV, q4k.KERNEL_GEMV_GATED, q4k.KERNEL_AUX)]
+    q4k.profile_enable(False)
+    assert launches == [0, 0, 1, 0], launches
+    assert G.kernel_name(q4k.PHASE_GATED_DECODE).startswith("mlp_")
+    ref = oracle.mlp_gate_up(xq, wg, wu, n, k, ggml_type=t)
+    assert row_rel_err(gate.float().cpu().numpy(), ref.astype(np.float32)) <= TOL
+
+
+@pytest.mark.parametrize("t", FUSED_GATE_UP)
+def test_gate_up_fused_with_ffn_norm(q4k, oracle, gpu, t):
+    """q4k_mlp with the layer's ffn_norm over Q5_K / IQ4_XS gate and up in the
+    decode phase: the norm runs inside the fused launch (no separate norm
+    launch), then the down projection adds the residual in place."""
+    m, n, k = 8, 1536, 4096
+    rng = np.random.default_rng(990 + t)
+    wg, wu, wd = make_weight(rng, n, k, t), make_weight(rng, n, k, t), make_weight(rng, k, n, t)
+    h0 = make_x(rng, m, k, 3.0)
+    nw = (1.0 + 0.2 * rng.standard_normal(k)).astype(np.float32)
+    G, U, D = (q4k.Weight(w, r, c, ggml_type=t) for w, r, c in ((wg, n, k), (wu, n, k), (wd, k, n)))
+    hidden = _t(h0, gpu)
+    gate = torch.empty((m, n), device=gpu)
+    torch.cuda.synchronize()
+    q4k.profile_enable(True)
+    q4k.mlp(hidden, G, U, D, hidden, gate, m, query_counts=[1] * m, norm_weight=_t(nw, gpu))
+    torch.cuda.synchronize()
+    gated, aux = q4k.profile_query(q4k.KERNEL_GEMV_GATED)[0], q4k.profile_query(q4k.KERNEL_AUX)[0]
+    q4k.profile_enable(False)
+    assert (gated, aux) == (1, 0), (gated, aux)
+    g_gpu = gate.cpu().numpy()
+    assert row_rel_err(g_gpu, oracle.mlp_gate_up(oracle.rms_norm(h0, nw), wg, wu, n, k, ggml_type=t)) <= TOL
+    assert row_rel_err(hidden.cpu().numpy(), oracle.linear(g_gpu, wd, k, n, aux=h0, post=1, ggml_type=t)) <= TOL
 
 
 @pytest.mark.parametrize("t", TYPES)
