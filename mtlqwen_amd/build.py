@@ -59,8 +59,7 @@ def build(verbose=False):
     with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB + ".tmp"
-    # rocBLAS: the plain fp16 GEMM behind prefill with the non-Q4_K types.
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lrocblas"], verbose)
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
     return LIB
 

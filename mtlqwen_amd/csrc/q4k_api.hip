@@ -14,7 +14,6 @@
 #include <string>
 #include <vector>
 
-#include <rocblas/rocblas.h>
 
 #include "../../include/q4k.h"
 #include "q4k_internal.h"
@@ -83,11 +82,6 @@ struct Workspace {
   size_t pack_bytes = 0;
   uint8_t* normed = nullptr;  // q4k_mlp's RMS-normalised x when the norm is not fused
   size_t normed_bytes = 0;
-  _Float16* wdq = nullptr;  // prefill with the other types: dequantised fp16 weights [n, k]
-  size_t wdq_elems = 0;
-  float* cbuf = nullptr;  // ... and the library GEMM's fp32 result [m, n]
-  size_t cbuf_elems = 0;
-  rocblas_handle blas = nullptr;
   std::vector<void*> retired;
   // Fixed-size buffers in the no-allocation scratch: never grown; a call
   // that needs more fails (ensure_buffer).
@@ -321,12 +315,12 @@ Kernel& resolve(q4k_weight* w, uint32_t phase) {
     k.kind = phase == Q4K_PHASE_GATED_DECODE ? kGemvGated : phase == Q4K_PHASE_PREFILL ? kGemm : kGemv;
     const bool other = w->type != Q4K_GGML_TYPE_Q4_K;
     if (other && k.kind == kGemm)
-      k.kind = kGemv;  // prefill of the other types: GEMV per 8-row group below 64 rows, dequantised fp16 GEMM from 64
+      k.kind = kGemv;  // prefill of the other types: GEMV per 8-row group below 64 rows, the typed MFMA GEMM from 64
     if (k.kind == kGemm && w->n < kGemmMinColumns)
       k.kind = kGemv;  // narrow Q4_K outputs: the GEMV per 8-row group at every row count
     k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + type_name(w->type) + "_k" + std::to_string(w->k) + "_n" +
              std::to_string(w->n) + "_" + suffix[phase] +
-             (k.kind == kGemm ? "_mfma32x32x16" : other && phase == Q4K_PHASE_PREFILL ? "_fp16_gemm" : "_mfma16x16x32");
+             (k.kind == kGemm ? "_mfma32x32x16" : "_mfma16x16x32");
   }
   return k;
 }
@@ -477,52 +471,34 @@ int set_device(int device) {
 // rows the GEMV per 8-row group (run_gemv_groups_locked); from 64 rows the
 // GEMM below.
 constexpr uint32_t kTypedGemmRows = 64;
-// Prefill-sized batches with the other types (m >= 64): x staged as fp16 rows
-// with power-of-two row scales, the weights dequantised to fp16 [n, k] (the
-// reference's prefill tile values), one rocBLAS GEMM with fp32 accumulation
-// and output, then the epilogue (row unscale, post 0/1/2, fp16 rounding).
+// Prefill-sized batches with the other types (m >= 64): x staged in the GEMM
+// order (fp16, power-of-two row scales, zero rows up to the 128-row tile; the
+// attn/ffn norm folded in), then the type's MFMA GEMM, which dequantises the
+// weights to the reference's prefill tile values in registers and applies the
+// epilogue (row unscale, post 0/1/2, fp16 rounding) in place.
 int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
                           uint32_t dtype, const float* norm_w, float eps) {
-  const size_t n = w->n, k = w->k;
-  if (ws.fixed)
-    return fail(Q4K_ETYPE, "q4k_linear_noalloc does not serve %u-row prefill with %s weights (their prefill GEMM is a library call that may allocate)",
-                m, type_name(w->type));
-  int rc = ensure_workspace(stream, ws, w->device, (size_t)m * k, m);
-  if (!rc)
-    rc = ensure_buffer(stream, ws, w->device, ws.wdq, ws.wdq_elems, n * k, "dequantised-weight workspace");
-  if (!rc)
-    rc = ensure_buffer(stream, ws, w->device, ws.cbuf, ws.cbuf_elems, (size_t)m * n, "GEMM result workspace");
+  const size_t rows = (size_t)gemm2_rows((int)m);
+  int rc = ensure_workspace(stream, ws, w->device, rows * w->k, rows);
   if (rc)
     return rc;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (!ws.blas && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
-    return fail(Q4K_ECAPTURE, "the library GEMM handle of device %d is created on first use, which allocates: make one call before the capture",
-                w->device);
-  if (!ws.blas && rocblas_create_handle(&ws.blas) != rocblas_status_success) {
-    ws.blas = nullptr;
-    return fail(Q4K_EHIP, "rocblas_create_handle failed on device %d", w->device);
-  }
   {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
-    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, nullptr, ws.scale, (int)m, (int)k, kStageRowMajor, norm_w, eps), "stage_x launch");
+    Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, nullptr, ws.scale, (int)m, (int)w->k, kStageGemm, norm_w, eps), "stage_x launch");
   }
-  {
-    LaunchTimer timer(stream, Q4K_KERNEL_AUX);
-    Q4K_TRY_HIP(launch_typed_dequant(stream, w->data, w->type, (uint32_t)n, (uint32_t)k, ws.wdq), "dequant launch");
-  }
-  // Row-major C [m, n] = X [m, k] . W [n, k]^T is column-major C^T = W^T' . X^T'
-  // with W read transposed.
-  if (rocblas_set_stream(ws.blas, stream) != rocblas_status_success)
-    return fail(Q4K_EHIP, "rocblas_set_stream failed");
-  const float one = 1.0f, zero = 0.0f;
-  const rocblas_status st =
-      rocblas_gemm_ex(ws.blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)n, (rocblas_int)m, (rocblas_int)k, &one, ws.wdq,
-                      rocblas_datatype_f16_r, (rocblas_int)k, ws.x, rocblas_datatype_f16_r, (rocblas_int)k, &zero, ws.cbuf, rocblas_datatype_f32_r,
-                      (rocblas_int)n, ws.cbuf, rocblas_datatype_f32_r, (rocblas_int)n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  if (st != rocblas_status_success)
-    return fail(Q4K_EHIP, "rocblas_gemm_ex failed (%d)", (int)st);
-  LaunchTimer timer(stream, Q4K_KERNEL_AUX);
-  Q4K_TRY_HIP(launch_gemm_post(stream, ws.cbuf, ws.scale, y, aux, (int)m, (int)n, (int)post, (int)dtype), "gemm epilogue launch");
+  GemmArgs a;
+  a.w = w->data;
+  a.xh = ws.x;
+  a.rowscale = ws.scale;
+  a.y = y;
+  a.aux = aux;
+  a.m = (int)m;
+  a.n = (int)w->n;
+  a.k = (int)w->k;
+  a.nb = (int)(w->k / 256);
+  a.post = (int)post;
+  LaunchTimer timer(stream, Q4K_KERNEL_GEMM);
+  Q4K_TRY_HIP(launch_typed_gemm(stream, a, w->type, (int)dtype, device_cus(w->device)), "typed gemm launch");
   return Q4K_OK;
 }
 

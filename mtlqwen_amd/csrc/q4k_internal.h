@@ -447,11 +447,10 @@ hipError_t launch_q4k_persistent(hipStream_t s, const GemvArgs& a, int dtype, in
 // post 0/1/2 on a.y / a.aux.
 hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, int dtype, int cus);
 
-// Prefill with the other types: their weights dequantised to fp16 [n, k]
-// (the reference's prefill tile values, rounded once), and the epilogue of a
-// library GEMM's fp32 result c [m, n]: y = post(c * rowscale[row], aux).
-hipError_t launch_typed_dequant(hipStream_t s, const uint8_t* w, uint32_t type, uint32_t n, uint32_t k, _Float16* out);
-hipError_t launch_gemm_post(hipStream_t s, const float* c, const float* rowscale, void* y, const void* aux, int m, int n, int post, int dtype);
+// Prefill GEMM for Q5_K, Q6_K, Q8_0 and IQ4_XS weights (x staged in the GEMM
+// order, 128-row tiles; any n that is a multiple of 16).
+bool typed_gemm_supported(uint32_t type, int m, int n);
+hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, int dtype, int cus);
 
 // Device-side GGUF -> tiled re-layout of Q6_K, Q8_0, Q5_K or IQ4_XS weights.
 hipError_t launch_typed_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type);

@@ -1281,8 +1281,9 @@ constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4
 // and aux for post 1 / 2) are issued before its stores so that their latency
 // is paid once per row tile; a tile wholly inside m (FULL) has no per-row
 // checks.
-template <typename OutT, int POST, bool FULL>
-__device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&acc)[8][4], int mt0, int ct0, int lane) {
+// CT column tiles per wave, of which the first nct lie inside n.
+template <typename OutT, int POST, bool FULL, int CT = 4>
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&acc)[8][CT], int mt0, int ct0, int lane, int nct = CT) {
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   const int g = lane >> 4, col = lane & 15;
@@ -1297,14 +1298,14 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
   const size_t col0 = (size_t)ct0 * 16 + col;
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt) {
-    float av[4][4];
+    float av[4][CT];
     if (POST != 0) {
 #pragma unroll
       for (int v = 0; v < 4; ++v)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < CT; ++c) {
           const int row = row0 + 16 * rt + v;
-          av[v][c] = (full || row < a.m) ? load_elem(aux, (size_t)row * a.n + col0 + 16 * c) : 0.0f;
+          av[v][c] = (full || row < a.m) && c < nct ? load_elem(aux, (size_t)row * a.n + col0 + 16 * c) : 0.0f;
         }
     }
 #pragma unroll
@@ -1313,7 +1314,9 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
       if (!full && row >= a.m)
         continue;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < CT; ++c) {
+        if (c >= nct)
+          continue;
         float acc_v = acc[rt][c][v] * rs[rt][v];
         if (sizeof(OutT) == 2)
           acc_v = round_half(acc_v);
@@ -2238,40 +2241,481 @@ __global__ __launch_bounds__(64 * W) void typed_gemv_persistent_kernel(GemvArgs 
   }
 }
 
-// One workgroup of 64 lanes per tile-block: lane 16g + i writes its 64
-// weights (decode_lane) as fp16 into row 16c + i of out [n, k], eight
-// consecutive k per 16-byte store.
-template <uint32_t TYPE>
-__global__ __launch_bounds__(64) void typed_dequant_kernel(const uint8_t* __restrict__ w, _Float16* __restrict__ out, uint32_t nb, uint32_t k) {
-  const size_t tb = blockIdx.x;
-  const uint32_t c = (uint32_t)(tb / nb), b = (uint32_t)(tb % nb);
-  const int lane = threadIdx.x, g = lane >> 4, i = lane & 15;
-  float v[64];
-  decode_lane(TYPE, w + tb * 16 * (size_t)type_block_bytes(TYPE), lane, v);
-  _Float16* row = out + (size_t)(16 * c + i) * k + 256 * (size_t)b + 64 * g;
-#pragma unroll
-  for (int fs = 0; fs < 8; ++fs) {
-    h8_t h;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      h[e] = (_Float16)v[8 * fs + e];
-    *reinterpret_cast<h8_t*>(row + 32 * (fs >> 2) + 8 * (fs & 3)) = h;
-  }
+// ----------------------------------------------------------------------------
+// Prefill GEMM for the other weight types (Q5_K, Q6_K, Q8_0, IQ4_XS).
+//
+// The pipelined GEMM of the Q4_K path with its B operand taken from a policy
+// of the type's tile-block (layouts in q4k_internal.h): the same A ring over
+// the activations in the GEMM staging order, a private 2-block B ring per
+// wave filled by LDS-DMA, and per u-step u the B fragments of MFMA fs = u
+// (low) and fs = 4 + u (high) of each column tile dequantised in registers to
+// the reference's prefill tile value (quant_linear.metal:49-115): its fp32
+// expression rounded once to fp16, bit for bit.
+//   Q5_K   h(d*sc*(q + 16h) - dmin*m): q + 16h as an exact fp16 integer, then
+//          one fp32 fma with d*sc and -dmin*m (both exact), the single fp32
+//          rounding of the reference's expression.
+//   Q6_K   h(d*sc*(q - 32)): the product has at most 23 significant bits, so
+//          fma(64 + q, d*sc, -96 d*sc) is exact.
+//   Q8_0   h(d*q): 19 bits; one fp16 multiply rounds the exact product once.
+//   IQ4_XS h(d*(ls - 32)*v): 23 bits; fma(1152 + v, dl, -1152 dl) is exact.
+// Per type: kCT column tiles per wave and kAS A ring slots (A loaded kAS - 1
+// u-steps ahead), so that both rings fit the 160 KB of LDS; kNL DMA loads per
+// tile-block.  Column tiles past n (a multiple of 16, not of the workgroup's
+// width) load the last tile and store nothing.
+// ----------------------------------------------------------------------------
+
+// Bit `from` (and from + 16) of h moved to bit `to` (and to + 16).
+__device__ __forceinline__ uint32_t move_bits(uint32_t h, int from, int to) {
+  return from >= to ? h >> (from - to) : h << (to - from);
 }
 
-// y = post(c * rowscale[row], aux) over [m, n], the rounding points of the
-// GEMM epilogue (fp16: the accumulator rounded before the post operation).
-template <typename OutT>
-__global__ __launch_bounds__(256) void gemm_post_kernel(const float* __restrict__ c, const float* __restrict__ rowscale, OutT* y, const OutT* aux,
-                                                        int m, int n, int post) {
-  const size_t total = (size_t)m * n;
-  for (size_t o = (size_t)blockIdx.x * 256 + threadIdx.x; o < total; o += (size_t)gridDim.x * 256) {
-    const int row = (int)(o / (size_t)n);
-    float acc_v = c[o] * rowscale[row];
-    if (sizeof(OutT) == 2)
-      acc_v = round_half(acc_v);
-    const float out = post == 1 ? acc_v + load_elem(aux, o) : post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
-    store_elem(y, o, out);
+// Two fp32 values rounded to one fp16 pair.  The empty asm keeps the fp32
+// results apart from the conversion (fused, they become a dependent pair of
+// half-register writes).
+__device__ __forceinline__ uint32_t pack_h2(float a0, float a1) {
+  asm("" : "+v"(a0), "+v"(a1));
+  return as_u32(h2_t{(_Float16)a0, (_Float16)a1});
+}
+
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+
+struct TgQ5K {
+  static constexpr int kTB = kTileN * kQ5BlockBytes, kCT = 4, kAS = 4, kNL = 5, kVPM = 4;
+  struct R {
+    u4_t hd;
+    uint2 h;
+  };
+  struct K {
+    float dl, cl, dh, ch;
+    uint32_t h0, h1;
+  };
+  struct W {
+    uint2 q;
+  };
+  static __device__ __forceinline__ void issue(const uint8_t* src, uint32_t v16, uint32_t v4, uint32_t l, int) {
+    lds_dma16<0>(src, v16, l);
+    lds_dma16<kSlabBytes>(src, v16, l);
+    lds_dma4<kHeaderOffset>(src, v4, l);
+    lds_dma4<2304>(src, v4, l);
+    lds_dma4<2560>(src, v4, l);
+  }
+  static __device__ __forceinline__ void raw(R& r, const uint8_t* tb, int lane) {
+    r.hd = *reinterpret_cast<const u4_t*>(tb + kHeaderOffset + 16 * (lane & 15));
+    r.h = *reinterpret_cast<const uint2*>(tb + 2304 + 8 * lane);
+  }
+  // Sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles): d * sc and -dmin * m.
+  static __device__ __forceinline__ void consts(K& k, const R& r, int lane) {
+    uint32_t p0, p1;
+    scale_min_packed(r.hd, lane >> 4, p0, p1);
+    const float d = half_bits_to_float(r.hd.x & 0xffffu), dm = half_bits_to_float(r.hd.x >> 16);
+    k.dl = d * (float)(p0 & 0xffu);
+    k.cl = -dm * (float)((p0 >> 16) & 0xffu);
+    k.dh = d * (float)(p1 & 0xffu);
+    k.ch = -dm * (float)((p1 >> 16) & 0xffu);
+    k.h0 = r.h.x;
+    k.h1 = r.h.y;
+  }
+  static __device__ __forceinline__ void words(W& w, const uint8_t* tb, int u, int lane) {
+    w.q = *reinterpret_cast<const uint2*>(tb + (u >> 1) * kSlabBytes + 16 * lane + 8 * (u & 1));
+  }
+  // B dword t of MFMA u (low nibbles): fifth bits at bit 4u + t (+16) of h0;
+  // of MFMA 4 + u (high nibbles): the same bits of h1.  The value is formed
+  // as fp16 1024 + q + 16h (low nibble at bit 0, fifth bit at bit 4) or
+  // 64 + q + 16h (nibble at bits 4..7, fifth bit at bit 8), and the bias
+  // removed exactly.
+  static __device__ __forceinline__ void dequant(const K& k, const W& w, int u, h8_t& blo, h8_t& bhi) {
+    const uint32_t lw[4] = {w.q.x, w.q.x >> 8, w.q.y, w.q.y >> 8};
+    u4_t lo, hi;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t vl = and_or(lw[t], 0x000F000Fu, and_or(move_bits(k.h0, 4 * u + t, 4), 0x00100010u, 0x64006400u));
+      const uint32_t vh = and_or(lw[t], 0x00F000F0u, and_or(move_bits(k.h1, 4 * u + t, 8), 0x01000100u, 0x54005400u));
+      const h2_t ql = as_h2(vl) + h2_splat(-1024.0f), qh = as_h2(vh) + h2_splat(-64.0f);
+      lo[t] = pack_h2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl));
+      hi[t] = pack_h2(__builtin_fmaf((float)qh[0], k.dh, k.ch), __builtin_fmaf((float)qh[1], k.dh, k.ch));
+    }
+    blo = __builtin_bit_cast(h8_t, lo);
+    bhi = __builtin_bit_cast(h8_t, hi);
+  }
+};
+
+struct TgQ6K {
+  static constexpr int kTB = kQ6TileBlockBytes, kCT = 4, kAS = 3, kNL = 5, kVPM = 3;
+  struct R {
+    uint32_t sc, d;
+  };
+  struct K {
+    float d;
+    uint32_t sc;
+  };
+  // Triples u / 2 (MFMA u) and 2 + u / 2 (MFMA 4 + u); C only for odd u.
+  struct W {
+    uint32_t a0, b0, c0, a1, b1, c1;
+  };
+  static __device__ __forceinline__ void issue(const uint8_t* src, uint32_t v16, uint32_t v4, uint32_t l, int lane) {
+    lds_dma16<0>(src, v16, l);
+    lds_dma16<1024>(src, v16, l);
+    lds_dma16<2048>(src, v16, l);
+    lds_dma4<kQ6ScaleOffset>(src, v4, l);
+    if (lane < 8)  // the 16 rows' d: 32 bytes
+      lds_dma4<kQ6DOffset>(src, v4, l);
+  }
+  static __device__ __forceinline__ void raw(R& r, const uint8_t* tb, int lane) {
+    r.sc = lds_u32(tb + kQ6ScaleOffset + 4 * lane);
+    r.d = *reinterpret_cast<const uint16_t*>(tb + kQ6DOffset + 2 * (lane & 15));
+  }
+  static __device__ __forceinline__ void consts(K& k, const R& r, int) {
+    k.d = half_bits_to_float(r.d);
+    k.sc = r.sc;
+  }
+  static __device__ __forceinline__ uint32_t dword(const uint8_t* tb, int j, int lane) {
+    return lds_u32(tb + (j >> 2) * 1024 + 16 * lane + 4 * (j & 3));
+  }
+  static __device__ __forceinline__ void words(W& w, const uint8_t* tb, int u, int lane) {
+    const int a = 3 * (u >> 1);
+    w.a0 = dword(tb, a, lane);
+    w.b0 = dword(tb, a + 1, lane);
+    w.a1 = dword(tb, a + 6, lane);
+    w.b1 = dword(tb, a + 7, lane);
+    w.c0 = (u & 1) ? dword(tb, a + 2, lane) : 0u;
+    w.c1 = (u & 1) ? dword(tb, a + 8, lane) : 0u;
+  }
+  // Outputs 8a + 4p .. 8a + 4p + 3 of triple (A, B, C) (p = u & 1) as fp16
+  // 64 + q (bias 0x5400: bit 4 of a half is 1), then d*sc*(q - 32) exactly.
+  static __device__ __forceinline__ h8_t triple(uint32_t A, uint32_t B, uint32_t C, int p, float ds) {
+    const uint32_t m6 = 0x03F003F0u, m4 = 0x00F000F0u, m2 = 0x03000300u, bias = 0x54005400u;
+    uint32_t o[4];
+    if (p == 0) {
+      o[0] = and_or(A, m6, bias);
+      o[1] = and_or(A >> 6, m6, bias);
+      o[2] = and_or(B, m6, bias);
+      o[3] = and_or(B >> 6, m6, bias);
+    } else {
+      o[0] = and_or(C, m6, bias);
+      o[1] = and_or(C >> 6, m6, bias);
+      o[2] = and_or(A << 4, m4, and_or(B << 8, m2, bias));
+      o[3] = and_or(C << 4, m4, and_or(B << 6, m2, bias));
+    }
+    const float c = -96.0f * ds;
+    u4_t r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const h2_t q = as_h2(o[t]);
+      r[t] = pack_h2(__builtin_fmaf((float)q[0], ds, c), __builtin_fmaf((float)q[1], ds, c));
+    }
+    return __builtin_bit_cast(h8_t, r);
+  }
+  // Scale of MFMA u: byte u / 2 of the lane's scale dword (stored sc + 128);
+  // of MFMA 4 + u: byte 2 + u / 2.  d * sc = fma(sc + 128, d, -128 d), exact.
+  static __device__ __forceinline__ void dequant(const K& k, const W& w, int u, h8_t& blo, h8_t& bhi) {
+    const float m128 = -128.0f * k.d;
+    const float dsl = __builtin_fmaf((float)((k.sc >> (8 * (u >> 1))) & 0xffu), k.d, m128);
+    const float dsh = __builtin_fmaf((float)((k.sc >> (8 * (2 + (u >> 1)))) & 0xffu), k.d, m128);
+    blo = triple(w.a0, w.b0, w.c0, u & 1, dsl);
+    bhi = triple(w.a1, w.b1, w.c1, u & 1, dsh);
+  }
+};
+
+struct TgQ8_0 {
+  static constexpr int kTB = kTileN * kQ8BlockBytes, kCT = 2, kAS = 5, kNL = 5, kVPM = 3;
+  struct R {
+    uint32_t dd;
+  };
+  struct K {
+    h2_t dl, dh;
+  };
+  struct W {
+    uint2 lo, hi;
+  };
+  static __device__ __forceinline__ void issue(const uint8_t* src, uint32_t v16, uint32_t v4, uint32_t l, int) {
+    lds_dma16<0>(src, v16, l);
+    lds_dma16<1024>(src, v16, l);
+    lds_dma16<2048>(src, v16, l);
+    lds_dma16<3072>(src, v16, l);
+    lds_dma4<0>(src + 4096, v4, l + 4096);  // past the instruction offset's range
+  }
+  static __device__ __forceinline__ void raw(R& r, const uint8_t* tb, int lane) {
+    r.dd = lds_u32(tb + 4096 + 4 * lane);
+  }
+  // d of records 2g (MFMAs 0..3) and 2g + 1 (MFMAs 4..7), in both halves.
+  static __device__ __forceinline__ void consts(K& k, const R& r, int) {
+    k.dl = as_h2(__builtin_amdgcn_perm(r.dd, r.dd, 0x01000100u));
+    k.dh = as_h2(__builtin_amdgcn_perm(r.dd, r.dd, 0x03020302u));
+  }
+  static __device__ __forceinline__ void words(W& w, const uint8_t* tb, int u, int lane) {
+    w.lo = *reinterpret_cast<const uint2*>(tb + (u >> 1) * 1024 + 16 * lane + 8 * (u & 1));
+    w.hi = *reinterpret_cast<const uint2*>(tb + (2 + (u >> 1)) * 1024 + 16 * lane + 8 * (u & 1));
+  }
+  // Byte q ^ 0x80 as fp16 1024 + (q + 128), minus 1152 (exact), times d.
+  static __device__ __forceinline__ h8_t frag(uint2 v, h2_t d) {
+    auto q = [&](uint32_t x, uint32_t sel) { return as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, x, sel)) + h2_splat(-1152.0f)) * d); };
+    return __builtin_bit_cast(h8_t, u4_t{q(v.x, 0x04010400u), q(v.x, 0x04030402u), q(v.y, 0x04010400u), q(v.y, 0x04030402u)});
+  }
+  static __device__ __forceinline__ void dequant(const K& k, const W& w, int, h8_t& blo, h8_t& bhi) {
+    blo = frag(w.lo, k.dl);
+    bhi = frag(w.hi, k.dh);
+  }
+};
+
+struct TgIQ4XS {
+  static constexpr int kTB = kTileN * kIQ4BlockBytes, kCT = 4, kAS = 5, kNL = 3, kVPM = 4;
+  struct R {
+    uint2 hd;
+  };
+  struct K {
+    float dl, cl, dh, ch;
+  };
+  struct W {
+    uint32_t lo, hi;
+  };
+  static __device__ __forceinline__ void issue(const uint8_t* src, uint32_t v16, uint32_t v4, uint32_t l, int lane) {
+    lds_dma16<0>(src, v16, l);
+    lds_dma16<1024>(src, v16, l);
+    if (lane < 32)  // the 16 rows' 8-byte headers: 128 bytes
+      lds_dma4<2048>(src, v4, l);
+  }
+  static __device__ __forceinline__ void raw(R& r, const uint8_t* tb, int lane) {
+    r.hd = *reinterpret_cast<const uint2*>(tb + 2048 + 8 * (lane & 15));
+  }
+  // Sub-blocks 2g (MFMAs 0..3) and 2g + 1 (4..7): dl = d * (ls - 32) and
+  // -1152 dl, both exact.
+  static __device__ __forceinline__ void consts(K& k, const R& r, int lane) {
+    const int j = 2 * (lane >> 4);
+    const uint32_t sh = r.hd.x >> 16, sl = r.hd.y;
+    const float d = half_bits_to_float(r.hd.x & 0xffffu);
+    const int ls0 = (int)(((sl >> (4 * j)) & 15u) | (((sh >> (2 * j)) & 3u) << 4));
+    const int ls1 = (int)(((sl >> (4 * j + 4)) & 15u) | (((sh >> (2 * j + 2)) & 3u) << 4));
+    k.dl = d * (float)(ls0 - 32);
+    k.cl = -1152.0f * k.dl;
+    k.dh = d * (float)(ls1 - 32);
+    k.ch = -1152.0f * k.dh;
+  }
+  static __device__ __forceinline__ void words(W& w, const uint8_t* tb, int u, int lane) {
+    w.lo = lds_u32(tb + 16 * lane + 4 * u);
+    w.hi = lds_u32(tb + 1024 + 16 * lane + 4 * u);
+  }
+  // Codebook value + 128 per byte (FmtIQ4XS::lookup) as fp16 1152 + v, then
+  // dl * v exactly.
+  static __device__ __forceinline__ h8_t frag(uint32_t wq, float dl, float cl) {
+    const uint32_t vlo = FmtIQ4XS::lookup(wq), vhi = FmtIQ4XS::lookup(wq >> 4);
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, vlo, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, vlo, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, vhi, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, vhi, 0x04030402u)};
+    u4_t r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const h2_t v = as_h2(p[t]);
+      r[t] = pack_h2(__builtin_fmaf((float)v[0], dl, cl), __builtin_fmaf((float)v[1], dl, cl));
+    }
+    return __builtin_bit_cast(h8_t, r);
+  }
+  static __device__ __forceinline__ void dequant(const K& k, const W& w, int, h8_t& blo, h8_t& bhi) {
+    blo = frag(w.lo, k.dl, k.cl);
+    bhi = frag(w.hi, k.dh, k.ch);
+  }
+};
+
+// Load accounting of the typed GEMM.  A wave issues per u-step its 4 A
+// fragments of A(t + kAS - 1) spread over its kCT column groups, each group's
+// share followed, at u = 0, by the kNL loads of that column's tile-block of
+// the next block.  vmcnt is in order, so A(t) has landed once no more than
+// the loads issued after its last fragment are outstanding.
+constexpr int tg_mod4(int v) {
+  return ((v % 4) + 4) % 4;
+}
+constexpr int tg_step_loads(int u, int ct, int nl) {
+  return 4 + (u == 0 ? ct * nl : 0);
+}
+// Loads issued after A(t)'s last fragment (issued at u-step t - ad) up to the
+// top of u-step t, u = t % 4; at u = 3 also no more than the 8 loads of
+// u-steps 1 and 2, which follow the next block's B (issued at u = 0).
+constexpr int tg_wait(int u, int ad, int ct, int nl) {
+  int n = tg_mod4(u - ad) == 0 ? nl : 0;
+  for (int j = 1; j < ad; ++j)
+    n += tg_step_loads(tg_mod4(u - j), ct, nl);
+  return u == 3 && n > 8 ? 8 : n;
+}
+// In the first block A(1 .. ad - 1) come from the prologue (after B(0), before
+// any u-step): the steady-state wait must not exceed the loads that really
+// follow them there.  (A(0) is waited for by the prologue itself.)
+constexpr bool tg_first_block_ok(int ad, int ct, int nl) {
+  for (int t = 1; t < ad && t < 4; ++t) {
+    int after = 4 * (ad - 1 - t);
+    for (int s = 0; s < t; ++s)
+      after += tg_step_loads(s % 4, ct, nl);
+    if (after < tg_wait(t, ad, ct, nl))
+      return false;
+  }
+  return true;
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One 128 x (64 kCT) output tile (column block bx, row block by); ntiles =
+// n / 16.  The step structure is the Q4_K GEMM's: the LDS reads of a u-step
+// first (the 16 A fragments, at u = 3 the next block's per-column data, the
+// raw B words of u-step t + 1), then per column tile its 16 MFMAs with the
+// dequantisation of the previous column for u-step t + 1 under them (the
+// last column's under the first column of the next u-step).
+template <class P, typename OutT>
+__device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles) {
+  constexpr int CT = P::kCT, AS = P::kAS, AD = AS - 1, NL = P::kNL, TB = P::kTB;
+  static_assert(tg_first_block_ok(AD, CT, NL), "first-block load accounting");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = a.nb, steps = 4 * nb;
+  const int mt0 = by * (kG2M / 16);
+  const int ct0 = bx * (4 * CT) + CT * wave;
+  const uint32_t aring = lds_addr(lds);
+  uint8_t* const bring = lds + AS * kG2ASlot + wave * (2 * CT * TB);
+  const uint32_t bring0 = lds_addr(bring);
+  const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
+  const _Float16* const xh = a.xh;
+
+  auto issue_a = [&](int t, int i) {
+    const int tc = t < steps ? t : steps - 1;
+    const int b = tc >> 2, u = tc & 3;
+    const int f = 4 * wave + i;
+    const _Float16* src = xh + ((((size_t)by * nb + b) * 4 + u) * 16 + f) * 512;
+    const uint32_t l = __builtin_amdgcn_readfirstlane(aring + (uint32_t)(t % AS) * kG2ASlot + (uint32_t)f * 1024);
+    lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
+  };
+  auto issue_b = [&](int blk, int c) {
+    const int bc = blk < nb ? blk : nb - 1;
+    const int ct = ct0 + c < ntiles ? ct0 + c : ntiles - 1;
+    const uint8_t* src = uniform_ptr(a.w + ((size_t)ct * nb + bc) * TB);
+    const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * CT + c) * TB);
+    P::issue(src, voff16, voff4, l, lane);
+  };
+
+  f4_t acc[8][CT];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      acc[rt][c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      asm volatile("" : "+a"(acc[rt][c]));
+    }
+
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+    issue_b(0, c);
+#pragma unroll
+  for (int t = 0; t < AD; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      issue_a(t, i);
+  vm_wait<4 * (AD - 1)>();  // B(0) and A(0)
+  typename P::K kk[CT];
+  h8_t bclo[CT], bchi[CT];
+  typename P::W wl;  // raw words of the last column for the current u-step
+  {
+    typename P::R r[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      P::raw(r[c], bring + c * TB, lane);
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      P::consts(kk[c], r[c], lane);
+#pragma unroll
+    for (int c = 0; c < CT - 1; ++c) {
+      typename P::W w;
+      P::words(w, bring + c * TB, 0, lane);
+      P::dequant(kk[c], w, 0, bclo[c], bchi[c]);
+    }
+    P::words(wl, bring + (CT - 1) * TB, 0, lane);
+  }
+  for (int blk = 0; blk < nb; ++blk) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * blk + u;
+      if (u == 0)
+        vm_wait<tg_wait(0, AD, CT, NL)>();
+      else if (u == 1)
+        vm_wait<tg_wait(1, AD, CT, NL)>();
+      else if (u == 2)
+        vm_wait<tg_wait(2, AD, CT, NL)>();
+      else
+        vm_wait<tg_wait(3, AD, CT, NL)>();
+      __syncthreads();  // A(t) of every wave landed; u-step t - 1 fully read
+      __builtin_amdgcn_sched_barrier(0);
+      const int bn = u == 3 ? blk + 1 : blk, un = (u + 1) & 3;
+      const uint8_t* aslot = lds + (size_t)(t % AS) * kG2ASlot;
+      h8_t af[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        af[i] = *reinterpret_cast<const h8_t*>(aslot + i * 1024 + 16 * lane);
+      const uint8_t* bslot = bring + (size_t)((bn & 1) * CT) * TB;
+      typename P::R r[CT];
+      if (u == 3) {
+#pragma unroll
+        for (int c = 0; c < CT; ++c)
+          P::raw(r[c], bslot + c * TB, lane);
+      }
+      typename P::W wv[CT];
+#pragma unroll
+      for (int c = 0; c < CT; ++c)
+        P::words(wv[c], bslot + c * TB, un, lane);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        if (c == 0)
+          P::dequant(kk[CT - 1], wl, u, bclo[CT - 1], bchi[CT - 1]);
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt], bclo[c], acc[rt][c], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt + 1], bchi[c], acc[rt][c], 0, 0, 0);
+        if (u == 3)
+          P::consts(kk[c], r[c], lane);
+        if (c > 0)
+          P::dequant(kk[c - 1], wv[c - 1], un, bclo[c - 1], bchi[c - 1]);
+#pragma unroll
+        for (int i = 4 * c / CT; i < 4 * (c + 1) / CT; ++i)
+          issue_a(t + AD, i);
+        if (u == 0)
+          issue_b(blk + 1, c);
+      }
+      wl = wv[CT - 1];
+      __builtin_amdgcn_sched_group_barrier(0x100, 64, 0);
+#pragma unroll
+      for (int i = 0; i < 16 * CT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, P::kVPM, 0);
+      }
+    }
+  }
+  vm_wait<0>();
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      asm volatile("" : "+a"(acc[rt][c]));
+
+  const bool full = mt0 * 16 + kG2M <= a.m;
+  const int nct = ntiles - ct0 >= CT ? CT : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
+  if (a.post == 0)
+    full ? gemm2_epilogue<OutT, 0, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 0, false, CT>(a, acc, mt0, ct0, lane, nct);
+  else if (a.post == 1)
+    full ? gemm2_epilogue<OutT, 1, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 1, false, CT>(a, acc, mt0, ct0, lane, nct);
+  else
+    full ? gemm2_epilogue<OutT, 2, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 2, false, CT>(a, acc, mt0, ct0, lane, nct);
+}
+
+// Persistent over the (column block, row block) tiles, as the Q4_K GEMM.
+template <class P, typename OutT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void typed_gemm_kernel(GemmArgs a, int tiles_x, int tiles, int ntiles) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[P::kAS * kG2ASlot + 4 * 2 * P::kCT * P::kTB];
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    if (tile != (int)blockIdx.x)
+      __syncthreads();
+    typed_gemm_tile<P, OutT>(a, lds, tile % tiles_x, tile / tiles_x, ntiles);
   }
 }
 
@@ -2708,42 +3152,36 @@ hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, in
   }
 }
 
-hipError_t launch_typed_dequant(hipStream_t s, const uint8_t* w, uint32_t type, uint32_t n, uint32_t k, _Float16* out) {
-  const uint32_t nb = k / 256;
-  const size_t tiles = (size_t)(n / 16) * nb;
-  if (tiles == 0)
-    return hipSuccess;
-  const dim3 grid((unsigned)tiles), block(64);
-  switch (type) {
-    case kTypeQ6_K:
-      (void)dispatch(typed_dequant_kernel<kTypeQ6_K>, grid, block, s, w, out, nb, k);
-      break;
-    case kTypeQ8_0:
-      (void)dispatch(typed_dequant_kernel<kTypeQ8_0>, grid, block, s, w, out, nb, k);
-      break;
-    case kTypeQ5_K:
-      (void)dispatch(typed_dequant_kernel<kTypeQ5_K>, grid, block, s, w, out, nb, k);
-      break;
-    case kTypeIQ4_XS:
-      (void)dispatch(typed_dequant_kernel<kTypeIQ4_XS>, grid, block, s, w, out, nb, k);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
+template <class P>
+hipError_t typed_gemm_launch(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
+  const int ntiles = a.n / 16, tiles_x = (ntiles + 4 * P::kCT - 1) / (4 * P::kCT);
+  const int tiles = tiles_x * ((a.m + kG2M - 1) / kG2M);
+  const dim3 grid((unsigned)(tiles > cus ? cus : tiles)), block(256);
+  if (dtype == kF32)
+    (void)dispatch(typed_gemm_kernel<P, float>, grid, block, s, a, tiles_x, tiles, ntiles);
+  else
+    (void)dispatch(typed_gemm_kernel<P, _Float16>, grid, block, s, a, tiles_x, tiles, ntiles);
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_post(hipStream_t s, const float* c, const float* rowscale, void* y, const void* aux, int m, int n, int post, int dtype) {
-  const size_t total = (size_t)m * n;
-  const unsigned grid = (unsigned)((total + 255) / 256 < 16384 ? (total + 255) / 256 : 16384);
-  if (total == 0)
-    return hipSuccess;
-  if (dtype == kF32)
-    (void)dispatch(gemm_post_kernel<float>, dim3(grid), dim3(256), s, c, rowscale, static_cast<float*>(y), static_cast<const float*>(aux), m, n, post);
-  else
-    (void)dispatch(gemm_post_kernel<_Float16>, dim3(grid), dim3(256), s, c, rowscale, static_cast<_Float16*>(y), static_cast<const _Float16*>(aux), m,
-                   n, post);
-  return hipGetLastError();
+bool typed_gemm_supported(uint32_t type, int m, int n) {
+  const bool served = type == kTypeQ5_K || type == kTypeQ6_K || type == kTypeQ8_0 || type == kTypeIQ4_XS;
+  return served && m > 0 && n > 0 && n % 16 == 0;
+}
+
+hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, int dtype, int cus) {
+  if (!typed_gemm_supported(type, a.m, a.n) || a.nb < 1)
+    return hipErrorInvalidValue;
+  switch (type) {
+    case kTypeQ5_K:
+      return typed_gemm_launch<TgQ5K>(s, a, dtype, cus);
+    case kTypeQ6_K:
+      return typed_gemm_launch<TgQ6K>(s, a, dtype, cus);
+    case kTypeQ8_0:
+      return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);
+    default:
+      return typed_gemm_launch<TgIQ4XS>(s, a, dtype, cus);
+  }
 }
 
 hipError_t launch_typed_relayout(hipStream_t s, const uint8_t* src, uint8_t* dst, uint32_t n, uint32_t k, uint32_t type) {

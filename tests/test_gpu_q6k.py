@@ -76,7 +76,7 @@ def test_q6k_fp16(q4k, oracle, gpu, m, post):
 
 def test_q6k_prefill_groups_and_kernel_names(q4k, oracle, gpu):
     W, _, _ = _linear(q4k, oracle, gpu, 730, 64, 512, 2048, counts=None)
-    assert W.kernel_name(1) == "linear_q6_k_k2048_n512_prefill_fp16_gemm"
+    assert W.kernel_name(1) == "linear_q6_k_k2048_n512_prefill_mfma16x16x32"
     W2, _, _ = _linear(q4k, oracle, gpu, 731, 8, 512, 2048, counts=[4, 4])
     assert W2.kernel_name(0) == "linear_q6_k_k2048_n512_decode_mfma16x16x32"
     _linear(q4k, oracle, gpu, 732, 21, 256, 1024, counts=[7, 14])  # prefill: groups of 8, 8, 5

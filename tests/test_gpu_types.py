@@ -14,7 +14,10 @@ upload (bit-identical to the host one); the gated projection (one fused
 launch for Q5_K and IQ4_XS in the decode phase, with and without the
 ffn_norm); a GGUF file;
 and, for every non-Q4_K type, prefill batches of 64 rows and more (the
-dequantised fp16 GEMM) with post 0 / 1 / 2 and fp16 activations.
+typed MFMA GEMM): M = 2048, ragged row and column tails (a workgroup with
+one live column tile, waves with none), one block of K, post 0 / 1 / 2 and
+fp16 activations, and one-hot rows that read single dequantised weights
+out, which must equal the oracle's fp32 value rounded to fp16 exactly.
 """
 import numpy as np
 import pytest
@@ -173,21 +176,53 @@ def test_tensor_from_gguf(q4k, oracle, gpu, tmp_path, t):
     assert row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k, ggml_type=t)) <= TOL
 
 
-# Prefill-sized batches (m >= 64) of the other types: x staged as fp16 rows,
-# the weights dequantised to fp16 (the reference's prefill tile values), one
-# rocBLAS GEMM, the library's epilogue.  Like the Q4_K GEMM, activations and
-# weights are single fp16 (expected row errors ~4e-4).
+# Prefill-sized batches (m >= 64) of the other types: x staged in the GEMM
+# order (fp16, power-of-two row scales), the type's MFMA GEMM dequantising
+# each weight to the reference's prefill tile value (fp16) in registers.  Like
+# the Q4_K GEMM, activations and weights are single fp16 (expected row errors
+# ~4e-4).  592 = 16 * 37 columns: the last workgroup has 5 live column tiles
+# (one wave with a single tile, Q8_0's 2-tile waves: one with one) and
+# waves with none.
 ALL_TYPES = TYPES + [14]
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 1024, 4096), (97, 2048, 2304), (200, 4096, 12288)])
+@pytest.mark.parametrize("m,n,k", [(64, 1024, 4096), (97, 2048, 2304), (200, 4096, 12288), (2048, 768, 2048), (130, 592, 256),
+                                   (300, 592, 1280)])
 @pytest.mark.parametrize("t", ALL_TYPES)
 def test_prefill_gemm(q4k, oracle, gpu, t, m, n, k):
     W, _ = _linear(q4k, oracle, gpu, t, 960 + m + t, m, n, k, counts=[m])
-    assert W.kernel_name(1).endswith("_prefill_fp16_gemm")
+    assert W.kernel_name(1).endswith("_prefill_mfma16x16x32")
 
 
 @pytest.mark.parametrize("post,dtype", [(1, torch.float32), (2, torch.float32), (0, torch.float16), (1, torch.float16)])
 @pytest.mark.parametrize("t", ALL_TYPES)
 def test_prefill_gemm_epilogues(q4k, oracle, gpu, t, post, dtype):
     _linear(q4k, oracle, gpu, t, 970 + post + t, 128, 1024, 4096, post=post, dtype=dtype, counts=[100, 28])
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_prefill_gemm_dequant_bit_exact(q4k, oracle, gpu, t):
+    """Row r of x is one-hot at element r of block r % nb, so y[r, j] is the
+    fp16 weight the GEMM formed for (j, that element) times 1: every element
+    position of a block, over all blocks, in 592 columns."""
+    m, n, k = 256, 592, 2048
+    nb = k // 256
+    rng = np.random.default_rng(990 + t)
+    w = make_weight(rng, n, k, t)
+    cols = np.arange(m) + 256 * (np.arange(m) % nb)
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), cols] = 1.0
+    W = q4k.Weight(w, n, k, ggml_type=t)
+    y = torch.full((m, n), float("nan"), device=gpu)
+    q4k.linear(_t(x, gpu), W, m, y, query_counts=[m])
+    torch.cuda.synchronize()
+    bb = w.shape[1] // nb
+    blocks = w.reshape(n, nb, bb)
+    expect = np.empty((m, n), np.float32)
+    for j in range(n):
+        deq = np.concatenate([oracle.dequant_block(blocks[j, b], t) for b in range(nb)])
+        expect[:, j] = deq[cols].astype(np.float16).astype(np.float32)
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    bad = np.argwhere(got != expect)  # exact (a zero weight may carry either sign)
+    assert bad.size == 0, f"type={t}: {len(bad)} weights differ, first (row, col) {bad[:4].tolist()}"
