@@ -53,9 +53,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--no-types", action="store_true", help="skip the Q8_0 / Q5_K / IQ4_XS LM-head timings")
+    ap.add_argument("--no-types", action="store_true", help="skip the Q8_0 / Q5_K / IQ4_XS LM-head and the typed prefill GEMM timings")
     ap.add_argument("--part", default="all",
-                    choices=["all", "decode", "prefill", "config2", "config3", "lm_head", "types", "shard", "neighbours"],
+                    choices=["all", "decode", "prefill", "config2", "config3", "lm_head", "types", "types_prefill", "shard", "neighbours"],
                     help="run one workload alone (for profiling runs that attribute kernel statistics to one configuration)")
     return ap.parse_args()
 
@@ -467,6 +467,62 @@ def types_bench(args, dev):
     return out
 
 
+def _random_typed(dev, n, k, t, seed):
+    """Random bytes of a GGUF tensor of type t with the fp16 scale fields
+    below 2^-7 (finite outputs)."""
+    import torch
+    import mtlqwen_amd as q4k
+
+    nb = k // 256
+    bb = q4k.q4k_nbytes(1, 256, t)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    raw = torch.randint(0, 256, (n * nb * bb,), dtype=torch.uint8, device=dev, generator=g)
+    if t == q4k.GGML_TYPE_Q8_0:
+        raw.view(n, nb * 8, 34)[:, :, 1] &= 0x1F
+    elif t == q4k.GGML_TYPE_Q6_K:
+        raw.view(n, nb, bb)[:, :, 209] &= 0x1F
+    else:
+        raw.view(n, nb, bb)[:, :, 1] &= 0x1F
+        if t == q4k.GGML_TYPE_Q5_K:
+            raw.view(n, nb, bb)[:, :, 3] &= 0x1F
+    return raw
+
+
+def types_prefill_bench(dev):
+    """The typed MFMA prefill GEMM at the config-4 shapes (M = 2048; gate
+    K = 4096 -> N = 12288 and down K = 12288 -> N = 4096), per launch with
+    dispatch-attached events."""
+    import torch
+    import mtlqwen_amd as q4k
+
+    M = 2048
+    out = {}
+    for name, t in (("q6_k", q4k.GGML_TYPE_Q6_K), ("q5_k", q4k.GGML_TYPE_Q5_K), ("q8_0", q4k.GGML_TYPE_Q8_0),
+                    ("iq4_xs", q4k.GGML_TYPE_IQ4_XS)):
+        res = {}
+        for shape, (n, k) in (("gate", (12288, 4096)), ("down", (4096, 12288))):
+            W = q4k.Weight(_random_typed(dev, n, k, t, 0x51A70040 + t + n), n, k, ggml_type=t)
+            x = torch.randn((M, k), device=dev, generator=torch.Generator(device=dev).manual_seed(0x51A70041 + t))
+            y = torch.empty((M, n), device=dev)
+            for _ in range(3):
+                q4k.linear(x, W, M, y, query_counts=[M])
+            torch.cuda.synchronize()
+            q4k.profile_enable(True)
+            for _ in range(10):
+                q4k.linear(x, W, M, y, query_counts=[M])
+            torch.cuda.synchronize()
+            gemm_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMM)
+            q4k.profile_enable(False)
+            tf = 2.0 * M * n * k / (gemm_ms * 1e-3) / 1e12
+            res[shape] = {"gemm_avg_us": round(gemm_ms * 1e3, 1), "tflops": round(tf, 1),
+                          "frac_of_peak": round(tf / FP16_DENSE_PEAK_TFLOPS, 4)}
+            W.close()
+            del x, y
+        out[name] = res
+        torch.cuda.empty_cache()
+    return out
+
+
 def prefill_bench(args, dev):
     import numpy as np
     import torch
@@ -645,6 +701,8 @@ def main():
             res["q4k_lm_head"], res["q6k_lm_head"] = lm_head_bench(dev, 12), lm_head_bench(dev, 14)
         elif args.part == "types":
             res["types_lm_head"] = types_bench(args, dev)
+        elif args.part == "types_prefill":
+            res["types_prefill"] = types_prefill_bench(dev)
         elif args.part == "shard":
             res["shard_1of8"] = shard_bench(args, dev)
         elif args.part == "neighbours":
@@ -660,6 +718,7 @@ def main():
     q4k_head = lm_head_bench(dev, 12) if want("lm_head") else None
     q6k = lm_head_bench(dev, 14) if want("lm_head") else None
     types = None if args.no_types or not want("types") else types_bench(args, dev)
+    types_pre = None if args.no_types or args.no_prefill or not want("types_prefill") else types_prefill_bench(dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     cpu = None if args.no_cpu else cpu_baseline(args)
@@ -711,6 +770,7 @@ def main():
         "q4k_lm_head": q4k_head,
         "q6k_lm_head": q6k,
         "types_lm_head": types,
+        "types_prefill": types_pre,
         "copy_ceiling_gbs": round(copy_gbs, 1),
         "mfma_ceiling_tflops": round(mfma_tf, 1),
         "cpu_baseline": cpu,

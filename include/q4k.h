@@ -136,10 +136,10 @@ int q4k_linear_norm(void* stream, q4k_weight* w, const float* norm_w, float eps,
  * decode pack (m <= 8, k <= 61440), 8 MiB of split-K partials, 4096 split-K
  * counters, 65536 row scales, and about 54 MiB of staged activations (e.g.
  * m * k <= 28.1 million for prefill, rows padded to 128).  A call needing
- * more fails with Q4K_ESHAPE and a message naming the buffer; prefill of 64
- * or more rows with weights other than Q4_K (a library GEMM) fails with
- * Q4K_ETYPE.  Calls allocate nothing (no hipMalloc, hipFree or allocating
- * library routine).  Every call on a GPU shares that GPU's array and leaves
+ * more fails with Q4K_ESHAPE and a message naming the buffer.  Every weight
+ * type is served, prefill included.  Calls allocate nothing (no hipMalloc,
+ * hipFree or allocating library routine).  Every call on a GPU shares that
+ * GPU's array and leaves
  * its contents behind: calls that overlap on one GPU (other streams or
  * threads) race; issue them in one stream order. */
 int q4k_linear_noalloc(void* stream, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, const uint32_t* query_counts,

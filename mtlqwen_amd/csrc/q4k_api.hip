@@ -551,9 +551,11 @@ int run_gemv_groups_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, con
   return Q4K_OK;
 }
 
+// Outputs narrower than kGemmMinColumns take the GEMV groups at every row
+// count, as with Q4_K (the per-row bar).
 int run_typed_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
                      uint32_t dtype, const float* norm_w, float eps) {
-  if (m >= kTypedGemmRows)
+  if (m >= kTypedGemmRows && w->n >= kGemmMinColumns)
     return run_typed_gemm_locked(stream, ws, w, x, y, aux, m, post, dtype, norm_w, eps);
   int rc = prenorm(stream, ws, w->device, x, norm_w, eps, m, w->k, dtype);
   if (rc)

@@ -1372,10 +1372,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     uint32_t p0, p1;
     scale_min_packed(hd, g, p0, p1);
     const float d = half_bits_to_float(hd.x & 0xffffu), dmin = half_bits_to_float(hd.x >> 16);
-    dsl[c] = d * (float)(p0 & 0xffu);
-    csl[c] = __builtin_fmaf(-1024.0f, dsl[c], -dmin * (float)((p0 >> 16) & 0xffu));
-    dsh[c] = d * (float)(p1 & 0xffu);
-    csh[c] = __builtin_fmaf(-64.0f, dsh[c], -dmin * (float)((p1 >> 16) & 0xffu));
+    dsl[c] = d * (float)(p0 & 0xffu) * 0x1p24f;
+    csl[c] = -dmin * (float)((p0 >> 16) & 0xffu);
+    dsh[c] = d * (float)(p1 & 0xffu) * 0x1p20f;
+    csh[c] = -dmin * (float)((p1 >> 16) & 0xffu);
   };
   // B fragments of column tile c from its two raw words (words 2(u & 1),
   // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants: the
@@ -1395,15 +1395,15 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   // The nibble masks and biases live in registers (VOP3 takes no literal on
   // this target), as plain values so that the scheduler sees the
   // v_and_or_b32 it selects as vector ALU work and interleaves it.
-  uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, b_lo = 0x64006400u, b_hi = 0x54005400u;
-  asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(b_lo), "+v"(b_hi));
+  uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
+  asm volatile("" : "+v"(m_lo), "+v"(m_hi));
   auto dequant_words = [&](int c, uint2 wv, h8_t& blo, h8_t& bhi) {
     const uint32_t lw[4] = {wv.x, wv.x >> 8, wv.y, wv.y >> 8};
     u4_t lo, hi;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const h2_t ql = as_h2((lw[e] & m_lo) | b_lo);
-      const h2_t qh = as_h2((lw[e] & m_hi) | b_hi);
+      const h2_t ql = as_h2(lw[e] & m_lo);
+      const h2_t qh = as_h2(lw[e] & m_hi);
       float a0 = __builtin_fmaf((float)ql[0], dsl[c], csl[c]), a1 = __builtin_fmaf((float)ql[1], dsl[c], csl[c]);
       float b0 = __builtin_fmaf((float)qh[0], dsh[c], csh[c]), b1 = __builtin_fmaf((float)qh[1], dsh[c], csh[c]);
       asm("" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
@@ -2310,9 +2310,9 @@ struct TgQ5K {
     uint32_t p0, p1;
     scale_min_packed(r.hd, lane >> 4, p0, p1);
     const float d = half_bits_to_float(r.hd.x & 0xffffu), dm = half_bits_to_float(r.hd.x >> 16);
-    k.dl = d * (float)(p0 & 0xffu);
+    k.dl = d * (float)(p0 & 0xffu) * 0x1p24f;
     k.cl = -dm * (float)((p0 >> 16) & 0xffu);
-    k.dh = d * (float)(p1 & 0xffu);
+    k.dh = d * (float)(p1 & 0xffu) * 0x1p20f;
     k.ch = -dm * (float)((p1 >> 16) & 0xffu);
     k.h0 = r.h.x;
     k.h1 = r.h.y;
@@ -2330,9 +2330,8 @@ struct TgQ5K {
     u4_t lo, hi;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const uint32_t vl = and_or(lw[t], 0x000F000Fu, and_or(move_bits(k.h0, 4 * u + t, 4), 0x00100010u, 0x64006400u));
-      const uint32_t vh = and_or(lw[t], 0x00F000F0u, and_or(move_bits(k.h1, 4 * u + t, 8), 0x01000100u, 0x54005400u));
-      const h2_t ql = as_h2(vl) + h2_splat(-1024.0f), qh = as_h2(vh) + h2_splat(-64.0f);
+      const h2_t ql = as_h2(and_or(lw[t], 0x000F000Fu, move_bits(k.h0, 4 * u + t, 4) & 0x00100010u));
+      const h2_t qh = as_h2(and_or(lw[t], 0x00F000F0u, move_bits(k.h1, 4 * u + t, 8) & 0x01000100u));
       lo[t] = pack_h2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl));
       hi[t] = pack_h2(__builtin_fmaf((float)qh[0], k.dh, k.ch), __builtin_fmaf((float)qh[1], k.dh, k.ch));
     }

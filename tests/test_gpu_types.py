@@ -200,12 +200,13 @@ def test_prefill_gemm_epilogues(q4k, oracle, gpu, t, post, dtype):
     _linear(q4k, oracle, gpu, t, 970 + post + t, 128, 1024, 4096, post=post, dtype=dtype, counts=[100, 28])
 
 
-@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("t", ALL_TYPES + [12])
 def test_prefill_gemm_dequant_bit_exact(q4k, oracle, gpu, t):
     """Row r of x is one-hot at element r of block r % nb, so y[r, j] is the
     fp16 weight the GEMM formed for (j, that element) times 1: every element
-    position of a block, over all blocks, in 592 columns."""
-    m, n, k = 256, 592, 2048
+    position of a block, over all blocks, in 592 columns (512 for Q4_K, whose
+    pipelined GEMM takes N in multiples of 256)."""
+    m, n, k = 256, 512 if t == 12 else 592, 2048
     nb = k // 256
     rng = np.random.default_rng(990 + t)
     w = make_weight(rng, n, k, t)

@@ -1,14 +1,15 @@
 """q4k_linear_noalloc (the entry point that allocates nothing) against
 q4k_linear through the C ABI: the same kernels on the same inputs, so the
 outputs must be identical, on two calls in a row (the second smaller) for
-every kernel family the entry point reaches; and its refusals."""
+every kernel family the entry point reaches, Q4_K and the other weight
+types' prefill GEMM; and its refusals."""
 import ctypes
 
 import numpy as np
 import pytest
 import torch
 
-from q4k_ref import make_q4k, make_weight, make_x, TYPE_Q6_K
+from q4k_ref import make_q4k, make_weight, make_x, TYPE_IQ4_XS, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -34,10 +35,20 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("label,n,k,first,second,post,dtype", CASES, ids=[c[0] for c in CASES])
-def test_noalloc_matches_linear(q4k, gpu, label, n, k, first, second, post, dtype):
+# The other weight types' prefill GEMM (and their per-8-row group GEMV below 64 rows).
+TYPED_CASES = [
+    ("Q6_K prefill GEMM", 1024, 4096, (300, [300]), (129, [129]), 1, torch.float32, TYPE_Q6_K),
+    ("Q8_0 prefill GEMM", 592, 2048, (200, [200]), (64, [64]), 0, torch.float16, TYPE_Q8_0),
+    ("Q5_K prefill GEMM then groups", 512, 2048, (130, [130]), (20, [20]), 2, torch.float32, TYPE_Q5_K),
+    ("IQ4_XS prefill GEMM", 768, 1024, (256, [256]), (65, [65]), 0, torch.float32, TYPE_IQ4_XS),
+]
+
+
+@pytest.mark.parametrize("label,n,k,first,second,post,dtype,t", [c + (TYPE_Q4_K,) for c in CASES] + TYPED_CASES,
+                         ids=[c[0] for c in CASES + TYPED_CASES])
+def test_noalloc_matches_linear(q4k, gpu, label, n, k, first, second, post, dtype, t):
     rng = np.random.default_rng(1300 + n % 97 + k % 89)
-    W = q4k.Weight(make_q4k(rng, n, k), n, k)
+    W = q4k.Weight(make_weight(rng, n, k, t), n, k, ggml_type=t)
     for m, counts in (first, second):
         x = torch.from_numpy(make_x(rng, m, k, 0.25)).to(gpu).to(dtype)
         aux0 = torch.from_numpy(make_x(rng, m, n, 0.5)).to(gpu).to(dtype) if post else None
@@ -60,9 +71,8 @@ def test_noalloc_refusals(q4k, gpu):
     rc = _noalloc(q4k, x, W, m, y)
     assert rc == -3
     assert "no-allocation scratch" in q4k.lib.q4k_last_error().decode()
-    # Prefill of 64+ rows with another type is a library GEMM: refused.
-    n, k, m = 256, 1024, 64
+    # The same for the other types' prefill GEMM.
     W6 = q4k.Weight(make_weight(rng, n, k, TYPE_Q6_K), n, k, ggml_type=TYPE_Q6_K)
-    rc = _noalloc(q4k, torch.zeros((m, k), device=gpu), W6, m, torch.zeros((m, n), device=gpu))
-    assert rc == -2 and "noalloc" in q4k.lib.q4k_last_error().decode()
+    rc = _noalloc(q4k, x, W6, m, y)
+    assert rc == -3 and "no-allocation scratch" in q4k.lib.q4k_last_error().decode()
     torch.cuda.synchronize()
