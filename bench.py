@@ -707,6 +707,8 @@ def main():
             res["shard_1of8"] = shard_bench(args, dev)
         elif args.part == "neighbours":
             res["neighbours"] = neighbours_bench(args, dev)
+        # the 1 GiB device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters
+        res["copy_ceiling_gbs"] = round(copy_ceiling(dev), 1)
         print(json.dumps(res), flush=True)
         return
 

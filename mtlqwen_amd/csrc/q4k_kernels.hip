@@ -1363,10 +1363,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   };
 
   // Block constants of the 4 column tiles, in fp32, from the 4 headers (this
-  // lane's column) of one block: for sub-block 2g (low nibbles) d * sc and
-  // -(1024 d * sc + dmin * m), for sub-block 2g + 1 (high nibbles) d * sc and
-  // -(64 d * sc + dmin * m).  d * sc and dmin * m are exact in fp32 (11-bit d
-  // times a 6-bit field).
+  // lane's column) of one block: for sub-block 2g (low nibbles) d * sc * 2^24
+  // and -dmin * m, for sub-block 2g + 1 (high nibbles) d * sc * 2^20 and
+  // -dmin * m.  All are exact in fp32 (11-bit d times a 6-bit field, times a
+  // power of two).
   float dsl[4], csl[4], dsh[4], csh[4];
   auto block_const = [&](int c, const u4_t& hd) {
     uint32_t p0, p1;
@@ -1380,21 +1380,17 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   // B fragments of column tile c from its two raw words (words 2(u & 1),
   // 2(u & 1) + 1 of slab u / 2 for u-step u), with the block constants: the
   // reference's prefill tile value h(d * sc * q - dmin * m), formed in fp32
-  // and rounded to fp16 once (quant_linear.metal:43,45).  (w & 0x000F000F) |
-  // 0x6400 is the fp16 value 1024 + q of two low nibbles, (w & 0x00F000F0) |
-  // 0x5400 the value 64 + q of two high nibbles; one v_fma_mix_f32 per weight
-  // then forms (B + q) * d * sc - (B d * sc + dmin * m) with the product exact
-  // and one rounding to fp32, and one v_cvt_pk_f16_f32 per pair rounds to
-  // fp16.  The bias B rides in the fp32 constant, so no instruction removes
-  // it; the constant itself is rounded to fp32 when B d * sc and dmin * m
-  // span more than 24 bits, which moves about 0.8 % of the weights by one
-  // fp16 ulp against the reference's value (numpy model of the benchmark's
-  // weights).  The empty asm keeps the fp32 results apart from the
-  // conversion: fused, they become v_fma_mixlo/mixhi_f16 pairs writing the
-  // two halves of one register, a dependent chain that measured 6 % slower.
-  // The nibble masks and biases live in registers (VOP3 takes no literal on
-  // this target), as plain values so that the scheduler sees the
-  // v_and_or_b32 it selects as vector ALU work and interleaves it.
+  // and rounded to fp16 once (quant_linear.metal:43,45), bit for bit.
+  // w & 0x000F000F puts two low nibbles into the low bits of two fp16
+  // halves: the denormals q * 2^-24 (w & 0x00F000F0: 16 q * 2^-24 for two
+  // high nibbles).  One v_fma_mix_f32 per weight, which takes fp16 denormal
+  // sources at their exact value, forms q * (d * sc * 2^24) - dmin * m (2^20
+  // for the high nibbles) with the product exact and one rounding to fp32,
+  // and one v_cvt_pk_f16_f32 per pair rounds to fp16.  The empty asm keeps
+  // the fp32 results apart from the conversion: fused, they become
+  // v_fma_mixlo/mixhi_f16 pairs writing the two halves of one register, a
+  // dependent chain that measured 6 % slower.  The nibble masks live in
+  // registers, as plain values that the scheduler sees as vector ALU work.
   uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
   asm volatile("" : "+v"(m_lo), "+v"(m_hi));
   auto dequant_words = [&](int c, uint2 wv, h8_t& blo, h8_t& bhi) {
@@ -2251,9 +2247,9 @@ __global__ __launch_bounds__(64 * W) void typed_gemv_persistent_kernel(GemvArgs 
 // (low) and fs = 4 + u (high) of each column tile dequantised in registers to
 // the reference's prefill tile value (quant_linear.metal:49-115): its fp32
 // expression rounded once to fp16, bit for bit.
-//   Q5_K   h(d*sc*(q + 16h) - dmin*m): q + 16h as an exact fp16 integer, then
-//          one fp32 fma with d*sc and -dmin*m (both exact), the single fp32
-//          rounding of the reference's expression.
+//   Q5_K   h(d*sc*(q + 16h) - dmin*m): q + 16h as an fp16 denormal (as the
+//          Q4_K nibbles), then one fp32 fma with d*sc*2^24 and -dmin*m (both
+//          exact), the single fp32 rounding of the reference's expression.
 //   Q6_K   h(d*sc*(q - 32)): the product has at most 23 significant bits, so
 //          fma(64 + q, d*sc, -96 d*sc) is exact.
 //   Q8_0   h(d*q): 19 bits; one fp16 multiply rounds the exact product once.
@@ -2305,7 +2301,8 @@ struct TgQ5K {
     r.hd = *reinterpret_cast<const u4_t*>(tb + kHeaderOffset + 16 * (lane & 15));
     r.h = *reinterpret_cast<const uint2*>(tb + 2304 + 8 * lane);
   }
-  // Sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles): d * sc and -dmin * m.
+  // Sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles): d * sc times
+  // 2^24 (2^20), and -dmin * m.
   static __device__ __forceinline__ void consts(K& k, const R& r, int lane) {
     uint32_t p0, p1;
     scale_min_packed(r.hd, lane >> 4, p0, p1);
@@ -2321,10 +2318,9 @@ struct TgQ5K {
     w.q = *reinterpret_cast<const uint2*>(tb + (u >> 1) * kSlabBytes + 16 * lane + 8 * (u & 1));
   }
   // B dword t of MFMA u (low nibbles): fifth bits at bit 4u + t (+16) of h0;
-  // of MFMA 4 + u (high nibbles): the same bits of h1.  The value is formed
-  // as fp16 1024 + q + 16h (low nibble at bit 0, fifth bit at bit 4) or
-  // 64 + q + 16h (nibble at bits 4..7, fifth bit at bit 8), and the bias
-  // removed exactly.
+  // of MFMA 4 + u (high nibbles): the same bits of h1.  The value is the fp16
+  // denormal (q + 16h) * 2^-24 (low nibble at bit 0, fifth bit at bit 4) or
+  // (q + 16h) * 2^-20 (nibble at bits 4..7, fifth bit at bit 8).
   static __device__ __forceinline__ void dequant(const K& k, const W& w, int u, h8_t& blo, h8_t& bhi) {
     const uint32_t lw[4] = {w.q.x, w.q.x >> 8, w.q.y, w.q.y >> 8};
     u4_t lo, hi;
