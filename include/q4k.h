@@ -193,6 +193,22 @@ int q4k_gather_rows(void* stream, const void* x, void* out, uint32_t k, const ui
  * overlap ids. */
 int q4k_embedding(void* stream, const q4k_weight* table, const int32_t* ids, uint32_t rows, void* y, uint32_t dtype);
 
+/* Token embedding of a packed batch, each row's token resolved in the kernel
+ * as embedding_q4_k does for a target query (quant_linear.metal:577-584,
+ * mode 0, with queryRow, batch.hpp:19-23; forward.cpp:125): query q owns
+ * counts[q] consecutive rows, starting at the sum of the counts before it,
+ * and row t of those takes token tokens[slots[q] * capacity + positions[q] +
+ * (t - start_q)] of the engine's request token buffer (a device array of
+ * int32, one row of `capacity` tokens per slot).  counts, positions and
+ * slots are host arrays of nqueries (1..64) entries; positions[q] +
+ * counts[q] must not exceed capacity.  Rows are dequantised as
+ * q4k_embedding's; *rows_out (if not NULL) receives the row count, the sum
+ * of counts.  The reference's drafter branches of the same kernel (DFlash
+ * mask rows, MTP proposals: modes 1 and 2, and mode 0 with a drafter state)
+ * stay with the engine.  y must not overlap tokens. */
+int q4k_embedding_batch(void* stream, const q4k_weight* table, const int32_t* tokens, uint32_t capacity, const uint32_t* counts,
+                        const uint32_t* positions, const uint32_t* slots, uint32_t nqueries, void* y, uint32_t dtype, uint32_t* rows_out);
+
 /* RMS norm (native_ops.metal:6-40 rms_norm; forward.cpp:82,114):
  * y[r] = x[r] * rsqrt(sum(x[r]^2) / k + eps) * w for m rows of k; w is a
  * device array of k fp32 weights (the reference uses eps = 1e-6,

@@ -70,6 +70,7 @@ def _load():
         "q4k_pack_queries": (c_int, [pu32, pu32, u32, pu32, pu32, pu32, pu32]),
         "q4k_gather_rows": (c_int, [p, p, p, u32, pu32, pu32, u32, u32, pu32]),
         "q4k_embedding": (c_int, [p, p, p, u32, p, u32]),
+        "q4k_embedding_batch": (c_int, [p, p, p, u32, pu32, pu32, pu32, u32, p, u32, pu32]),
         "q4k_rms_norm": (c_int, [p, p, p, p, u32, u32, ctypes.c_float, u32]),
         "q4k_rms_norm_gather": (c_int, [p, p, p, p, u32, pu32, pu32, u32, ctypes.c_float, u32, pu32]),
         "q4k_profile_enable": (c_int, [c_int]),

@@ -1321,6 +1321,50 @@ int q4k_embedding(void* stream, const q4k_weight* table, const int32_t* ids, uin
   return Q4K_OK;
 }
 
+int q4k_embedding_batch(void* stream, const q4k_weight* table, const int32_t* tokens, uint32_t capacity, const uint32_t* counts,
+                        const uint32_t* positions, const uint32_t* slots, uint32_t nqueries, void* y, uint32_t dtype, uint32_t* rows_out) {
+  if (!table || !tokens || !counts || !positions || !slots || !y)
+    return fail(Q4K_EINVAL, "null argument");
+  if (dtype > Q4K_DTYPE_F16)
+    return fail(Q4K_EINVAL, "bad dtype %u", dtype);
+  if (table->type != Q4K_GGML_TYPE_Q4_K)
+    return fail(Q4K_ETYPE, "the embedding table must be Q4_K (embedding_q4_k)");
+  if (nqueries == 0 || nqueries > kEmbedMaxQueries)
+    return fail(Q4K_ESHAPE, "nqueries must be 1..%u (got %u)", kEmbedMaxQueries, nqueries);
+  EmbedQueries qs{};
+  qs.n = nqueries;
+  qs.capacity = capacity;
+  uint64_t rows = 0;
+  uint32_t max_slot = 0;
+  for (uint32_t q = 0; q < nqueries; ++q) {
+    if ((uint64_t)positions[q] + counts[q] > capacity)
+      return fail(Q4K_ESHAPE, "query %u: position %u + count %u exceeds the capacity %u", q, positions[q], counts[q], capacity);
+    qs.start[q] = (uint32_t)rows;
+    qs.count[q] = counts[q];
+    qs.position[q] = positions[q];
+    qs.slot[q] = slots[q];
+    rows += counts[q];
+    max_slot = slots[q] > max_slot ? slots[q] : max_slot;
+  }
+  if (rows == 0 || rows > 65535)
+    return fail(Q4K_ESHAPE, "the batch must have 1..65535 rows (got %llu)", (unsigned long long)rows);
+  if ((uint64_t)(max_slot + 1) * capacity > 0x7fffffffull)
+    return fail(Q4K_ESHAPE, "slot %u x capacity %u exceeds the token buffer's 32-bit index", max_slot, capacity);
+  if (rows_out)
+    *rows_out = (uint32_t)rows;
+  const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
+  if (overlaps(tokens, (size_t)(max_slot + 1) * capacity * 4, y, (size_t)rows * table->k * es))
+    return fail(Q4K_EALIAS, "y must not overlap tokens");
+  int rc = set_device(table->device);
+  if (rc)
+    return rc;
+  LaunchTimer timer(static_cast<hipStream_t>(stream), Q4K_KERNEL_AUX);
+  Q4K_TRY_HIP(launch_embedding_batch(static_cast<hipStream_t>(stream), table->data, tokens, qs, y, (int)rows, (int)table->n, (int)table->k,
+                                     (int)dtype),
+              "embedding launch");
+  return Q4K_OK;
+}
+
 int q4k_rms_norm(void* stream, const void* x, const float* w, void* y, uint32_t m, uint32_t k, float eps, uint32_t dtype) {
   if (!x || !w || !y)
     return fail(Q4K_EINVAL, "null argument");

@@ -343,6 +343,15 @@ struct GatherIndex {
   uint32_t src[64];
 };
 
+// The queries of a packed batch for the token embedding: query q owns rows
+// [start[q], start[q] + count[q]) and reads its tokens from row slot[q] of
+// the request buffer (capacity tokens per slot), from position[q] on.
+constexpr uint32_t kEmbedMaxQueries = 64;
+struct EmbedQueries {
+  uint32_t n, capacity;
+  uint32_t start[kEmbedMaxQueries], count[kEmbedMaxQueries], position[kEmbedMaxQueries], slot[kEmbedMaxQueries];
+};
+
 // Activation staging layouts.
 enum StageMode : int {
   kStageRowMajor = 0,  // fp16 [m, k] (GEMM A operand)
@@ -428,6 +437,8 @@ hipError_t launch_fill_u32(hipStream_t s, uint32_t* p, uint32_t v, uint32_t n);
 
 // Token embedding from a tiled Q4_K table (n rows of k): y[t] = row ids[t].
 hipError_t launch_embedding(hipStream_t s, const uint8_t* w, const int32_t* ids, void* y, int rows, int n, int k, int dtype);
+hipError_t launch_embedding_batch(hipStream_t s, const uint8_t* w, const int32_t* tokens, const EmbedQueries& qs, void* y, int rows, int n, int k,
+                                  int dtype);
 
 // RMS norm of `rows` rows of k (idx == nullptr: row r reads x row r;
 // otherwise x row idx->src[r]).

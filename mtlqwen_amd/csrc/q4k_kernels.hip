@@ -1277,11 +1277,13 @@ constexpr int kG2ASlot = 16 * 1024;                    // 8 row tiles x 2 fragme
 constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4 tile-blocks
 
 // Epilogue of a 128 x 64 wave tile.  Lane (col, g) holds rows 16 rt + 4 g + v
-// of column col of each column tile.  All loads of a row tile (row scales,
-// and aux for post 1 / 2) are issued before its stores so that their latency
-// is paid once per row tile; a tile wholly inside m (FULL) has no per-row
-// checks.
-// CT column tiles per wave, of which the first nct lie inside n.
+// of column col of each column tile.  The aux loads (post 1 / 2) run one row
+// tile ahead of the stores: those of row tile rt + 1 are issued before the
+// stores of row tile rt, so their latency overlaps the previous tile's stores
+// instead of being paid once per row tile (rows differ, so an aux that is y
+// itself is read before it is written).  A tile wholly inside m (FULL) has no
+// per-row checks.  CT column tiles per wave, of which the first nct lie
+// inside n.
 template <typename OutT, int POST, bool FULL, int CT = 4>
 __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&acc)[8][CT], int mt0, int ct0, int lane, int nct = CT) {
   OutT* y = reinterpret_cast<OutT*>(a.y);
@@ -1296,18 +1298,23 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
   for (int rt = 0; rt < 8; ++rt)
     rs[rt] = *reinterpret_cast<const f4_t*>(a.rowscale + row0 + 16 * rt);
   const size_t col0 = (size_t)ct0 * 16 + col;
+  float av[2][4][CT];
+  auto load_aux = [&](int rt, float (&dst)[4][CT]) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const int row = row0 + 16 * rt + v;
+        dst[v][c] = (full || row < a.m) && c < nct ? load_elem(aux, (size_t)row * a.n + col0 + 16 * c) : 0.0f;
+      }
+  };
+  if (POST != 0)
+    load_aux(0, av[0]);
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt) {
-    float av[4][CT];
-    if (POST != 0) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int c = 0; c < CT; ++c) {
-          const int row = row0 + 16 * rt + v;
-          av[v][c] = (full || row < a.m) && c < nct ? load_elem(aux, (size_t)row * a.n + col0 + 16 * c) : 0.0f;
-        }
-    }
+    if (POST != 0 && rt + 1 < 8)
+      load_aux(rt + 1, av[(rt + 1) & 1]);
+    const float (&cur)[4][CT] = av[rt & 1];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = row0 + 16 * rt + v;
@@ -1320,11 +1327,49 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
         float acc_v = acc[rt][c][v] * rs[rt][v];
         if (sizeof(OutT) == 2)
           acc_v = round_half(acc_v);
-        const float out = POST == 1 ? acc_v + av[v][c] : POST == 2 ? silu(av[v][c]) * acc_v : acc_v;
+        const float out = POST == 1 ? acc_v + cur[v][c] : POST == 2 ? silu(cur[v][c]) * acc_v : acc_v;
         store_elem(y, (size_t)row * a.n + col0 + 16 * c, out);
       }
     }
   }
+}
+
+// Tile order of the persistent GEMMs.  Workgroup b runs on XCD b % 8 (the
+// dispatcher deals workgroups to the eight XCDs in turn).  In the plain order
+// tile t = b + i * grid has column block t % tiles_x, so an XCD owns whole
+// column blocks and streams the A operand of every row block.  With rg > 0
+// the tile grid is cut into 8 rectangles of tiles_y / rg row blocks by
+// tiles_x / (8 / rg) column blocks, one per XCD, and the XCD's workgroups
+// take its tiles column by column, so that the tiles running together on one
+// XCD share the A of a few row blocks and the B of a few column blocks in
+// that XCD's L2.
+struct TileMap {
+  int tiles_x, tiles;  // column blocks, all tiles
+  int rg;              // 0: plain order; else row groups (8 / rg column groups)
+  int rows, cols;      // rectangle of one XCD (rg > 0)
+};
+
+__device__ __forceinline__ int tile_count(const TileMap& m) {
+  if (m.rg == 0)
+    return ((int)blockIdx.x < m.tiles) ? (m.tiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int per = (int)gridDim.x >> 3, j = (int)blockIdx.x >> 3;
+  const int rect = m.rows * m.cols;
+  return j < rect ? (rect - 1 - j) / per + 1 : 0;
+}
+
+// The i-th tile of this workgroup as (column block, row block).
+__device__ __forceinline__ void tile_at(const TileMap& m, int i, int& bx, int& by) {
+  if (m.rg == 0) {
+    const int t = (int)blockIdx.x + i * (int)gridDim.x;
+    bx = t % m.tiles_x;
+    by = t / m.tiles_x;
+    return;
+  }
+  const int x = (int)blockIdx.x & 7, per = (int)gridDim.x >> 3;
+  const int l = ((int)blockIdx.x >> 3) + i * per;
+  const int cg = 8 / m.rg;
+  by = (x / cg) * m.rows + l % m.rows;
+  bx = (x % cg) * m.cols + l / m.rows;
 }
 
 // One 128 x 256 output tile (column block bx, row block by).
@@ -1353,9 +1398,12 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
   };
   // B(blk, c): tile-block c of block blk (clamped) into ring half blk & 1.
+  // Column tiles are nb tile-blocks apart.
+  const uint8_t* const wcol = a.w + (size_t)ct0 * nb * kTileBlockBytes;
+  const size_t cstride = (size_t)nb * kTileBlockBytes;
   auto issue_b = [&](int blk, int c) {
     const int bc = blk < nb ? blk : nb - 1;
-    const uint8_t* src = uniform_ptr(a.w + ((size_t)(ct0 + c) * nb + bc) * kTileBlockBytes);
+    const uint8_t* src = uniform_ptr(wcol + (size_t)bc * kTileBlockBytes + c * cstride);
     const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * 4 + c) * kTileBlockBytes);
     lds_dma16<0>(src, voff16, l);
     lds_dma16<kSlabBytes>(src, voff16, l);
@@ -1452,10 +1500,19 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
       dequant_words(c, *reinterpret_cast<const uint2*>(bring + c * kTileBlockBytes + 16 * lane), bclo[c], bchi[c]);
     wv3 = *reinterpret_cast<const uint2*>(bring + 3 * kTileBlockBytes + 16 * lane);
   }
+  // A in the loop: this wave's 4 fragments of u-step t are 4 consecutive KB
+  // at xa + 16 KB * t of the staging and at 4 KB * wave of ring slot t % 5;
+  // fragment i is the instruction offset 1 KB * i.  The ring addresses of
+  // the slot read (ar) and written (aw) roll instead of being recomputed.
+  const uint8_t* const xa = reinterpret_cast<const uint8_t*>(xh) + ((size_t)by * nb * 64 + 4 * wave) * 1024;
+  const uint32_t aend = aring + kG2AS * kG2ASlot;
+  uint32_t ar = aring, aw = aring + kG2AD * kG2ASlot + 4096u * (uint32_t)wave;
   for (int blk = 0; blk < nb; ++blk) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * blk + u;
+      const int ta = t + kG2AD < steps ? t + kG2AD : steps - 1;
+      const uint8_t* const asrc = uniform_ptr(xa + (size_t)ta * 16384);
       // Own loads issued after A(t) (during u-steps t - 4 .. t - 1, in the
       // order of the column groups below): 15 at u = 0 (the 3 of B tile 3
       // that follow A(t) at u-step t - 4, then 3 x 4), 24 at u = 1, 2, 3.
@@ -1474,7 +1531,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
       // words of u-step t + 1.  At u = 3 that is the next block, whose B
       // landed before A(t) (issued at u = 0).
       const int bn = u == 3 ? blk + 1 : blk, un = (u + 1) & 3;
-      const uint8_t* aslot = lds + (size_t)(t % kG2AS) * kG2ASlot;
+      const uint8_t* aslot = lds + (ar - aring);
       h8_t af[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -1512,11 +1569,20 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
           dequant_words(c - 1, wv[c - 1], bclo[c - 1], bchi[c - 1]);
         // The loads of the column group, spread over the step: fragment c
         // of A(t + 4) and, at u = 0, tile-block c of B(blk + 1).
-        issue_a(t + kG2AD, c);
+        if (c == 0)
+          lds_dma16<0>(asrc, voff16, aw);
+        else if (c == 1)
+          lds_dma16<1024>(asrc, voff16, aw);
+        else if (c == 2)
+          lds_dma16<2048>(asrc, voff16, aw);
+        else
+          lds_dma16<3072>(asrc, voff16, aw);
         if (u == 0)
           issue_b(blk + 1, c);
       }
       wv3 = wv[3];
+      ar = ar + kG2ASlot == aend ? aring : ar + kG2ASlot;
+      aw = aw + kG2ASlot >= aend ? aw + kG2ASlot - kG2AS * kG2ASlot : aw + kG2ASlot;
       // Schedule of the step: the LDS reads first, then each MFMA followed
       // by a share of the vector work (the next step's dequantisation, and
       // at u = 3 the next block's constants), so that no vector work is
@@ -1557,18 +1623,19 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     full ? gemm2_epilogue<OutT, 2, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 2, false>(a, acc, mt0, ct0, lane);
 }
 
-// Persistent launch: workgroup b takes tiles b, b + grid, ... in the order of
-// a (column block, row block) grid with the column block fastest, so that
-// tile t runs on XCD t % 8 as it would in a one-tile-per-workgroup launch.
-// Consecutive tiles of a workgroup reuse its LDS rings; a barrier separates
-// the last reads of one tile from the first loads of the next.
+// Persistent launch: workgroup b takes its tiles in the order of the tile
+// map.  Consecutive tiles of a workgroup reuse its LDS rings; a barrier
+// separates the last reads of one tile from the first loads of the next.
 template <typename OutT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a, int tiles_x, int tiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a, TileMap map) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    if (tile != (int)blockIdx.x)
+  const int count = tile_count(map);
+  for (int i = 0; i < count; ++i) {
+    if (i > 0)
       __syncthreads();
-    gemm2_tile<OutT>(a, lds, tile % tiles_x, tile / tiles_x);
+    int bx, by;
+    tile_at(map, i, bx, by);
+    gemm2_tile<OutT>(a, lds, bx, by);
   }
 }
 
@@ -1637,11 +1704,8 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const T* __restrict__ 
 // outside [0, n) give a zero row.
 // ----------------------------------------------------------------------------
 template <typename OutT>
-__global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restrict__ w, const int32_t* __restrict__ ids, OutT* __restrict__ y, int n,
-                                                        int nb) {
+__device__ __forceinline__ void embedding_elem(const uint8_t* __restrict__ w, int id, OutT* __restrict__ y, int n, int nb, int t, int b, int e) {
 #pragma clang fp contract(off)
-  const int b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
-  const int id = ids[t];
   float v = 0.0f;
   if (id >= 0 && id < n) {
     const int i = id & 15;
@@ -1672,6 +1736,28 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restric
     v = val - mterm;
   }
   store_elem(y, (size_t)t * nb * 256 + (size_t)b * 256 + e, v);
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restrict__ w, const int32_t* __restrict__ ids, OutT* __restrict__ y, int n,
+                                                        int nb) {
+  embedding_elem(w, ids[blockIdx.y], y, n, nb, (int)blockIdx.y, (int)blockIdx.x, (int)threadIdx.x);
+}
+
+// The same over a packed batch, each row's token resolved in the kernel
+// (quant_linear.metal:577-584 mode 0 with queryRow, batch.hpp:19-23): row t
+// belongs to the first query q with t < start[q] + count[q] and takes the
+// request buffer's token tokens[slot[q] * capacity + position[q] + t -
+// start[q]].
+template <typename OutT>
+__global__ __launch_bounds__(256) void embedding_batch_kernel(const uint8_t* __restrict__ w, const int32_t* __restrict__ tokens, OutT* __restrict__ y,
+                                                              int n, int nb, EmbedQueries qs) {
+  const uint32_t t = blockIdx.y;
+  uint32_t q = 0;
+  while (q + 1 < qs.n && t >= qs.start[q] + qs.count[q])
+    ++q;
+  const int id = tokens[(size_t)qs.slot[q] * qs.capacity + qs.position[q] + (t - qs.start[q])];
+  embedding_elem(w, id, y, n, nb, (int)t, (int)blockIdx.x, (int)threadIdx.x);
 }
 
 // ----------------------------------------------------------------------------
@@ -2705,12 +2791,15 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
 
 // Persistent over the (column block, row block) tiles, as the Q4_K GEMM.
 template <class P, typename OutT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void typed_gemm_kernel(GemmArgs a, int tiles_x, int tiles, int ntiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void typed_gemm_kernel(GemmArgs a, TileMap map, int ntiles) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[P::kAS * kG2ASlot + 4 * 2 * P::kCT * P::kTB];
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    if (tile != (int)blockIdx.x)
+  const int count = tile_count(map);
+  for (int i = 0; i < count; ++i) {
+    if (i > 0)
       __syncthreads();
-    typed_gemm_tile<P, OutT>(a, lds, tile % tiles_x, tile / tiles_x, ntiles);
+    int bx, by;
+    tile_at(map, i, bx, by);
+    typed_gemm_tile<P, OutT>(a, lds, bx, by, ntiles);
   }
 }
 
@@ -3003,15 +3092,32 @@ hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters)
   return hipGetLastError();
 }
 
+// The tile map of a persistent GEMM launch of `grid` workgroups over a
+// tiles_y x tiles_x tile grid: the XCD rectangles when the grid deals the
+// same number of workgroups to each XCD and the rectangles divide the grid
+// (Q4K_GEMM_XCD_ROWS: row groups, default 4; 0 keeps the plain order).
+TileMap make_tile_map(int tiles_x, int tiles_y, int grid) {
+  static const int rg_env = env_int("Q4K_GEMM_XCD_ROWS", 4);
+  TileMap m{tiles_x, tiles_x * tiles_y, 0, 0, 0};
+  const int rg = rg_env == 1 || rg_env == 2 || rg_env == 4 || rg_env == 8 ? rg_env : 0;
+  if (rg && grid % 8 == 0 && tiles_y % rg == 0 && tiles_x % (8 / rg) == 0) {
+    m.rg = rg;
+    m.rows = tiles_y / rg;
+    m.cols = tiles_x / (8 / rg);
+  }
+  return m;
+}
+
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
-  const int tiles_x = a.n / kG2N, tiles = tiles_x * ((a.m + kG2M - 1) / kG2M);
+  const int tiles_x = a.n / kG2N, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
   static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);
   const int grid = persist && tiles > cus ? cus : tiles;
+  const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
   const dim3 block(256);
   if (dtype == kF32)
-    (void)dispatch(q4k_gemm2_kernel<float>, dim3((unsigned)grid), block, s, a, tiles_x, tiles);
+    (void)dispatch(q4k_gemm2_kernel<float>, dim3((unsigned)grid), block, s, a, map);
   else
-    (void)dispatch(q4k_gemm2_kernel<_Float16>, dim3((unsigned)grid), block, s, a, tiles_x, tiles);
+    (void)dispatch(q4k_gemm2_kernel<_Float16>, dim3((unsigned)grid), block, s, a, map);
   return hipGetLastError();
 }
 
@@ -3040,6 +3146,18 @@ hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dty
     (void)dispatch(gather_rows_kernel<float>, grid, block, s, static_cast<const float*>(x), static_cast<float*>(out), k, idx);
   else
     (void)dispatch(gather_rows_kernel<_Float16>, grid, block, s, static_cast<const _Float16*>(x), static_cast<_Float16*>(out), k, idx);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding_batch(hipStream_t s, const uint8_t* w, const int32_t* tokens, const EmbedQueries& qs, void* y, int rows, int n, int k,
+                                  int dtype) {
+  if (rows == 0)
+    return hipSuccess;
+  const dim3 grid((unsigned)(k / 256), (unsigned)rows), block(256);
+  if (dtype == kF32)
+    (void)dispatch(embedding_batch_kernel<float>, grid, block, s, w, tokens, static_cast<float*>(y), n, k / 256, qs);
+  else
+    (void)dispatch(embedding_batch_kernel<_Float16>, grid, block, s, w, tokens, static_cast<_Float16*>(y), n, k / 256, qs);
   return hipGetLastError();
 }
 
@@ -3150,12 +3268,14 @@ hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, in
 template <class P>
 hipError_t typed_gemm_launch(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   const int ntiles = a.n / 16, tiles_x = (ntiles + 4 * P::kCT - 1) / (4 * P::kCT);
-  const int tiles = tiles_x * ((a.m + kG2M - 1) / kG2M);
-  const dim3 grid((unsigned)(tiles > cus ? cus : tiles)), block(256);
+  const int tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
+  const int g = tiles > cus ? cus : tiles;
+  const TileMap map = make_tile_map(tiles_x, tiles_y, g);
+  const dim3 grid((unsigned)g), block(256);
   if (dtype == kF32)
-    (void)dispatch(typed_gemm_kernel<P, float>, grid, block, s, a, tiles_x, tiles, ntiles);
+    (void)dispatch(typed_gemm_kernel<P, float>, grid, block, s, a, map, ntiles);
   else
-    (void)dispatch(typed_gemm_kernel<P, _Float16>, grid, block, s, a, tiles_x, tiles, ntiles);
+    (void)dispatch(typed_gemm_kernel<P, _Float16>, grid, block, s, a, map, ntiles);
   return hipGetLastError();
 }
 

@@ -257,6 +257,29 @@ def embedding(table, ids, y, stream=None):
     return y
 
 
+def embedding_batch(table, tokens, capacity, counts, positions, slots, y, stream=None):
+    """Token embedding of a packed batch with each row's token resolved in
+    the kernel (embedding_q4_k mode 0 with queryRow, quant_linear.metal:577-584,
+    batch.hpp:19-23): query q owns counts[q] consecutive rows, which read
+    tokens[slots[q] * capacity + positions[q] + i] of the request token buffer
+    ``tokens`` (int32 device tensor, ``capacity`` tokens per slot).  Returns
+    the row count."""
+    if tokens.dtype != torch.int32:
+        raise TypeError("tokens must be an int32 tensor")
+    if not (len(counts) == len(positions) == len(slots)):
+        raise ValueError("counts, positions and slots must have one entry per query")
+    rows = int(sum(counts))
+    _check_tensor(tokens, (max(slots) + 1) * capacity if len(slots) else 0, "tokens", table.device)
+    _check_tensor(y, rows * table.k, "y", table.device)
+    c, nq = u32_array(counts)
+    p, _ = u32_array(positions)
+    sl, _ = u32_array(slots)
+    out = ctypes.c_uint32()
+    check(lib.q4k_embedding_batch(_stream(stream, table.device), table.handle, _ptr(tokens), capacity, c, p, sl, nq, _ptr(y), _dtype_code(y),
+                                  ctypes.byref(out)))
+    return out.value
+
+
 def rms_norm(x, weight, y, eps=1e-6, stream=None):
     """RMS norm of every row of ``x`` (native_ops.metal:6-40) with fp32
     ``weight`` [k]; ``y`` may be ``x``."""

@@ -659,6 +659,19 @@ int64_t q4o_gather_row(const uint32_t* start, const uint32_t* count, const uint3
   return -1;
 }
 
+/* quant_linear.metal:577-584 (embedding_q4_k, mode 0, a target query) with
+ * queryRow (batch.hpp:19-23): row t belongs to the first query q with
+ * t < start[q] + count[q]; its token is the request buffer's entry
+ * tokens[slot[q] * capacity + position[q] + (t - start[q])].  Returns the
+ * token, or -1 when no query owns row t. */
+int64_t q4o_embedding_token(const uint32_t* start, const uint32_t* count, const uint32_t* position, const uint32_t* slot, int nqueries,
+                            uint32_t capacity, const int32_t* tokens, uint32_t t) {
+  for (int q = 0; q < nqueries; ++q)
+    if (t < start[q] + count[q])
+      return tokens[(size_t)slot[q] * capacity + position[q] + (t - start[q])];
+  return -1;
+}
+
 /* ------------------------------------------------- adjacent consumers -- */
 
 /* quant_linear.metal:572-591: element r of the row's block (col >> 8) is

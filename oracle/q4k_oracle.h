@@ -132,6 +132,14 @@ uint32_t q4o_pack(const uint32_t* counts, const uint32_t* samples, int nqueries,
  * query that owns logit row r.  Returns -1 if r is not owned by any query. */
 int64_t q4o_gather_row(const uint32_t* start, const uint32_t* count, const uint32_t* samples, const uint32_t* logit, int nqueries, uint32_t r);
 
+/* Token id of row t of a packed batch for the token embedding
+ * (quant_linear.metal:577-584 mode 0, batch.hpp:19-23 queryRow): the first
+ * query q with t < start[q] + count[q] owns it; its token is
+ * tokens[slot[q] * capacity + position[q] + (t - start[q])].  -1 when no
+ * query owns row t. */
+int64_t q4o_embedding_token(const uint32_t* start, const uint32_t* count, const uint32_t* position, const uint32_t* slot, int nqueries,
+                            uint32_t capacity, const int32_t* tokens, uint32_t t);
+
 /* Token-embedding gather-dequant: row t of y (k values) is row ids[t] of the
  * Q4_K table w (n rows of k/256 blocks), each element d*sc*q - dmin*m in fp32
  * ((d*sc)*q first, then the min product subtracted).

@@ -280,6 +280,9 @@ def load_oracle():
     lib.q4o_pack.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 2 + [i] + [ctypes.POINTER(ctypes.c_uint32)] * 2
     lib.q4o_gather_row.restype = ctypes.c_int64
     lib.q4o_gather_row.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 4 + [i, ctypes.c_uint32]
+    lib.q4o_embedding_token.restype = ctypes.c_int64
+    lib.q4o_embedding_token.argtypes = [ctypes.POINTER(ctypes.c_uint32)] * 4 + [i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_int32),
+                                                                                ctypes.c_uint32]
     for name in ("q4o_embedding_f32", "q4o_embedding_f16"):
         getattr(lib, name).restype = i
         getattr(lib, name).argtypes = [p, u8p, i, i, p, i]
@@ -399,6 +402,16 @@ class Oracle:
         """Input row of every LM-head output row (q4o_gather_row over the pack)."""
         start, logit, _ = self.pack(counts, samples)
         return [self.gather_row(start, counts, samples, logit, r) for r in range(sum(samples))]
+
+    def embedding_tokens(self, counts, positions, slots, capacity, tokens):
+        """Token id of every row of a packed batch (q4o_embedding_token;
+        starts are the prefix sums of counts)."""
+        n = len(counts)
+        start = np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.uint32)
+        arrs = [(ctypes.c_uint32 * n)(*[int(v) for v in a]) for a in (start, counts, positions, slots)]
+        tok = np.ascontiguousarray(tokens, np.int32)
+        tp = tok.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+        return [self.lib.q4o_embedding_token(*arrs, n, capacity, tp, t) for t in range(int(sum(counts)) + 1)]
 
     def gather_row(self, start, count, samples, logit, r):
         n = len(start)

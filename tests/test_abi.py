@@ -125,6 +125,8 @@ def test_neighbour_entry_points_validate_before_hip(q4k):
     fake = ctypes.c_void_p(0x1000)
     u32 = ctypes.c_uint32
     assert lib.q4k_embedding(None, None, fake, 1, fake, 0) == -1
+    one = (u32 * 1)(1)
+    assert lib.q4k_embedding_batch(None, None, fake, 8, one, one, one, 1, fake, 0, None) == -1
     assert lib.q4k_rms_norm(None, None, fake, fake, 1, 16, ctypes.c_float(1e-6), 0) == -1
     assert lib.q4k_rms_norm(None, fake, fake, fake, 1, 16, ctypes.c_float(-1.0), 0) == -1
     assert lib.q4k_rms_norm(None, fake, fake, fake, 1, 0, ctypes.c_float(1e-6), 0) == -3

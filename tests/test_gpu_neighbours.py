@@ -58,6 +58,37 @@ def test_embedding_full_vocabulary(q4k, oracle, gpu):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_embedding_batch_resolves_rows_in_kernel(q4k, oracle, gpu, dtype):
+    """A packed batch with config 3's lengths {512, 37, 1, 1, 200, 5, 1, 64}
+    (821 rows) at random positions of random slots of a 9 x 1024 request
+    token buffer: each row's token is found in the kernel (queryRow); the
+    result equals the oracle's embedding of the oracle's row tokens bit for
+    bit.  Then the entry point's shape checks."""
+    n, k, capacity, nslots = 1008, 4096, 1024, 9
+    rng = np.random.default_rng(82)
+    w = make_q4k(rng, n, k, dmax=2.0)
+    T = q4k.Weight(w, n, k)
+    counts = [512, 37, 1, 1, 200, 5, 1, 64]
+    positions = [int(rng.integers(0, capacity - c + 1)) for c in counts]
+    slots = [int(s) for s in rng.permutation(nslots)[:len(counts)]]
+    tokens = rng.integers(0, n, nslots * capacity).astype(np.int32)
+    y = torch.full((sum(counts), k), float("nan"), device=gpu, dtype=dtype)
+    rows = q4k.embedding_batch(T, _t(tokens, gpu), capacity, counts, positions, slots, y)
+    torch.cuda.synchronize()
+    assert rows == 821
+    ids = np.array(oracle.embedding_tokens(counts, positions, slots, capacity, tokens)[:-1], np.int32)
+    ref = oracle.embedding(w, n, k, ids, f16=dtype == torch.float16)
+    got = y.cpu().numpy()
+    view = np.uint16 if dtype == torch.float16 else np.uint32
+    assert np.array_equal(got.view(view), ref.view(view))
+    # A query running past the capacity, and no queries: refused before any launch.
+    with pytest.raises(RuntimeError):
+        q4k.embedding_batch(T, _t(tokens, gpu), capacity, [5], [capacity - 4], [0], y)
+    with pytest.raises(RuntimeError):
+        q4k.embedding_batch(T, _t(tokens, gpu), capacity, [], [], [], y)
+
+
 def _norm_close(got, ref, f16):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)

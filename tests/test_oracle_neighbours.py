@@ -113,3 +113,28 @@ def test_rms_norm_gather_is_rms_norm_of_the_lm_head_rows(oracle):
     assert np.array_equal(oracle.rms_norm(x, w, src=src), oracle.rms_norm(x, w)[src])
     # speculative verify rows: every row of 8 queries of 5 (forward.cpp:180-183)
     assert oracle.logit_sources([5] * 8, [5] * 8) == list(range(40))
+
+
+def test_embedding_tokens_closed_form(oracle):
+    """Rows of a packed batch to request-buffer tokens (quant_linear.metal:577-584
+    mode 0 with queryRow, batch.hpp:19-23), worked by hand: queries of 3, 1 and
+    2 rows at positions 5, 0, 7 of slots 2, 0, 1 of a 3 x 10 token buffer."""
+    tokens = np.arange(30, dtype=np.int32) * 7 + 1
+    got = oracle.embedding_tokens([3, 1, 2], [5, 0, 7], [2, 0, 1], 10, tokens)
+    assert got == [176, 183, 190, 1, 120, 127, -1]
+
+
+def test_embedding_tokens_are_the_slot_slices_in_query_order(oracle):
+    """Every batch: the row tokens are the queries' slices
+    buffer[slot, position:position + count] concatenated in query order."""
+    rng = np.random.default_rng(77)
+    for _ in range(40):
+        nq, slots_n, capacity = int(rng.integers(1, 9)), 9, 64
+        counts = rng.integers(1, 20, nq)
+        positions = np.array([rng.integers(0, capacity - c + 1) for c in counts])
+        slots = rng.permutation(slots_n)[:nq]
+        tokens = rng.integers(0, 248320, slots_n * capacity).astype(np.int32)
+        got = oracle.embedding_tokens(counts, positions, slots, capacity, tokens)
+        buf = tokens.reshape(slots_n, capacity)
+        want = np.concatenate([buf[s, p:p + c] for s, p, c in zip(slots, positions, counts)])
+        assert got[:-1] == want.tolist() and got[-1] == -1
