@@ -659,8 +659,8 @@ constexpr int kGuWaveFloats = 2 * 64 * kGuXRow;
 // The x of one item of the fused gate/up GEMV, packed: wave w loads K-blocks
 // bw, bw + 1 of all 8 rows (one coalesced load per (block, row), lane l
 // holding elements 4l..4l+3; rows >= m read row 0 and are zeroed), calls
-// issue_first() so that its first weight units queue behind x, and turns its
-// blocks into MFMA operands in registers (through its LDS region).  NORM: x
+// issue_first() once its x has landed, and turns its blocks into MFMA
+// operands in registers (through its LDS region).  NORM: x
 // is RMS-normalised on the way in (native_ops.metal:6-40, the norm
 // forward.cpp:114 applies before the MLP): the 8 waves hold all of x between
 // them, so each row's sum of squares is their partial sums (ssq [wave][row])
@@ -698,7 +698,6 @@ __device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float (*xl)[kG
       nw[j] = *reinterpret_cast<const f4_t*>(a.norm_w + (size_t)(bw + j) * 256 + 4 * lane);
   }
   __builtin_amdgcn_sched_barrier(0);
-  issue_first();
 
   if constexpr (NORM) {
     float ss[8];
@@ -750,6 +749,13 @@ __device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float (*xl)[kG
         v4[e] = r < a.m ? xv[j][r][e] : 0.0f;
       *reinterpret_cast<f4_t*>(xw + (j * 64 + dl + r) * kXRow + doff) = v4;
     }
+  // The first weight loads go out once x has landed, not with it: issued
+  // together, every wave's first units queue ahead of the x of later
+  // workgroups (measured: kernel 15.0 against 15.6 us at config 1).  The
+  // LDS transposition and the register pack below run under them.
+  __builtin_amdgcn_sched_barrier(0);
+  issue_first();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < BPW; ++j) {
     float t32[32];
@@ -815,10 +821,10 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
 
   // Units are loaded into registers DQ ahead of the one being computed
   // (header dword, then the two quant slabs; the scheduling barriers keep
-  // the issue order: x first, then unit by unit).  A shallow window keeps
-  // the memory queues short, so x and each wave's next unit arrive early;
-  // issuing more units ahead measured slower (they queue ahead of the x of
-  // later workgroups).
+  // the issue order: x first, then unit by unit, the first units once x has
+  // landed).  A shallow window keeps the memory queues short, so x and each
+  // wave's next unit arrive early; issuing more units ahead measured slower
+  // (they queue ahead of the x of later workgroups).
   constexpr int DQ = 2;
   uint32_t hw[U];
   u4_t q0[U], q1[U];
