@@ -320,7 +320,7 @@ Kernel& resolve(q4k_weight* w, uint32_t phase) {
       k.kind = kGemv;  // narrow Q4_K outputs: the GEMV per 8-row group at every row count
     k.name = std::string(phase == Q4K_PHASE_GATED_DECODE ? "mlp_" : "linear_") + type_name(w->type) + "_k" + std::to_string(w->k) + "_n" +
              std::to_string(w->n) + "_" + suffix[phase] +
-             (k.kind == kGemm ? "_mfma32x32x16" : "_mfma16x16x32");
+             "_mfma16x16x32";
   }
   return k;
 }
@@ -656,8 +656,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     Q4K_TRY_HIP(launch_q4k_persistent(stream, a, (int)dtype, device_cus(w->device)), "gemv persistent launch");
     return Q4K_OK;
   }
-  const bool gemm2 = !gemv && gemm2_supported((int)m, (int)w->n);
-  const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : gemm2 ? (size_t)gemm2_rows((int)m) : m;
+  const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : (size_t)gemm2_rows((int)m);
   // xs is read 32 lanes at a time from its start; +128 halves of slack.
   const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : 0;
   int rc = ensure_workspace(stream, ws, w->device, ws_rows * w->k + xs_halves, ws_rows);
@@ -666,7 +665,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
   _Float16* xs = ws.x + ws_rows * w->k;
   if (restage) {
     LaunchTimer timer(stream, Q4K_KERNEL_STAGE);
-    const int mode = gemm2 ? kStageGemm : !gemv ? kStageRowMajor : split ? kStageFragSplit : kStageFrag;
+    const int mode = !gemv ? kStageGemm : split ? kStageFragSplit : kStageFrag;
     Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode, norm_w, eps), "stage_x launch");
   }
   if (gemv) {
@@ -700,10 +699,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.nb = (int)(w->k / 256);
     a.post = (int)post;
     LaunchTimer timer(stream, Q4K_KERNEL_GEMM);
-    if (gemm2)
-      Q4K_TRY_HIP(launch_gemm2(stream, a, (int)dtype, device_cus(w->device)), "gemm launch");
-    else
-      Q4K_TRY_HIP(launch_gemm(stream, a, (int)dtype), "gemm launch");
+    Q4K_TRY_HIP(launch_gemm2(stream, a, (int)dtype, device_cus(w->device)), "gemm launch");
   }
   return Q4K_OK;
 }

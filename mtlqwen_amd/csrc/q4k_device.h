@@ -53,27 +53,11 @@ __device__ __forceinline__ void load8(const _Float16* p, float* v) {
     v[i] = (float)a[i];
 }
 
-// Scales and mins of sub-blocks 2g and 2g+1 from the three packed words of a
-// block header (quant_linear.metal:12-20, taken four bytes at a time).
-__device__ __forceinline__ void scale_min_pair(u4_t hd, int g, uint32_t& sc0, uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
-  const uint32_t sh = 16u * (uint32_t)(g & 1);
-  const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
-  // Sub-blocks 0-3 keep 6 bits in a / b; sub-blocks 4-7 take the low 4 bits
-  // from c and the top 2 from a >> 2 / b >> 2.  Written as one formula with
-  // per-lane selects of plain values: a branch on g would split the caller's
-  // instruction schedule into divergent blocks.
-  const bool low = g < 2;
-  const uint32_t ysh = low ? 0u : 2u, xsh = low ? 0u : 4u;
-  const uint32_t xa = low ? a : c, xb = (low ? b : c) >> xsh, ya = a >> ysh, yb = b >> ysh;
-  sc0 = (xa & 15u) | (ya & 0x30u);
-  sc1 = ((xa >> 8) & 15u) | ((ya >> 8) & 0x30u);
-  m0 = (xb & 15u) | (yb & 0x30u);
-  m1 = ((xb >> 8) & 15u) | ((yb >> 8) & 0x30u);
-}
-
-// The same pairs as 16-bit lanes: p0 = sc(2g) | m(2g) << 16, p1 = sc(2g + 1) |
-// m(2g + 1) << 16.  Bytes 0 / 1 of the selected words are gathered with one
-// v_perm_b32 per word pair.
+// Scales and mins of sub-blocks 2g and 2g + 1 from the three packed words of
+// a block header (quant_linear.metal:12-20, taken four bytes at a time), as
+// 16-bit lanes: p0 = sc(2g) | m(2g) << 16, p1 = sc(2g + 1) | m(2g + 1) << 16.
+// Bytes 0 / 1 of the selected words are gathered with one v_perm_b32 per
+// word pair.
 __device__ __forceinline__ void scale_min_packed(u4_t hd, int g, uint32_t& p0, uint32_t& p1) {
   const uint32_t sh = 16u * (uint32_t)(g & 1);
   const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;

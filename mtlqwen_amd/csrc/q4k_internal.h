@@ -354,7 +354,6 @@ struct EmbedQueries {
 
 // Activation staging layouts.
 enum StageMode : int {
-  kStageRowMajor = 0,  // fp16 [m, k] (GEMM A operand)
   kStageFrag = 1,      // fp16 in GEMV fragment order, m rows
   kStageFragSplit = 2, // fragment order, rows [0, m) = hi, rows [m, 2m) = lo
   kStageGemm = 3       // fp16 in the pipelined GEMM's order (gemm_frag_offset), no xs
@@ -417,10 +416,8 @@ hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const
 // GEMV for m <= 48.
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvShape& shape, bool gated);
 
-hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype);
-
 // Pipelined GEMM: xh holds the activations staged in the GEMM order
-// (kStageGemm) for gemm2_rows(m) rows; N a multiple of 256.
+// (kStageGemm) for gemm2_rows(m) rows; any N that is a multiple of 16.
 bool gemm2_supported(int m, int n);
 int gemm2_rows(int m);
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus);

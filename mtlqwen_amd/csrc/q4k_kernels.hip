@@ -1,16 +1,23 @@
-// Q4_K linear() kernels for gfx950 (MI355X / CDNA4).
+// Q4_K linear() kernels for gfx950 (MI355X / CDNA4), and the other GGUF
+// weight types on the same surface.
 //
-//  stage_x_kernel   activations -> fp16 with a per-row power-of-two scale
-//  q4k_gemv_kernel  decode-shaped (m <= 48) GEMV on v_mfma_f32_16x16x32_f16,
-//                   optionally fused gate/up with the SiLU(gate)*up epilogue
-//  q4k_gemm_kernel  prefill-shaped GEMM: Q4_K tiles dequantised to fp16 in LDS,
-//                   v_mfma_f32_32x32x16_f16, fp32 accumulation, post 0/1/2
-//  gather_rows_kernel, relayout_kernel
-//  embedding_kernel, rms_norm_kernel   the path's neighbours in a pass (token
-//                   embedding gather-dequant, RMS norm / LM-head rms_norm_gather)
+//  stage_x_kernel, stage_gemm_kernel, stage_pack_kernel
+//                   activations -> fp16 operands with power-of-two scales
+//  q4k_gemv_kernel  staged decode GEMV (up to 48 rows), optionally gated
+//  q4k_gemv_gate_up_kernel   fused gate/up decode GEMV, x packed in registers
+//  q4k_gemv_splitk_kernel    split-K decode GEMV (K = 12288)
+//  typed_gemv_kernel, typed_gemv_persistent_kernel, typed_gate_up_kernel
+//                   decode GEMVs over a format policy (Q6_K, Q8_0, Q5_K,
+//                   IQ4_XS; Q4_K for the wide LM head)
+//  q4k_gemm2_kernel, typed_gemm_kernel
+//                   pipelined prefill GEMMs on v_mfma_f32_16x16x32_f16
+//  gather_rows_kernel, relayout_kernel, typed_relayout_kernel
+//  embedding_kernel, embedding_batch_kernel, rms_norm_kernel
+//                   the path's neighbours in a pass (token embedding
+//                   gather-dequant, RMS norm / LM-head rms_norm_gather)
 //
-// Reference semantics: backend/metal/kernel/quant_linear.metal (Q4_K parts)
-// and backend/metal/kernel/fused_kernels.metal:11-78.
+// Reference semantics: backend/metal/kernel/quant_linear.metal and
+// backend/metal/kernel/fused_kernels.metal.
 #include <float.h>
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
@@ -77,11 +84,6 @@ __device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row,
     hi[i] = (_Float16)t;
     lo[i] = (_Float16)(t - (float)hi[i]);
     sum += t;
-  }
-  if (MODE == kStageRowMajor) {
-    if (live)
-      *reinterpret_cast<h8_t*>(xo + (size_t)row * k + (size_t)c * 8) = hi;
-    return;
   }
   if (MODE == kStageGemm) {
     if (live)
@@ -1139,122 +1141,6 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
 
 
 // ----------------------------------------------------------------------------
-// GEMM (prefill).  Workgroup tile 128 x 128, 4 waves of 64 x 64, k-step 64
-// (one quarter of a Q4_K block).  Per k-step: the 128x64 fp16 activation tile
-// is copied to LDS; 256 threads dequantise the 128x64 weight tile to
-// h(d*sc*q - dmin*m) (quant_linear.metal:43,45) into LDS; each wave then runs
-// 16 v_mfma_f32_32x32x16_f16.
-// ----------------------------------------------------------------------------
-constexpr int kBM = 128, kBN = 128, kBK = 64, kLds = kBK + 8;
-
-template <typename OutT>
-__global__ __launch_bounds__(256) void q4k_gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLds];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[kBN * kLds];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-  const int nb = a.nb;
-
-  f16_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        acc[i][j][v] = 0.0f;
-
-  // A copy: thread -> (row, 32-element half of the k-step).
-  const int ar = tid >> 1, ak = (tid & 1) * 32;
-  const bool a_live = m0 + ar < a.m;
-  const _Float16* a_src = a.xh + (size_t)(m0 + ar) * a.k + ak;
-  // B dequant: thread -> (column, slab).
-  const int bc = tid >> 1, hh = tid & 1;
-  const int bn = n0 + bc;
-  const bool b_live = bn < a.n;
-  const uint8_t* b_tile = a.w + (size_t)(bn >> 4) * nb * kTileBlockBytes;
-  const int bi = bn & 15;
-
-  for (int kb = 0; kb < nb; ++kb) {
-    const uint8_t* tb = b_tile + (size_t)kb * kTileBlockBytes;
-    u4_t hd = b_live ? *reinterpret_cast<const u4_t*>(tb + kHeaderOffset + 16 * bi) : u4_t{0u, 0u, 0u, 0u};
-    const float d = half_bits_to_float(hd.x & 0xffffu), dmin = half_bits_to_float(hd.x >> 16);
-    for (int gq = 0; gq < 4; ++gq) {
-      // Stage A.
-      h8_t av[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        av[j] = a_live ? *reinterpret_cast<const h8_t*>(a_src + (size_t)kb * 256 + gq * 64 + j * 8) : h8_t{};
-      // Dequantise B: 16 quant bytes = 16 low-nibble + 16 high-nibble weights.
-      u4_t raw = b_live ? *reinterpret_cast<const u4_t*>(tb + hh * kSlabBytes + 16 * (gq * 16 + bi)) : u4_t{0u, 0u, 0u, 0u};
-      uint32_t sc0, mn0, sc1, mn1;
-      scale_min_pair(hd, gq, sc0, mn0, sc1, mn1);
-      const float ds0 = d * (float)sc0, dm0 = dmin * (float)mn0, ds1 = d * (float)sc1, dm1 = dmin * (float)mn1;
-      h8_t lo[2], hi[2];
-#pragma unroll
-      for (int wd = 0; wd < 4; ++wd) {
-        const uint32_t wv = raw[wd];
-        // Stored byte order within a word is (0, 2, 1, 3) of the quant bytes.
-        const uint32_t qb[4] = {wv & 0xffu, (wv >> 16) & 0xffu, (wv >> 8) & 0xffu, wv >> 24};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lo[wd >> 1][(wd & 1) * 4 + e] = (_Float16)(ds0 * (float)(qb[e] & 15u) - dm0);
-          hi[wd >> 1][(wd & 1) * 4 + e] = (_Float16)(ds1 * (float)(qb[e] >> 4) - dm1);
-        }
-      }
-      __syncthreads();  // previous k-step's MFMA reads are done
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<h8_t*>(&As[ar * kLds + ak + j * 8]) = av[j];
-      _Float16* bdst = &Bs[bc * kLds + 16 * hh];
-      *reinterpret_cast<h8_t*>(bdst) = lo[0];
-      *reinterpret_cast<h8_t*>(bdst + 8) = lo[1];
-      *reinterpret_cast<h8_t*>(bdst + 32) = hi[0];
-      *reinterpret_cast<h8_t*>(bdst + 40) = hi[1];
-      __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < kBK / 16; ++kk) {
-        h8_t af[2], bf[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          af[i] = *reinterpret_cast<const h8_t*>(&As[(wm * 64 + i * 32 + (lane & 31)) * kLds + kk * 16 + 8 * (lane >> 5)]);
-          bf[i] = *reinterpret_cast<const h8_t*>(&Bs[(wn * 64 + i * 32 + (lane & 31)) * kLds + kk * 16 + 8 * (lane >> 5)]);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      }
-    }
-  }
-
-  OutT* y = reinterpret_cast<OutT*>(a.y);
-  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-      if (n >= a.n)
-        continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row >= a.m)
-          continue;
-        const size_t o = (size_t)row * a.n + n;
-        float acc_v = acc[i][j][v] * a.rowscale[row];
-        if (sizeof(OutT) == 2)
-          acc_v = round_half(acc_v);
-        const float out = a.post == 1 ? acc_v + load_elem(aux, o) : a.post == 2 ? silu(load_elem(aux, o)) * acc_v : acc_v;
-        store_elem(y, o, out);
-      }
-    }
-}
-
-// ----------------------------------------------------------------------------
 // Pipelined GEMM (prefill, N a multiple of 256).
 //
 // Workgroup tile 128 rows x 256 columns, 4 waves; wave w owns columns
@@ -1378,9 +1264,11 @@ __device__ __forceinline__ void tile_at(const TileMap& m, int i, int& bx, int& b
   bx = (x % cg) * m.cols + l / m.rows;
 }
 
-// One 128 x 256 output tile (column block bx, row block by).
+// One 128 x 256 output tile (column block bx, row block by).  Column tiles
+// at or past ntiles = n / 16 (a last, partial column block) load the last
+// column tile (in bounds) and store nothing.
 template <typename OutT>
-__device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int bx, int by) {
+__device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
@@ -1404,12 +1292,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
   };
   // B(blk, c): tile-block c of block blk (clamped) into ring half blk & 1.
-  // Column tiles are nb tile-blocks apart.
-  const uint8_t* const wcol = a.w + (size_t)ct0 * nb * kTileBlockBytes;
-  const size_t cstride = (size_t)nb * kTileBlockBytes;
   auto issue_b = [&](int blk, int c) {
     const int bc = blk < nb ? blk : nb - 1;
-    const uint8_t* src = uniform_ptr(wcol + (size_t)bc * kTileBlockBytes + c * cstride);
+    const int ct = ct0 + c < ntiles ? ct0 + c : ntiles - 1;
+    const uint8_t* src = uniform_ptr(a.w + ((size_t)ct * nb + bc) * kTileBlockBytes);
     const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * 4 + c) * kTileBlockBytes);
     lds_dma16<0>(src, voff16, l);
     lds_dma16<kSlabBytes>(src, voff16, l);
@@ -1621,12 +1507,13 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
 
   // One straight-line epilogue per (post code, tile inside m or not).
   const bool full = mt0 * 16 + kG2M <= a.m;
+  const int nct = ntiles - ct0 >= 4 ? 4 : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
   if (a.post == 0)
-    full ? gemm2_epilogue<OutT, 0, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 0, false>(a, acc, mt0, ct0, lane);
+    full ? gemm2_epilogue<OutT, 0, true>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 0, false>(a, acc, mt0, ct0, lane, nct);
   else if (a.post == 1)
-    full ? gemm2_epilogue<OutT, 1, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 1, false>(a, acc, mt0, ct0, lane);
+    full ? gemm2_epilogue<OutT, 1, true>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 1, false>(a, acc, mt0, ct0, lane, nct);
   else
-    full ? gemm2_epilogue<OutT, 2, true>(a, acc, mt0, ct0, lane) : gemm2_epilogue<OutT, 2, false>(a, acc, mt0, ct0, lane);
+    full ? gemm2_epilogue<OutT, 2, true>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 2, false>(a, acc, mt0, ct0, lane, nct);
 }
 
 // Persistent launch: workgroup b takes its tiles in the order of the tile
@@ -1641,7 +1528,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       __syncthreads();
     int bx, by;
     tile_at(map, i, bx, by);
-    gemm2_tile<OutT>(a, lds, bx, by);
+    gemm2_tile<OutT>(a, lds, bx, by, a.n / 16);
   }
 }
 
@@ -3014,9 +2901,7 @@ hipError_t launch_typed_gate_up(hipStream_t s, const GemvArgs& a, uint32_t type,
 template <typename InT, bool NORM>
 hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs, float* rowscale, int m, int k, int mode, RowNorm nrm) {
   const dim3 grid((unsigned)m), block(256);
-  if (mode == kStageRowMajor)
-    (void)dispatch(stage_x_kernel<InT, kStageRowMajor, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
-  else if (mode == kStageFrag)
+  if (mode == kStageFrag)
     (void)dispatch(stage_x_kernel<InT, kStageFrag, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
   else if (mode == kStageGemm && m < 2048)  // fewer than 256 workgroups of 8 rows: one row each
     (void)dispatch(stage_x_kernel<InT, kStageGemm, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
@@ -3085,8 +2970,7 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvSh
 }
 
 bool gemm2_supported(int m, int n) {
-  static const bool enabled = env_int("Q4K_GEMM2", 1) != 0;
-  return enabled && n % kG2N == 0 && m > 0;
+  return n > 0 && n % 16 == 0 && m > 0;
 }
 
 int gemm2_rows(int m) {
@@ -3115,7 +2999,9 @@ TileMap make_tile_map(int tiles_x, int tiles_y, int grid) {
 }
 
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
-  const int tiles_x = a.n / kG2N, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
+  if (!gemm2_supported(a.m, a.n) || a.nb < 1)
+    return hipErrorInvalidValue;
+  const int tiles_x = (a.n + kG2N - 1) / kG2N, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
   static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);
   const int grid = persist && tiles > cus ? cus : tiles;
   const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
@@ -3124,15 +3010,6 @@ hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
     (void)dispatch(q4k_gemm2_kernel<float>, dim3((unsigned)grid), block, s, a, map);
   else
     (void)dispatch(q4k_gemm2_kernel<_Float16>, dim3((unsigned)grid), block, s, a, map);
-  return hipGetLastError();
-}
-
-hipError_t launch_gemm(hipStream_t s, const GemmArgs& a, int dtype) {
-  const dim3 grid((unsigned)((a.n + kBN - 1) / kBN), (unsigned)((a.m + kBM - 1) / kBM)), block(256);
-  if (dtype == kF32)
-    (void)dispatch(q4k_gemm_kernel<float>, grid, block, s, a);
-  else
-    (void)dispatch(q4k_gemm_kernel<_Float16>, grid, block, s, a);
   return hipGetLastError();
 }
 
