@@ -1165,6 +1165,9 @@ __global__ __launch_bounds__(512) void q4k_gemv_splitk_kernel(GemvArgs a, float*
 // issue is spread over the step.
 // ----------------------------------------------------------------------------
 constexpr int kG2M = 128, kG2N = 256, kG2AS = 5, kG2AD = 4;  // A ring slots, A distance
+// Time of one 128-column tile (two column tiles per wave) in tenths of a
+// 256-column tile's, for the choice between the two tilings.
+constexpr int kGemmNarrowTileTime = 6;
 constexpr int kG2ASlot = 16 * 1024;                    // 8 row tiles x 2 fragments x 1 KB
 constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4 tile-blocks
 
@@ -2490,6 +2493,56 @@ struct TgIQ4XS {
   }
 };
 
+// Q4_K on the same template, two column tiles per wave (128 columns per
+// workgroup): for prefill grids that the 256-column Q4_K GEMM leaves short of
+// the CUs.  The dequantisation is that GEMM's (fp16 denormal nibbles, one
+// fp32 fma with d*sc*2^24 or d*sc*2^20 and -dmin*m): the reference's value
+// exactly.
+struct TgQ4K {
+  static constexpr int kTB = kTileBlockBytes, kCT = 2, kAS = 5, kNL = 3, kVPM = 2;
+  struct R {
+    u4_t hd;
+  };
+  struct K {
+    float dl, cl, dh, ch;
+  };
+  struct W {
+    uint2 q;
+  };
+  static __device__ __forceinline__ void issue(const uint8_t* src, uint32_t v16, uint32_t v4, uint32_t l, int) {
+    lds_dma16<0>(src, v16, l);
+    lds_dma16<kSlabBytes>(src, v16, l);
+    lds_dma4<kHeaderOffset>(src, v4, l);
+  }
+  static __device__ __forceinline__ void raw(R& r, const uint8_t* tb, int lane) {
+    r.hd = *reinterpret_cast<const u4_t*>(tb + kHeaderOffset + 16 * (lane & 15));
+  }
+  static __device__ __forceinline__ void consts(K& k, const R& r, int lane) {
+    uint32_t p0, p1;
+    scale_min_packed(r.hd, lane >> 4, p0, p1);
+    const float d = half_bits_to_float(r.hd.x & 0xffffu), dm = half_bits_to_float(r.hd.x >> 16);
+    k.dl = d * (float)(p0 & 0xffu) * 0x1p24f;
+    k.cl = -dm * (float)((p0 >> 16) & 0xffu);
+    k.dh = d * (float)(p1 & 0xffu) * 0x1p20f;
+    k.ch = -dm * (float)((p1 >> 16) & 0xffu);
+  }
+  static __device__ __forceinline__ void words(W& w, const uint8_t* tb, int u, int lane) {
+    w.q = *reinterpret_cast<const uint2*>(tb + (u >> 1) * kSlabBytes + 16 * lane + 8 * (u & 1));
+  }
+  static __device__ __forceinline__ void dequant(const K& k, const W& w, int, h8_t& blo, h8_t& bhi) {
+    const uint32_t lw[4] = {w.q.x, w.q.x >> 8, w.q.y, w.q.y >> 8};
+    u4_t lo, hi;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const h2_t ql = as_h2(lw[t] & 0x000F000Fu), qh = as_h2(lw[t] & 0x00F000F0u);
+      lo[t] = pack_h2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl));
+      hi[t] = pack_h2(__builtin_fmaf((float)qh[0], k.dh, k.ch), __builtin_fmaf((float)qh[1], k.dh, k.ch));
+    }
+    blo = __builtin_bit_cast(h8_t, lo);
+    bhi = __builtin_bit_cast(h8_t, hi);
+  }
+};
+
 // Load accounting of the typed GEMM.  A wave issues per u-step its 4 A
 // fragments of A(t + kAS - 1) spread over its kCT column groups, each group's
 // share followed, at u = 0, by the kNL loads of that column's tile-block of
@@ -2998,10 +3051,25 @@ TileMap make_tile_map(int tiles_x, int tiles_y, int grid) {
   return m;
 }
 
+template <class P>
+hipError_t typed_gemm_launch(hipStream_t s, const GemmArgs& a, int dtype, int cus);
+
+// Rounds of workgroups (tiles / CUs, rounded up) of the 256-column and
+// 128-column tilings, weighted by the time of one tile of each.
+bool gemm2_narrow(int tiles256, int tiles128, int cus) {
+  static const int forced = env_int("Q4K_GEMM_NARROW", -1);  // -1 auto, 0 off, 1 always
+  if (forced >= 0)
+    return forced == 1;
+  const int r4 = (tiles256 + cus - 1) / cus, r2 = (tiles128 + cus - 1) / cus;
+  return r2 * kGemmNarrowTileTime < r4 * 10;
+}
+
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   if (!gemm2_supported(a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
   const int tiles_x = (a.n + kG2N - 1) / kG2N, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
+  if (gemm2_narrow(tiles, ((a.n / 16 + 7) / 8) * tiles_y, cus))
+    return typed_gemm_launch<TgQ4K>(s, a, dtype, cus);
   static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);
   const int grid = persist && tiles > cus ? cus : tiles;
   const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
