@@ -85,11 +85,6 @@ __device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row,
     lo[i] = (_Float16)(t - (float)hi[i]);
     sum += t;
   }
-  if (MODE == kStageGemm) {
-    if (live)
-      *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, c, nb)) = hi;
-    return;
-  }
   if (live) {
     *reinterpret_cast<h8_t*>(xo + frag_offset(row, c, nb)) = hi;
     if (MODE == kStageFragSplit)
@@ -2956,8 +2951,6 @@ hipError_t stage_launch(hipStream_t s, const InT* x, _Float16* xo, _Float16* xs,
   const dim3 grid((unsigned)m), block(256);
   if (mode == kStageFrag)
     (void)dispatch(stage_x_kernel<InT, kStageFrag, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
-  else if (mode == kStageGemm && m < 2048)  // fewer than 256 workgroups of 8 rows: one row each
-    (void)dispatch(stage_x_kernel<InT, kStageGemm, NORM>, grid, block, s, x, xo, xs, rowscale, m, k, nrm);
   else if (mode == kStageGemm && k / 256 <= 16)
     (void)dispatch(stage_gemm_kernel<InT, 16, 32, NORM>, dim3((unsigned)((m + 7) / 8)), block, s, x, xo, rowscale, m, k, nrm);
   else if (mode == kStageGemm && k % 512 == 0 && k / 512 <= 24)  // K <= 12288: one read of x, 64 threads per row
