@@ -331,7 +331,7 @@ struct GemvArgs {
 
 struct GemmArgs {
   const uint8_t* w;
-  const _Float16* xh;  // staged activations, row-major [m, k]
+  const _Float16* xh;  // staged activations in the GEMM order (gemm_frag_offset)
   const float* rowscale;
   void* y;
   const void* aux;
