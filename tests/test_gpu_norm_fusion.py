@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from q4k_ref import make_q4k, make_x, row_rel_err
+from q4k_ref import TYPE_IQ4_XS, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, make_q4k, make_weight, make_x, row_rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -57,6 +57,33 @@ def test_linear_norm(q4k, oracle, gpu, label, m, counts, n, k, post, fused):
     err = row_rel_err(got, ref)
     assert err <= TOL, f"{label}: {err:.3g}"
     assert aux_n == (0 if fused else 1), f"{label}: {aux_n} separate norm launches"
+
+
+@pytest.mark.parametrize("t,m,n,k,post", [(TYPE_Q6_K, 300, 1024, 4096, 0), (TYPE_Q5_K, 130, 592, 2048, 1), (TYPE_Q8_0, 64, 512, 1024, 2),
+                                          (TYPE_IQ4_XS, 200, 768, 2048, 0)])
+def test_linear_norm_typed_prefill(q4k, oracle, gpu, t, m, n, k, post):
+    """The other types' prefill GEMM with attn_norm folded into its staging
+    (no separate norm launch)."""
+    rng = np.random.default_rng(1470 + t + m)
+    w = make_weight(rng, n, k, t)
+    W = q4k.Weight(w, n, k, ggml_type=t)
+    x = make_x(rng, m, k, 3.0)
+    x[1] *= 25.0
+    nw = _norm_weight(rng, k)
+    aux = make_x(rng, m, n, 2.0) if post else None
+    y = torch.from_numpy(aux).to(gpu) if post else torch.full((m, n), float("nan"), device=gpu)
+    torch.cuda.synchronize()
+    q4k.profile_enable(True)
+    q4k.linear_norm(torch.from_numpy(x).to(gpu), W, torch.from_numpy(nw).to(gpu), m, y, auxiliary=y if post else None, gated=(post == 2),
+                    query_counts=[m])
+    torch.cuda.synchronize()
+    aux_n = _aux_launches(q4k)
+    q4k.profile_enable(False)
+    ref = oracle.linear(oracle.rms_norm(x, nw), w, n, k, aux=aux, post=post, ggml_type=t)
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert row_rel_err(got, ref) <= TOL
+    assert aux_n == 0
 
 
 def test_linear_norm_f16(q4k, oracle, gpu):
