@@ -2538,6 +2538,13 @@ struct TgQ4K {
   }
 };
 
+// A policy with two column tiles per wave (128 columns per workgroup) and a
+// 5-slot A ring, for grids the 4-tile form leaves short of the CUs.
+template <class P>
+struct Narrow : P {
+  static constexpr int kCT = 2, kAS = 5;
+};
+
 // Load accounting of the typed GEMM.  A wave issues per u-step its 4 A
 // fragments of A(t + kAS - 1) spread over its kCT column groups, each group's
 // share followed, at u = 0, by the kNL loads of that column's tile-block of
@@ -3231,15 +3238,17 @@ bool typed_gemm_supported(uint32_t type, int m, int n) {
 hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, int dtype, int cus) {
   if (!typed_gemm_supported(type, a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
+  const int ntiles = a.n / 16, tiles_y = (a.m + kG2M - 1) / kG2M;
+  const bool narrow = gemm2_narrow(((ntiles + 15) / 16) * tiles_y, ((ntiles + 7) / 8) * tiles_y, cus);
   switch (type) {
     case kTypeQ5_K:
-      return typed_gemm_launch<TgQ5K>(s, a, dtype, cus);
+      return narrow ? typed_gemm_launch<Narrow<TgQ5K>>(s, a, dtype, cus) : typed_gemm_launch<TgQ5K>(s, a, dtype, cus);
     case kTypeQ6_K:
-      return typed_gemm_launch<TgQ6K>(s, a, dtype, cus);
+      return narrow ? typed_gemm_launch<Narrow<TgQ6K>>(s, a, dtype, cus) : typed_gemm_launch<TgQ6K>(s, a, dtype, cus);
     case kTypeQ8_0:
-      return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);
+      return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);  // two column tiles per wave already
     default:
-      return typed_gemm_launch<TgIQ4XS>(s, a, dtype, cus);
+      return narrow ? typed_gemm_launch<Narrow<TgIQ4XS>>(s, a, dtype, cus) : typed_gemm_launch<TgIQ4XS>(s, a, dtype, cus);
   }
 }
 
