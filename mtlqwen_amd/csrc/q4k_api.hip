@@ -303,6 +303,9 @@ int check_counts(const uint32_t* counts, uint32_t nq, uint32_t m) {
 // hi/lo GEMV.
 constexpr uint32_t kGemmMinColumns = 256;
 constexpr uint32_t kGemvSplitRows = 24;
+// Longest row the staged Q4_K GEMV takes at up to 8 rows; longer rows go to
+// the decode pack and the per-type GEMV.
+constexpr uint32_t kStagedGemvMaxK = 12288;
 
 // The kernel family each phase resolves to.  Decode-shaped phases (0, 2, 3)
 // run the MFMA GEMV; prefill (1) runs the LDS-tiled MFMA GEMM, whose slot also
@@ -612,6 +615,16 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
     Q4K_TRY_HIP(launch_gemv_splitk(stream, a, (int)dtype, plan, ws.part, ws.counters), "gemv split-K launch");
     return Q4K_OK;
+  }
+  if (gemv && !wu && m <= 8 && w->k > kStagedGemvMaxK) {
+    // Long rows with no split-K plan (K = 32768): the fragment staging
+    // reduces each row in one workgroup, so the decode pack (parallel over
+    // blocks) and the per-type GEMV take them (32 us for 8 rows x 32768 ->
+    // 4096, against 41 us staged).
+    int rc = prenorm(stream, ws, w->device, x, norm_w, eps, m, w->k, dtype);
+    if (rc)
+      return rc;
+    return run_gemv_groups_locked(stream, ws, w, x, y, aux, m, post, dtype);
   }
   if (gemv && wu && gemv_gate_up_supported((int)m, (int)(w->k / 256), (int)w->n)) {
     // Fused gate/up GEMV: packs x in registers, no staging launch.

@@ -2,8 +2,8 @@
 (quant_linear.metal:593-618) through the phase it is instantiated for,
 against the CPU oracle: decode (8 one-token queries; the +add pairs with the
 residual epilogue, post 1), prefill_small (one query of 8 rows) and prefill
-(one query of 96 rows).  K = 32768 has no split-K plan and takes the staged
-GEMV in decode.  Bar: max row-relative error 1e-3."""
+(one query of 96 rows).  K = 32768 has no split-K plan and takes the decode
+pack plus the per-type GEMV in decode.  Bar: max row-relative error 1e-3."""
 import numpy as np
 import pytest
 import torch
