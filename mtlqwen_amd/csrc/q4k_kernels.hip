@@ -244,7 +244,11 @@ __device__ __forceinline__ void pack_block_row(const float (&v)[4], int r, int l
 // leaves 8 workgroups, on different XCDs, writing 16 bytes of each line).
 // TPR threads per row (32, or 64 for long rows: 512 threads per workgroup).
 // CPT > 0: the row's K / (8 TPR) <= CPT chunks per thread stay in registers
-// between the maximum and the conversion; CPT == 0: x is read twice.
+// between the maximum and the conversion; CPT == 0: x is read twice.  With
+// 64 threads per row the 8 pieces of a line come from 8 waves at different
+// times, and lines left the L2 partly written (1.38 x the output bytes
+// written at K = 12288): those rows pass their pieces through LDS, half of
+// the chunks at a time, and 8 consecutive lanes then store each line whole.
 // Reduction over the lanes of one staged row: lanes 0..31 and 32..63 of a
 // wave are two rows (TPR = 32), or the whole wave is one (TPR = 64).
 template <int TPR, bool MAX>
@@ -303,9 +307,11 @@ __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restri
   }
   float up, down;
   pow2_scale(mx, up, down);
-  if (!live)
+  // Rows past m write nothing; with the LDS path their waves stay for its
+  // barriers.
+  if (!live && !(CPT > 0 && TPR == 64))
     return;
-  if (q == 0)
+  if (q == 0 && live)
     rowscale[row] = down;
   const float cs = NORM ? up * r : up;
   auto put = [&](int j, const float* w) {
@@ -315,7 +321,40 @@ __global__ __launch_bounds__(8 * TPR) void stage_gemm_kernel(const InT* __restri
       h[i] = (_Float16)(w[i] * cs);
     *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(row, q + TPR * j, nb)) = h;
   };
-  if (CPT > 0) {
+  if constexpr (CPT > 0 && TPR == 64) {
+    // LDS piece (chunk, row of the 8) at 16 (8 chunk + row); CPT / 2 chunks
+    // of every thread per half.
+    constexpr int HALF = (CPT + 1) / 2;
+    __shared__ __attribute__((aligned(16))) h8_t piece[HALF * TPR * 8];
+    const int r8 = t / TPR;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      if (hf)
+        __syncthreads();  // the first half's stores have read their pieces
+#pragma unroll
+      for (int jj = 0; jj < HALF; ++jj) {
+        const int j = hf * HALF + jj;
+        if (j < CPT && j < cpt) {
+          h8_t h;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            h[i] = (_Float16)(v[j][i] * cs);
+          piece[(jj * TPR + q) * 8 + r8] = h;
+        }
+      }
+      __syncthreads();
+      // Thread t stores piece (chunk (t / 8) + 64 i of the half, row t % 8):
+      // lanes 8c .. 8c + 7 write one whole line.
+      const int pr = t & 7, pc = t >> 3;
+      const int prow = blockIdx.x * 8 + pr;
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) {
+        const int jj = i, j = hf * HALF + jj, c = pc + TPR * j;
+        if (j < CPT && j < cpt && prow < m)
+          *reinterpret_cast<h8_t*>(xo + gemm_frag_offset(prow, c, nb)) = piece[(jj * TPR + pc) * 8 + pr];
+      }
+    }
+  } else if (CPT > 0) {
 #pragma unroll
     for (int j = 0; j < (CPT > 0 ? CPT : 1); ++j)
       if (j < cpt)
