@@ -27,6 +27,7 @@ CASES = [
     ("decode, 40 rows", 40, [5] * 8, 1024, 4096, 1, True),
     ("prefill GEMM", 300, [300], 4096, 4096, 0, True),
     ("prefill GEMM, eight-row staging", 2050, [2050], 256, 4096, 2, True),
+    ("prefill GEMM, K=12288 staging through LDS", 300, [300], 256, 12288, 1, True),
     ("split-K (K=12288)", 8, [1] * 8, 4096, 12288, 1, False),
     ("narrow prefill (GEMV groups)", 100, [100], 128, 1024, 0, False),
 ]
