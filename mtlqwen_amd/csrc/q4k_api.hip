@@ -1136,11 +1136,40 @@ int mlp_gate_up_impl(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x
     Q4K_TRY_HIP(launch_typed_gate_up(s, a, wg->type, (int)dtype, device_cus(wg->device)), "typed gate/up launch");
     return Q4K_OK;
   }
+  Workspace& ws = workspace(wg->device);
+  std::lock_guard<std::mutex> lock(ws.mu);
+  if (q4 && resolve(wg, phase).kind == kGemm && m > 16u * kGemvMaxRowTiles && gemm2_supported((int)m, (int)wg->n)) {
+    // Both projections on the pipelined GEMM: one gated launch over x staged
+    // once computes SiLU(gate) * up with the two-call form's roundings (the
+    // same buffer bit for bit), without storing the gate and reading it back.
+    resolve(wu, phase);
+    const size_t rows = (size_t)gemm2_rows((int)m);
+    rc = ensure_workspace(s, ws, wg->device, rows * wg->k, rows);
+    if (rc)
+      return rc;
+    {
+      LaunchTimer timer(s, Q4K_KERNEL_STAGE);
+      Q4K_TRY_HIP(launch_stage_x(s, x, (int)dtype, ws.x, nullptr, ws.scale, (int)m, (int)wg->k, kStageGemm, norm_w, eps), "stage_x launch");
+    }
+    GemmArgs a;
+    a.w = wg->data;
+    a.wu = wu->data;
+    a.xh = ws.x;
+    a.rowscale = ws.scale;
+    a.y = y;
+    a.aux = nullptr;
+    a.m = (int)m;
+    a.n = (int)wg->n;
+    a.k = (int)wg->k;
+    a.nb = (int)(wg->k / 256);
+    a.post = Q4K_POST_GATE;
+    LaunchTimer timer(s, Q4K_KERNEL_GEMM);
+    Q4K_TRY_HIP(launch_gemm2_gated(s, a, (int)dtype, device_cus(wg->device)), "gated gemm launch");
+    return Q4K_OK;
+  }
   // forward.cpp:116-118: gate -> y (post 0), then up with aux = y, post 2, in
   // place.  Both read the same x: it is staged once (with the norm, if any),
   // under one hold of the workspace lock.
-  Workspace& ws = workspace(wg->device);
-  std::lock_guard<std::mutex> lock(ws.mu);
   rc = run_linear_locked(s, ws, wg, nullptr, x, y, nullptr, m, Q4K_POST_STORE, dtype, phase, true, norm_w, eps);
   if (rc)
     return rc;

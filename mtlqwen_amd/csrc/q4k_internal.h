@@ -331,6 +331,7 @@ struct GemvArgs {
 
 struct GemmArgs {
   const uint8_t* w;
+  const uint8_t* wu = nullptr;  // the gated GEMM's up matrix (w is the gate)
   const _Float16* xh;  // staged activations in the GEMM order (gemm_frag_offset)
   const float* rowscale;
   void* y;
@@ -421,6 +422,10 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvSh
 bool gemm2_supported(int m, int n);
 int gemm2_rows(int m);
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus);
+// Gate and up projections of one prefill MLP in one launch (both Q4_K, the
+// same n and k, x staged once): y = SiLU(x W^T) * (x Wu^T) with the
+// roundings of the two-call form (gate stored, then up with post 2 over it).
+hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int cus);
 
 // One MFMA-ceiling launch: `blocks` workgroups of 4 waves, each wave issuing
 // 32 * iters v_mfma_f32_16x16x32_f16 (16384 FLOP each); out holds blocks * 256 floats.

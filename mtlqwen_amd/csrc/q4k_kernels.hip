@@ -1263,6 +1263,43 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
   }
 }
 
+// Epilogue of the gated GEMM's 128 x 32 wave tile: the gate tiles (columns
+// 0, 1 of acc) and the up tiles (2, 3) of the same two output column tiles
+// combine as in the two-call form: SiLU(gate) * up, each of gate and up
+// first unscaled and, for fp16 outputs, rounded to fp16 (the gate value the
+// first call stores, the up value the second call's epilogue forms).  nct of
+// the two output tiles lie inside n.
+template <typename OutT, bool FULL>
+__device__ __forceinline__ void gemm2_epilogue_gated(const GemmArgs& a, const f4_t (&acc)[8][4], int mt0, int ct0, int lane, int nct) {
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const int g = lane >> 4, col = lane & 15;
+  const int row0 = mt0 * 16 + 4 * g;
+  f4_t rs[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+    rs[rt] = *reinterpret_cast<const f4_t*>(a.rowscale + row0 + 16 * rt);
+  const size_t col0 = (size_t)ct0 * 16 + col;
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = row0 + 16 * rt + v;
+      if (!FULL && row >= a.m)
+        continue;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        if (c >= nct)
+          continue;
+        float gv = acc[rt][c][v] * rs[rt][v], uv = acc[rt][2 + c][v] * rs[rt][v];
+        if (sizeof(OutT) == 2) {
+          gv = round_half(gv);
+          uv = round_half(uv);
+        }
+        store_elem(y, (size_t)row * a.n + col0 + 16 * c, silu(gv) * uv);
+      }
+    }
+}
+
 // Tile order of the persistent GEMMs.  Workgroup b runs on XCD b % 8 (the
 // dispatcher deals workgroups to the eight XCDs in turn).  In the plain order
 // tile t = b + i * grid has column block t % tiles_x, so an XCD owns whole
@@ -1303,15 +1340,18 @@ __device__ __forceinline__ void tile_at(const TileMap& m, int i, int& bx, int& b
 
 // One 128 x 256 output tile (column block bx, row block by).  Column tiles
 // at or past ntiles = n / 16 (a last, partial column block) load the last
-// column tile (in bounds) and store nothing.
-template <typename OutT>
+// column tile (in bounds) and store nothing.  GATED: the workgroup's 128
+// output columns of the gated GEMM; wave w takes output column tiles
+// ct0 = 8 bx + 2 w and ct0 + 1, whose gate tiles are its B columns 0, 1 and
+// whose up tiles (a.wu) are its columns 2, 3.
+template <typename OutT, bool GATED>
 __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
   const int nb = a.nb, steps = 4 * nb;
   const int mt0 = by * (kG2M / 16);                         // first row tile
-  const int ct0 = bx * (kG2N / 16) + 4 * wave;              // this wave's first column tile
+  const int ct0 = GATED ? bx * 8 + 2 * wave : bx * (kG2N / 16) + 4 * wave;  // this wave's first column tile
   const uint32_t aring = lds_addr(lds);
   uint8_t* const bring = lds + kG2AS * kG2ASlot + wave * kG2BWave;
   const uint32_t bring0 = lds_addr(bring);
@@ -1331,8 +1371,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   // B(blk, c): tile-block c of block blk (clamped) into ring half blk & 1.
   auto issue_b = [&](int blk, int c) {
     const int bc = blk < nb ? blk : nb - 1;
-    const int ct = ct0 + c < ntiles ? ct0 + c : ntiles - 1;
-    const uint8_t* src = uniform_ptr(a.w + ((size_t)ct * nb + bc) * kTileBlockBytes);
+    const int cc = GATED ? ct0 + (c & 1) : ct0 + c;
+    const int ct = cc < ntiles ? cc : ntiles - 1;
+    const uint8_t* const wm = GATED && c >= 2 ? a.wu : a.w;
+    const uint8_t* src = uniform_ptr(wm + ((size_t)ct * nb + bc) * kTileBlockBytes);
     const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * 4 + c) * kTileBlockBytes);
     lds_dma16<0>(src, voff16, l);
     lds_dma16<kSlabBytes>(src, voff16, l);
@@ -1544,6 +1586,11 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
 
   // One straight-line epilogue per (post code, tile inside m or not).
   const bool full = mt0 * 16 + kG2M <= a.m;
+  if constexpr (GATED) {
+    const int nct2 = ntiles - ct0 >= 2 ? 2 : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
+    full ? gemm2_epilogue_gated<OutT, true>(a, acc, mt0, ct0, lane, nct2) : gemm2_epilogue_gated<OutT, false>(a, acc, mt0, ct0, lane, nct2);
+    return;
+  }
   const int nct = ntiles - ct0 >= 4 ? 4 : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
   if (a.post == 0)
     full ? gemm2_epilogue<OutT, 0, true>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 0, false>(a, acc, mt0, ct0, lane, nct);
@@ -1556,7 +1603,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
 // Persistent launch: workgroup b takes its tiles in the order of the tile
 // map.  Consecutive tiles of a workgroup reuse its LDS rings; a barrier
 // separates the last reads of one tile from the first loads of the next.
-template <typename OutT>
+template <typename OutT, bool GATED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a, TileMap map) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
   const int count = tile_count(map);
@@ -1565,7 +1612,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       __syncthreads();
     int bx, by;
     tile_at(map, i, bx, by);
-    gemm2_tile<OutT>(a, lds, bx, by, a.n / 16);
+    gemm2_tile<OutT, GATED>(a, lds, bx, by, a.n / 16);
   }
 }
 
@@ -3114,9 +3161,24 @@ hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
   const dim3 block(256);
   if (dtype == kF32)
-    (void)dispatch(q4k_gemm2_kernel<float>, dim3((unsigned)grid), block, s, a, map);
+    (void)dispatch(q4k_gemm2_kernel<float, false>, dim3((unsigned)grid), block, s, a, map);
   else
-    (void)dispatch(q4k_gemm2_kernel<_Float16>, dim3((unsigned)grid), block, s, a, map);
+    (void)dispatch(q4k_gemm2_kernel<_Float16, false>, dim3((unsigned)grid), block, s, a, map);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
+  if (!gemm2_supported(a.m, a.n) || a.nb < 1 || !a.wu)
+    return hipErrorInvalidValue;
+  // 128 output columns (256 B columns: gate and up) per tile.
+  const int tiles_x = (a.n / 16 + 7) / 8, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
+  const int grid = tiles > cus ? cus : tiles;
+  const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
+  const dim3 block(256);
+  if (dtype == kF32)
+    (void)dispatch(q4k_gemm2_kernel<float, true>, dim3((unsigned)grid), block, s, a, map);
+  else
+    (void)dispatch(q4k_gemm2_kernel<_Float16, true>, dim3((unsigned)grid), block, s, a, map);
   return hipGetLastError();
 }
 
