@@ -274,8 +274,9 @@ def configs_bench(dev, parts=("config2", "config3"), sets=3):
         counts 5 (the decode phase, forward.cpp:190): QKV 4096 -> 6144, O
         4096 -> 4096 with the residual, and the config-1 MLP (q4k_mlp);
       config 3: ragged prefill of lengths {512,37,1,1,200,5,1,64} = 821 rows
-        (the prefill phase): QKV, O with the residual, gate (post 0), up with
-        in-place SiLU gating (post 2), down with the residual, then
+        (the prefill phase): QKV, O with the residual, gate and up in one
+        q4k_mlp_gate_up call (SiLU(gate) * up into the gate buffer, one gated
+        GEMM launch), down with the residual, then
         rms_norm_gather of each sequence's last row and the Q4_K LM head
         4096 -> 248,320 on those 8 rows (forward.cpp:72-75, 115-119).
     Reports the time per pass and its algorithmic rate: weight + activation
@@ -356,8 +357,7 @@ def configs_bench(dev, parts=("config2", "config3"), sets=3):
     def pass3():
         q4k.linear(x, qkv, M, yq, query_counts=lengths)
         q4k.linear(x, o, M, hidden, auxiliary=hidden, query_counts=lengths)
-        q4k.linear(x, gw, M, gate, query_counts=lengths)
-        q4k.linear(x, uw, M, gate, auxiliary=gate, gated=True, query_counts=lengths)
+        q4k.mlp_gate_up(x, gw, uw, M, gate, query_counts=lengths)
         q4k.linear(gate, dw, M, hidden, auxiliary=hidden, query_counts=lengths)
         q4k.rms_norm_gather(hidden, norm_w, lm_rows, lengths, [1] * 8)
         q4k.linear(lm_rows, head, 8, logits, query_counts=[8])
@@ -365,7 +365,7 @@ def configs_bench(dev, parts=("config2", "config3"), sets=3):
     dt = run(pass3)
     flops = 2 * M * K * (6144 + K + 2 * F + F)
     head_flops = 2 * 8 * K * 248320
-    out["config3"] = {"workload": "M=821 ragged prefill {512,37,1,1,200,5,1,64}: QKV, O + residual, gate, up (SiLU gating in place), down + residual, rms_norm_gather, Q4_K LM head 4096->248320 on 8 rows",
+    out["config3"] = {"workload": "M=821 ragged prefill {512,37,1,1,200,5,1,64}: QKV, O + residual, gate/up (q4k_mlp_gate_up: one gated GEMM launch, SiLU(gate) * up), down + residual, rms_norm_gather, Q4_K LM head 4096->248320 on 8 rows",
                       "us_per_pass": round(dt * 1e6, 2), "projection_flop": flops, "tflops_incl_lm_head": round((flops + head_flops) / dt / 1e12, 1),
                       "kernels": {"prefill": qkv.kernel_name(1), "lm_head": head.kernel_name(2)}}
     return out
@@ -552,9 +552,9 @@ def prefill_bench(args, dev):
     with torch.cuda.graph(graph):
         for _ in range(per_graph):
             step()
-    # Untimed warm-up by wall time: in a kernel trace the gate GEMM of the
-    # first replays takes 237-282 us and settles near 200 us after about
-    # 30 ms of back-to-back GEMMs.
+    # Untimed warm-up by wall time: in a kernel trace the GEMMs of the first
+    # replays run up to 15 % slower than after about 30 ms of back-to-back
+    # GEMMs.
     t_end = time.perf_counter() + args.prefill_warmup_ms * 1e-3
     while True:
         timed_graph(graph, 2)
@@ -562,19 +562,29 @@ def prefill_bench(args, dev):
             break
     elapsed = timed_graph(graph, args.prefill_steps)
     ms = elapsed / (args.prefill_steps * per_graph) * 1e3
-    q4k.profile_enable(True)
-    for _ in range(args.prefill_steps):
-        step()
-    torch.cuda.synchronize()
-    gemm_ms, gemm_n = kernel_avg_ms(q4k, q4k.KERNEL_GEMM)
-    q4k.profile_enable(False)
+    # Per-kernel durations, each GEMM family timed on its own (eager launches
+    # carrying start/stop events): the gated gate/up GEMM (both projections
+    # of the step in one launch), then the down GEMM.
+    def timed_gemm(fn):
+        q4k.profile_enable(True)
+        for _ in range(args.prefill_steps):
+            fn()
+        torch.cuda.synchronize()
+        avg, n = kernel_avg_ms(q4k, q4k.KERNEL_GEMM)
+        q4k.profile_enable(False)
+        return avg, n
+
+    gu_ms, gu_n = timed_gemm(lambda: q4k.mlp_gate_up(x, G, U, M, gate, query_counts=counts))
+    dn_ms, dn_n = timed_gemm(lambda: q4k.linear(gate, D, M, out, query_counts=counts))
     flop_gemm = 2.0 * M * N * K
     return {
         "ms_per_step": ms,
         "tflops": 3 * flop_gemm / (ms * 1e-3) / 1e12,
-        "gemm_avg_us": gemm_ms * 1e3,
-        "gemm_launches": gemm_n,
-        "gemm_tflops": flop_gemm / (gemm_ms * 1e-3) / 1e12,
+        "gated_gemm_avg_us": gu_ms * 1e3,
+        "gated_gemm_launches": gu_n,
+        "gated_gemm_tflops": 2 * flop_gemm / (gu_ms * 1e-3) / 1e12,
+        "down_gemm_avg_us": dn_ms * 1e3,
+        "down_gemm_tflops": flop_gemm / (dn_ms * 1e-3) / 1e12,
     }
 
 
@@ -789,20 +799,23 @@ def main():
     }
     if pre:
         line["prefill"] = {
-            "workload": "config4: M=2048 Q4_K MLP (gate, up with in-place SiLU gating, down) on MFMA GEMM",
+            "workload": "config4: M=2048 Q4_K MLP on MFMA GEMM: gate and up in one gated GEMM launch (SiLU(gate) * up into the gate buffer), then down",
             "value": round(pre["tflops"], 2),
             "unit": "TFLOP/s",
             "ms_per_step": round(pre["ms_per_step"], 4),
             "roofline": {
-                "kernel": "q4k_gemm2_kernel (M=2048, 206.16 GFLOP per launch)",
+                "kernel": "q4k_gemm2_kernel<float,true> (gated gate/up GEMM, M=2048, K=4096, N=12288 x2: 412.32 GFLOP per launch)",
                 "bound": "mfma",
-                "achieved": round(pre["gemm_tflops"], 1),
+                "achieved": round(pre["gated_gemm_tflops"], 1),
                 "peak": FP16_DENSE_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
-                "frac": round(pre["gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4),
+                "frac": round(pre["gated_gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4),
                 "traffic": profiled_traffic("gemm2_config4_traffic.txt"),
-                "avg_us": round(pre["gemm_avg_us"], 2),
+                "avg_us": round(pre["gated_gemm_avg_us"], 2),
             },
+            "down_gemm": {"kernel": "q4k_gemm2_kernel<float,false> (K=12288 -> N=4096, 206.16 GFLOP)",
+                          "avg_us": round(pre["down_gemm_avg_us"], 2), "tflops": round(pre["down_gemm_tflops"], 1),
+                          "frac": round(pre["down_gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4)},
         }
     print(json.dumps(line), flush=True)
 
