@@ -147,8 +147,10 @@ int q4k_linear_noalloc(void* stream, q4k_weight* w, const void* x, void* y, cons
 
 /* Gated MLP projection (model/qwen35/forward.cpp:115-118).
  * Decode passes: one fused gate/up kernel, y = silu(x.Wg^T) * (x.Wu^T)
- * (fused_kernels.metal:44-78).  Other passes: the reference's two calls,
- * gate with post 0 into y, then up with post 2 over y in place.
+ * (fused_kernels.metal:44-78).  Other passes: the result of the reference's
+ * two calls, gate with post 0 into y, then up with post 2 over y in place;
+ * Q4_K pairs at prefill row counts compute it in one gated GEMM launch (y
+ * bit for bit as the two calls leave it), other cases make the two calls.
  * y is the gate buffer [m, n]. */
 int q4k_mlp_gate_up(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x, void* y, uint32_t m, const uint32_t* query_counts,
                     uint32_t nqueries, uint32_t dtype);
