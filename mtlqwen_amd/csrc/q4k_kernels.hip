@@ -941,9 +941,13 @@ __global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
 // b % 8), so their partials meet in one L2.
 // ----------------------------------------------------------------------------
 // Bytes of LDS one split-K slice uses.
+// The slice of x as read: one row of one block per (block, row) pair, 1 KB
+// of fp32 (512 B of fp16) at a stride of 1040 B, so that the 8 rows' 128-byte
+// reads of the pack fall in different banks.
+constexpr int kSplitkStageStride = 1040;
 template <int NM, int T, int BPS, int DP>
 constexpr int splitk_lds_bytes() {
-  return 8 * DP * (NM * T / 8) * kTileBlockBytes + BPS * 8 * 64 * 16 + BPS * 64 * 8 + BPS * 8 * 4 + BPS * 8 * 1024;
+  return 8 * DP * (NM * T / 8) * kTileBlockBytes + BPS * 8 * 64 * 16 + BPS * 64 * 8 + BPS * 8 * 4 + BPS * 8 * kSplitkStageStride;
 }
 
 // One workgroup's K-slice ks of column group grp (see above), over LDS of
@@ -958,7 +962,7 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
   constexpr int kFragBytes = BPS * 8 * 64 * 16;  // [BPS][8 fragments][64 lanes] x 16 B
   constexpr int kXsBytes = BPS * 64 * 8;         // [BPS][64 lanes] x 4 halves
   constexpr int kDscBytes = BPS * 8 * 4;         // [BPS][8 rows]
-  constexpr int kStageBytes = BPS * 8 * 1024;    // the slice of x as read: [BPS * 8 (block, row) pairs] x 1 KB
+  constexpr int kStageBytes = BPS * 8 * kSplitkStageStride;  // the slice of x as read, per (block, row) pair
   constexpr int kSlots = DP * PW;                // ring slots per wave
   constexpr int kRingBytes = W * kSlots * kTileBlockBytes;
   static_assert(kRingBytes + kFragBytes + kXsBytes + kDscBytes + kStageBytes == splitk_lds_bytes<NM, T, BPS, DP>(), "LDS layout");
@@ -1011,7 +1015,7 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
     for (int j = 0; j < PPW; ++j) {
       const int pr = wave + W * j, r = pr & 7;
       const OutT* src = xin + (size_t)r * a.k + (size_t)(kb0 + (pr >> 3)) * 256;
-      const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr(stage + (size_t)pr * 1024));
+      const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr(stage + (size_t)pr * kSplitkStageStride));
       if (sizeof(OutT) == 4) {
         lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
       } else {
@@ -1026,24 +1030,50 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
     issue(i);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PW * DP) : "memory");
   __syncthreads();
+  // Wave w < BPS packs block w of the slice, all 8 rows, as the fused gate/up
+  // GEMV packs its blocks: lane 16 g + 8 h + r takes elements 64 g + 32 h +
+  // [0, 32) of row r (128 contiguous bytes of the stage), so that the row
+  // maximum and the sub-block sums are mostly in-lane, and writes the block's
+  // fragments, min-term operands and unscale factors to LDS.  Rows >= m are
+  // zero.
+  static_assert(BPS <= W, "one block per packing wave");
+  if (wave < BPS) {
+    const int r = lane & 7, e0 = 64 * (lane >> 4) + 32 * ((lane >> 3) & 1);
+    const uint8_t* src = stage + (size_t)(8 * wave + r) * kSplitkStageStride;
+    float t32[32];
+    if (sizeof(OutT) == 4) {
 #pragma unroll
-  for (int j = 0; j < PPW; ++j) {
-    const int pr = wave + W * j, i = pr >> 3, r = pr & 7;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (live) {
-      if (sizeof(OutT) == 4) {
-        const f4_t t4 = *reinterpret_cast<const f4_t*>(stage + (size_t)pr * 1024 + 16 * lane);
+      for (int c = 0; c < 8; ++c) {
+        const f4_t v4 = *reinterpret_cast<const f4_t*>(src + 4 * e0 + 16 * c);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          v[e] = t4[e];
-      } else {
-        const h4_t t4 = *reinterpret_cast<const h4_t*>(stage + (size_t)pr * 1024 + 8 * lane);
+          t32[4 * c + e] = v4[e];
+      }
+    } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] = (float)t4[e];
+      for (int c = 0; c < 4; ++c) {
+        const h8_t v8 = *reinterpret_cast<const h8_t*>(src + 2 * e0 + 16 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          t32[8 * c + e] = (float)v8[e];
       }
     }
-    pack_block_row(v, r, lane, xf + (size_t)i * 8 * 64, reinterpret_cast<h4_t*>(xs) + (size_t)i * 64, const_cast<float*>(dscl) + (size_t)i * 8);
+    if (r >= a.m) {
+#pragma unroll
+      for (int e = 0; e < 32; ++e)
+        t32[e] = 0.0f;
+    }
+    XBlock xb;
+    pack_x_regs(t32, lane, xb);
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+      xf[((size_t)wave * 8 + f) * 64 + lane] = __builtin_bit_cast(u4_t, xb.frag[f]);
+    reinterpret_cast<h4_t*>(xs)[(size_t)wave * 64 + lane] = xb.xs;
+    if (lane == 0 || lane == 16) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        const_cast<float*>(dscl)[wave * 8 + (lane >> 2) + v] = xb.dv[v];
+    }
   }
   __syncthreads();
 
