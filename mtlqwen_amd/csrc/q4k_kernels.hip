@@ -1286,7 +1286,11 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
         float acc_v = acc[rt][c][v] * rs[rt][v];
         if (sizeof(OutT) == 2)
           acc_v = round_half(acc_v);
-        const float out = POST == 1 ? acc_v + cur[v][c] : POST == 2 ? silu(cur[v][c]) * acc_v : acc_v;
+        float out = POST == 1 ? acc_v + cur[v][c] : POST == 2 ? silu(cur[v][c]) * acc_v : acc_v;
+        // The fp32 value is formed before any conversion to fp16: fused into
+        // the conversion (v_fma_mix) the product would round once instead of
+        // twice, as the reference's half(silu(g) * u) does.
+        asm("" : "+v"(out));
         store_elem(y, (size_t)row * a.n + col0 + 16 * c, out);
       }
     }
@@ -1325,7 +1329,9 @@ __device__ __forceinline__ void gemm2_epilogue_gated(const GemmArgs& a, const f4
           gv = round_half(gv);
           uv = round_half(uv);
         }
-        store_elem(y, (size_t)row * a.n + col0 + 16 * c, silu(gv) * uv);
+        float out = silu(gv) * uv;
+        asm("" : "+v"(out));  // the fp32 value first, as in the post-2 epilogue
+        store_elem(y, (size_t)row * a.n + col0 + 16 * c, out);
       }
     }
 }
