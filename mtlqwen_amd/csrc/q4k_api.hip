@@ -404,6 +404,26 @@ int ensure_splitk_workspace(hipStream_t stream, Workspace& ws, int device, size_
   return Q4K_OK;
 }
 
+// The pipelined GEMM of a shape with few tiles for the CUs runs two K-halves
+// per tile (gemm2_split): their accumulators and arrival counters live in
+// the split-K workspace.
+int device_cus(int device);
+
+int gemm2_split_buffers(hipStream_t stream, Workspace& ws, int device, GemmArgs& a, bool gated) {
+  if (!gemm2_split(a.m, a.n, a.nb, device_cus(device)))
+    return Q4K_OK;
+  size_t part_floats = 0, counters = 0;
+  gemm2_split_workspace(a.m, a.n, gated, &part_floats, &counters);
+  int rc = ensure_splitk_workspace(stream, ws, device, part_floats, counters);
+  if (rc)
+    return rc;
+  if (ws.fixed)  // the scratch's counters start at zero for this launch (a fill kernel: capture-safe)
+    Q4K_TRY_HIP(launch_fill_u32(stream, reinterpret_cast<uint32_t*>(ws.counters), 0u, (uint32_t)counters), "counter fill launch");
+  a.part = ws.part;
+  a.counters = ws.counters;
+  return Q4K_OK;
+}
+
 // Packs x (m <= 8 rows) for the per-item and persistent GEMVs.
 int stage_pack(hipStream_t stream, Workspace& ws, int device, const void* x, uint32_t dtype, uint32_t m, uint32_t k, DecodePack* pk) {
   const size_t nb = k / 256;
@@ -711,6 +731,9 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.k = (int)w->k;
     a.nb = (int)(w->k / 256);
     a.post = (int)post;
+    rc = gemm2_split_buffers(stream, ws, w->device, a, false);
+    if (rc)
+      return rc;
     LaunchTimer timer(stream, Q4K_KERNEL_GEMM);
     Q4K_TRY_HIP(launch_gemm2(stream, a, (int)dtype, device_cus(w->device)), "gemm launch");
   }
@@ -960,13 +983,13 @@ int check_linear(const q4k_weight* w, const void* x, const void* y, const void* 
 // address of each GPU's copy comes from hipGetSymbolAddress, taken once per
 // device at that device's first call (with the device current), and only
 // that address is used (kernel arguments, fills).
-constexpr size_t kScratchBytes = 64ull << 20;
+constexpr size_t kScratchBytes = 88ull << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 // Fixed regions of the scratch: decode pack, split-K partials and counters,
 // row scales; the rest holds the staged activations.
 constexpr size_t kScrPackBytes = 2ull << 20;
-constexpr size_t kScrPartBytes = 8ull << 20;
+constexpr size_t kScrPartBytes = 32ull << 20;  // the largest two-K-halves GEMM (128 tiles)
 constexpr size_t kScrCounterBytes = 16ull << 10;
 constexpr size_t kScrScaleBytes = 256ull << 10;
 constexpr size_t kScrXBytes = kScratchBytes - kScrPackBytes - kScrPartBytes - kScrCounterBytes - kScrScaleBytes;
@@ -1163,6 +1186,9 @@ int mlp_gate_up_impl(void* stream, q4k_weight* wg, q4k_weight* wu, const void* x
     a.k = (int)wg->k;
     a.nb = (int)(wg->k / 256);
     a.post = Q4K_POST_GATE;
+    rc = gemm2_split_buffers(s, ws, wg->device, a, true);
+    if (rc)
+      return rc;
     LaunchTimer timer(s, Q4K_KERNEL_GEMM);
     Q4K_TRY_HIP(launch_gemm2_gated(s, a, (int)dtype, device_cus(wg->device)), "gated gemm launch");
     return Q4K_OK;

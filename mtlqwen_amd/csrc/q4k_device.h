@@ -238,6 +238,19 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return r;
 }
 
+// The store reads its 16 data bytes after issue: a vector write to them must
+// wait (wait states the compiler cannot insert after an asm store), hence the
+// s_nop.
+__device__ __forceinline__ void store_coherent4(float* p, f4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 2" ::"v"(p), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ f4_t load_coherent4(const float* p) {
+  f4_t r;
+  asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(r) : "v"(p));
+  return r;
+}
+
 // Pins a register value to this point of the program: an asm load's result
 // is used only after the explicit wait that precedes hold().
 template <typename V>

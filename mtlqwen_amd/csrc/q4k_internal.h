@@ -337,6 +337,10 @@ struct GemmArgs {
   void* y;
   const void* aux;
   int m, n, k, nb, post;
+  // K-halves (gemm2_split): the halves' accumulators and per-tile arrival
+  // counters (zero before the launch; every launch leaves them zero).
+  float* part = nullptr;
+  int* counters = nullptr;
 };
 
 struct GatherIndex {
@@ -421,6 +425,10 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a, int dtype, const GemvSh
 // (kStageGemm) for gemm2_rows(m) rows; any N that is a multiple of 16.
 bool gemm2_supported(int m, int n);
 int gemm2_rows(int m);
+// Whether the pipelined GEMM (plain and gated alike) of this shape runs as two
+// K-halves per tile (few tiles for the CUs), and the workspace it then needs.
+bool gemm2_split(int m, int n, int nb, int cus);
+void gemm2_split_workspace(int m, int n, bool gated, size_t* part_floats, size_t* counters);
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus);
 // Gate and up projections of one prefill MLP in one launch (both Q4_K, the
 // same n and k, x staged once): y = SiLU(x W^T) * (x Wu^T) with the

@@ -1380,12 +1380,15 @@ __device__ __forceinline__ void tile_at(const TileMap& m, int i, int& bx, int& b
 // output columns of the gated GEMM; wave w takes output column tiles
 // ct0 = 8 bx + 2 w and ct0 + 1, whose gate tiles are its B columns 0, 1 and
 // whose up tiles (a.wu) are its columns 2, 3.
-template <typename OutT, bool GATED>
-__device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles) {
+template <typename OutT, bool GATED, bool SPLIT>
+__device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles, int kb0, int nbr, int item,
+                                           int* s_last) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int nb = a.nb, steps = 4 * nb;
+  // Blocks [kb0, kb0 + nbr) of K (all of them unless SPLIT); u-steps and
+  // ring positions count from kb0.
+  const int nb = a.nb, steps = 4 * nbr;
   const int mt0 = by * (kG2M / 16);                         // first row tile
   const int ct0 = GATED ? bx * 8 + 2 * wave : bx * (kG2N / 16) + 4 * wave;  // this wave's first column tile
   const uint32_t aring = lds_addr(lds);
@@ -1398,7 +1401,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   // (clamped to the last u-step past the end).
   auto issue_a = [&](int t, int i) {
     const int tc = t < steps ? t : steps - 1;
-    const int b = tc >> 2, u = tc & 3;
+    const int b = kb0 + (tc >> 2), u = tc & 3;
     const int f = 4 * wave + i;
     const _Float16* src = xh + ((((size_t)by * nb + b) * 4 + u) * 16 + f) * 512;
     const uint32_t l = __builtin_amdgcn_readfirstlane(aring + (uint32_t)(t % kG2AS) * kG2ASlot + (uint32_t)f * 1024);
@@ -1406,7 +1409,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   };
   // B(blk, c): tile-block c of block blk (clamped) into ring half blk & 1.
   auto issue_b = [&](int blk, int c) {
-    const int bc = blk < nb ? blk : nb - 1;
+    const int bc = kb0 + (blk < nbr ? blk : nbr - 1);
     const int cc = GATED ? ct0 + (c & 1) : ct0 + c;
     const int ct = cc < ntiles ? cc : ntiles - 1;
     const uint8_t* const wm = GATED && c >= 2 ? a.wu : a.w;
@@ -1511,10 +1514,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
   // at xa + 16 KB * t of the staging and at 4 KB * wave of ring slot t % 5;
   // fragment i is the instruction offset 1 KB * i.  The ring addresses of
   // the slot read (ar) and written (aw) roll instead of being recomputed.
-  const uint8_t* const xa = reinterpret_cast<const uint8_t*>(xh) + ((size_t)by * nb * 64 + 4 * wave) * 1024;
+  const uint8_t* const xa = reinterpret_cast<const uint8_t*>(xh) + ((size_t)by * nb * 64 + (size_t)kb0 * 64 + 4 * wave) * 1024;
   const uint32_t aend = aring + kG2AS * kG2ASlot;
   uint32_t ar = aring, aw = aring + kG2AD * kG2ASlot + 4096u * (uint32_t)wave;
-  for (int blk = 0; blk < nb; ++blk) {
+  for (int blk = 0; blk < nbr; ++blk) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * blk + u;
@@ -1620,6 +1623,44 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
     for (int c = 0; c < 4; ++c)
       asm volatile("" : "+a"(acc[rt][c]));
 
+  if constexpr (SPLIT) {
+    // Two K-halves per tile (items 2 tile, 2 tile + 1): each stores its
+    // accumulators (written through to memory), and the second to arrive
+    // adds the other's and runs the epilogue.  fp32 addition commutes, so
+    // the result does not depend on which half arrives last.
+    constexpr size_t kWaveFloats = 32 * 64 * 4;
+    float* const mine = a.part + ((size_t)item * 4 + wave) * kWaveFloats + 4 * lane;
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        store_coherent4(mine + (rt * 4 + c) * 256, acc[rt][c]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+      *s_last = count_arrival(&a.counters[item >> 1]) == 1;
+    __syncthreads();
+    if (!*s_last)
+      return;
+    const float* const other = a.part + ((size_t)(item ^ 1) * 4 + wave) * kWaveFloats + 4 * lane;
+    f4_t pv[8][4];
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        pv[rt][c] = load_coherent4(other + (rt * 4 + c) * 256);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        hold(pv[rt][c]);
+        acc[rt][c] += pv[rt][c];
+      }
+    if (tid == 0)
+      reset_counter(&a.counters[item >> 1]);  // ready for the next launch
+  }
+
   // One straight-line epilogue per (post code, tile inside m or not).
   const bool full = mt0 * 16 + kG2M <= a.m;
   if constexpr (GATED) {
@@ -1639,16 +1680,30 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
 // Persistent launch: workgroup b takes its tiles in the order of the tile
 // map.  Consecutive tiles of a workgroup reuse its LDS rings; a barrier
 // separates the last reads of one tile from the first loads of the next.
-template <typename OutT, bool GATED>
+// SPLIT: items 2 t and 2 t + 1 are the two K-halves of tile t (plain tile
+// order), taken in turn by the workgroups.
+template <typename OutT, bool GATED, bool SPLIT = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a, TileMap map) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
-  const int count = tile_count(map);
-  for (int i = 0; i < count; ++i) {
-    if (i > 0)
-      __syncthreads();
-    int bx, by;
-    tile_at(map, i, bx, by);
-    gemm2_tile<OutT, GATED>(a, lds, bx, by, a.n / 16);
+  __shared__ int s_last;
+  if constexpr (SPLIT) {
+    const int half = a.nb >> 1;
+    for (int it = (int)blockIdx.x, i = 0; it < 2 * map.tiles; it += (int)gridDim.x, ++i) {
+      if (i > 0)
+        __syncthreads();
+      const int tile = it >> 1, ks = it & 1;
+      gemm2_tile<OutT, GATED, true>(a, lds, tile % map.tiles_x, tile / map.tiles_x, a.n / 16, ks ? half : 0, ks ? a.nb - half : half, it,
+                                    &s_last);
+    }
+  } else {
+    const int count = tile_count(map);
+    for (int i = 0; i < count; ++i) {
+      if (i > 0)
+        __syncthreads();
+      int bx, by;
+      tile_at(map, i, bx, by);
+      gemm2_tile<OutT, GATED, false>(a, lds, bx, by, a.n / 16, 0, a.nb, 0, &s_last);
+    }
   }
 }
 
@@ -3186,10 +3241,46 @@ bool gemm2_narrow(int tiles256, int tiles128, int cus) {
   return r2 * kGemmNarrowTileTime < r4 * 10;
 }
 
+// Two K-halves per tile when the tiles fill at most half the CUs and K is
+// long (K >= 8192: the halves' write-through exchange, about 20 us per
+// launch, is then smaller than what the second half of the CUs saves; at
+// M = 821 it takes the K = 12288 down projection from 119.7 us on the
+// 128-column template to 107.2 us, while the K = 4096 O projection went
+// from 48.6 to 54.4 us and keeps the template).
+bool gemm2_split(int m, int n, int nb, int cus) {
+  static const int on = env_int("Q4K_GEMM2_SPLIT", 1);
+  const int tiles = ((n + kG2N - 1) / kG2N) * ((m + kG2M - 1) / kG2M);
+  return on && nb >= 32 && 2 * tiles <= cus;
+}
+
+void gemm2_split_workspace(int m, int n, bool gated, size_t* part_floats, size_t* counters) {
+  const int tiles_x = gated ? (n / 16 + 7) / 8 : (n + kG2N - 1) / kG2N, tiles = tiles_x * ((m + kG2M - 1) / kG2M);
+  *part_floats = (size_t)2 * tiles * 4 * 32 * 64 * 4;
+  *counters = (size_t)tiles;
+}
+
+namespace {
+template <bool GATED>
+hipError_t gemm2_split_launch(hipStream_t s, const GemmArgs& a, int dtype, int tiles_x, int tiles_y, int cus) {
+  const int tiles = tiles_x * tiles_y, grid = 2 * tiles < cus ? 2 * tiles : cus;
+  const TileMap map{tiles_x, tiles, 0, 0, 0};
+  if (dtype == kF32)
+    (void)dispatch(q4k_gemm2_kernel<float, GATED, true>, dim3((unsigned)grid), dim3(256), s, a, map);
+  else
+    (void)dispatch(q4k_gemm2_kernel<_Float16, GATED, true>, dim3((unsigned)grid), dim3(256), s, a, map);
+  return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   if (!gemm2_supported(a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
   const int tiles_x = (a.n + kG2N - 1) / kG2N, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
+  if (gemm2_split(a.m, a.n, a.nb, cus)) {
+    if (!a.part || !a.counters)
+      return hipErrorInvalidValue;
+    return gemm2_split_launch<false>(s, a, dtype, tiles_x, tiles_y, cus);
+  }
   if (gemm2_narrow(tiles, ((a.n / 16 + 7) / 8) * tiles_y, cus))
     return typed_gemm_launch<TgQ4K>(s, a, dtype, cus);
   static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);
@@ -3208,6 +3299,13 @@ hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int c
     return hipErrorInvalidValue;
   // 128 output columns (256 B columns: gate and up) per tile.
   const int tiles_x = (a.n / 16 + 7) / 8, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
+  // K-halves exactly when the plain GEMM of this shape takes them, so that
+  // the gated launch stays bit-identical to the gate-then-up calls.
+  if (gemm2_split(a.m, a.n, a.nb, cus)) {
+    if (!a.part || !a.counters)
+      return hipErrorInvalidValue;
+    return gemm2_split_launch<true>(s, a, dtype, tiles_x, tiles_y, cus);
+  }
   const int grid = tiles > cus ? cus : tiles;
   const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
   const dim3 block(256);

@@ -5,7 +5,8 @@ up with post 2 over it in place) run through linear(): the same buffer bit for
 bit, one GEMM launch instead of two, and the oracle on the first and last row
 of every 128-row block.  Cases: ragged row blocks and column blocks (a
 workgroup with one live output tile), one block of K, fp16 activations, the
-config-4 shape, and the ffn_norm folded into the shared staging.
+config-4 shape, long K with few tiles (two K-halves per tile, summed by the
+second half to finish), and the ffn_norm folded into the shared staging.
 Bar for the oracle: max row-relative error 1e-3."""
 import numpy as np
 import pytest
@@ -34,9 +35,11 @@ def _gemm_launches(q4k, fn):
 
 
 # (m, n, k, dtype): n = 1296 and 272 leave the last 128-column workgroup one
-# live output tile; k = 256 is one block.
+# live output tile; k = 256 is one block; k = 8192 and 12288 with few tiles
+# run as two K-halves per tile in both forms.
 SHAPES = [(300, 512, 1024, torch.float32), (257, 1296, 2048, torch.float32), (129, 272, 1024, torch.float32),
-          (130, 512, 256, torch.float16), (2048, 12288, 4096, torch.float32)]
+          (130, 512, 256, torch.float16), (2048, 12288, 4096, torch.float32),
+          (200, 1024, 8192, torch.float32), (130, 512, 12288, torch.float16)]
 
 
 @pytest.mark.parametrize("m,n,k,dtype", SHAPES)

@@ -29,6 +29,7 @@ CASES = [
     ("persistent GEMV (wide N)", 65536, 4096, (8, [1] * 8), (2, [1] * 2), 0, torch.float32),
     ("staged GEMV (40 rows)", 4096, 4096, (40, [5] * 8), (20, [5] * 4), 0, torch.float32),
     ("prefill GEMM", 4096, 4096, (300, [300]), (129, [129]), 2, torch.float32),
+    ("prefill GEMM in two K-halves", 1024, 8192, (300, [300]), (129, [129]), 1, torch.float32),
     ("narrow prefill (GEMV groups)", 128, 1024, (100, [100]), (30, [30]), 0, torch.float32),
     ("fp16 prefill GEMM", 512, 2048, (200, [200]), (70, [70]), 1, torch.float16),
     ("fp16 decode GEMV", 1024, 2048, (8, [1] * 8), (5, [1] * 5), 0, torch.float16),
