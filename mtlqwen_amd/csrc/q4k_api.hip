@@ -718,7 +718,7 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.rows = rows;
     a.split = split ? 1 : 0;
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr), wu != nullptr), "gemv launch");
+    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr, device_cus(w->device)), wu != nullptr), "gemv launch");
   } else {
     GemmArgs a;
     a.w = w->data;

@@ -396,7 +396,7 @@ struct GemvShape {
 // rows = staged fragment rows (2m when split).  The environment variables
 // Q4K_GEMV_TILES (1 or 2) and Q4K_GEMV_WAVES (4, 8 or 16) override the
 // column tiles and waves per workgroup, for tuning.
-GemvShape gemv_shape(int rows, int n, int nb, bool gated);
+GemvShape gemv_shape(int rows, int n, int nb, bool gated, int cus);
 
 // Fused gate/up GEMV for m <= 8 rows and K = 4096 that packs x itself (no
 // staging launch); reads a.x, a.w, a.wu (and a.norm_w when set) and writes a.y.

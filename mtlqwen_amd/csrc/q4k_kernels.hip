@@ -2978,7 +2978,11 @@ hipError_t gemv_one_row_tile(hipStream_t s, const GemvArgs& a, int dtype, int wa
 }
 
 template <int RT, bool GATED>
-hipError_t gemv_multi_row_tile(hipStream_t s, const GemvArgs& a, int dtype, int waves) {
+hipError_t gemv_multi_row_tile(hipStream_t s, const GemvArgs& a, int dtype, int waves, int tiles) {
+  if constexpr (!GATED) {
+    if (tiles == 2)
+      return gemv_launch<RT, 2, 4, 0, false>(s, a, dtype);
+  }
   if (waves >= 8)
     return gemv_launch<RT, 1, 8, 0, GATED>(s, a, dtype);
   return gemv_launch<RT, 1, 4, 0, GATED>(s, a, dtype);
@@ -2996,8 +3000,8 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a, int dtype, const Gemv
     return gemv_one_row_tile<1, GATED>(s, a, dtype, shape.waves);
   }
   if (shape.row_tiles == 2)
-    return gemv_multi_row_tile<2, GATED>(s, a, dtype, shape.waves);
-  return gemv_multi_row_tile<3, GATED>(s, a, dtype, shape.waves);
+    return gemv_multi_row_tile<2, GATED>(s, a, dtype, shape.waves, shape.tiles);
+  return gemv_multi_row_tile<3, GATED>(s, a, dtype, shape.waves, shape.tiles);
 }
 
 }  // namespace
@@ -3169,7 +3173,7 @@ hipError_t launch_stage_x(hipStream_t s, const void* x, int dtype, _Float16* xo,
                 : stage_launch<_Float16, false>(s, static_cast<const _Float16*>(x), xo, xs, rowscale, m, k, mode, nrm);
 }
 
-GemvShape gemv_shape(int rows, int n, int nb, bool gated) {
+GemvShape gemv_shape(int rows, int n, int nb, bool gated, int cus) {
   GemvShape sh;
   sh.row_tiles = rows <= 16 ? 1 : rows <= 32 ? 2 : 3;
   // One 16-column tile per workgroup (two for very wide outputs, one row tile,
@@ -3178,6 +3182,15 @@ GemvShape gemv_shape(int rows, int n, int nb, bool gated) {
   const int ctiles = n / 16;
   static const int env_tiles = env_int("Q4K_GEMV_TILES", 0), env_waves = env_int("Q4K_GEMV_WAVES", 0);
   sh.tiles = (sh.row_tiles == 1 && !gated && n % 32 == 0 && ctiles >= 4096) ? 2 : 1;
+  // More than one row tile: each workgroup reads all of the staged x (its
+  // launches fit about 4 us + 14 us per MB of x a CU reads).  Between one
+  // and two workgroups per CU, two column tiles per workgroup (4 waves) take
+  // one round with half the x reads per tile: at M = 40, N = 6144 (the QKV
+  // projection, 384 tiles) 11.7 us against 14.6.  Narrower outputs lose CUs
+  // that way (N = 4096: 12.5 against 9.4 us), and gate/up pairs, three
+  // workgroups per CU, measured 34.3 against 26.7 us (three tiles: 27.9).
+  if (sh.row_tiles > 1 && !gated && ctiles % 2 == 0 && ctiles > cus && ctiles <= 2 * cus)
+    sh.tiles = 2;
   if (env_tiles == 1 || (env_tiles == 2 && sh.row_tiles == 1 && !gated && n % 32 == 0))
     sh.tiles = env_tiles;
   const int groups = ctiles / sh.tiles;
