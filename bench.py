@@ -804,7 +804,7 @@ def main():
             "unit": "TFLOP/s",
             "ms_per_step": round(pre["ms_per_step"], 4),
             "roofline": {
-                "kernel": "q4k_gemm2_kernel<float,true> (gated gate/up GEMM, M=2048, K=4096, N=12288 x2: 412.32 GFLOP per launch)",
+                "kernel": "q4k_gemm2_kernel<float,true,false> (gated gate/up GEMM, M=2048, K=4096, N=12288 x2: 412.32 GFLOP per launch)",
                 "bound": "mfma",
                 "achieved": round(pre["gated_gemm_tflops"], 1),
                 "peak": FP16_DENSE_PEAK_TFLOPS,
@@ -813,7 +813,7 @@ def main():
                 "traffic": profiled_traffic("gemm2_config4_traffic.txt"),
                 "avg_us": round(pre["gated_gemm_avg_us"], 2),
             },
-            "down_gemm": {"kernel": "q4k_gemm2_kernel<float,false> (K=12288 -> N=4096, 206.16 GFLOP)",
+            "down_gemm": {"kernel": "q4k_gemm2_kernel<float,false,false> (K=12288 -> N=4096, 206.16 GFLOP)",
                           "avg_us": round(pre["down_gemm_avg_us"], 2), "tflops": round(pre["down_gemm_tflops"], 1),
                           "frac": round(pre["down_gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4)},
         }
