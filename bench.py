@@ -603,6 +603,25 @@ def profiled_traffic(name):
     return None
 
 
+GATE_UP_BYTES = 57147392  # the fused gate/up GEMV's algorithmic bytes at config 1
+
+
+def read_ceiling(dev, gate_up_us=None):
+    """What a plain streaming read of the fused gate/up's byte count reaches on
+    this box: 10 rotating buffers of GATE_UP_BYTES (571 MB, past the 256 MB
+    memory-side cache), read with the GEMVs' non-temporal 16-byte loads."""
+    import torch
+    import mtlqwen_amd as q4k
+    bufs = [torch.empty(GATE_UP_BYTES, dtype=torch.uint8, device=dev) for _ in range(10)]
+    gbs = q4k.read_ceiling(bufs, reps=100)
+    del bufs
+    out = {"bytes_per_launch": GATE_UP_BYTES, "buffers": 10, "gbs": round(gbs, 1), "frac_of_8tbs": round(gbs / 8000.0, 4),
+           "us_per_launch": round(GATE_UP_BYTES / gbs / 1e3, 2)}
+    if gate_up_us:
+        out["gate_up_gemv_frac_of_this"] = round((GATE_UP_BYTES / gate_up_us / 1e3) / gbs, 4)
+    return out
+
+
 def copy_ceiling(dev):
     import torch
     n = 1 << 28  # 1 GiB of fp32
@@ -743,6 +762,7 @@ def main():
     types_pre = None if args.no_types or args.no_prefill or not want("types_prefill") else types_prefill_bench(dev)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
+    read_ceil = read_ceiling(dev, dec["gated"]["avg_us"] if "avg_us" in dec.get("gated", {}) else None)
     cpu = None if args.no_cpu else cpu_baseline(args)
 
     g = dec["gated"]
@@ -794,6 +814,7 @@ def main():
         "types_lm_head": types,
         "types_prefill": types_pre,
         "copy_ceiling_gbs": round(copy_gbs, 1),
+        "hbm_read_ceiling": read_ceil,
         "mfma_ceiling_tflops": round(mfma_tf, 1),
         "cpu_baseline": cpu,
     }

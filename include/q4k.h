@@ -288,6 +288,16 @@ int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, dou
  * allocates and frees a small device buffer. */
 int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops);
 
+/* Measured streaming-read rate of the device (no counterpart in the
+ * reference; bench.py records it beside the published HBM peak).  Reads the
+ * `count` device buffers of `bytes` each (16-byte aligned, `bytes` a multiple
+ * of 16) in turn, `reps` launches in all after one warm-up pass, with the
+ * non-temporal 16-byte loads the GEMVs stream their weights with, and returns
+ * the average rate in GB/s (launch gaps included).  Rotating buffers larger
+ * than the memory-side cache together keep the reads on HBM.  Synchronises
+ * the stream; allocates and frees a small device buffer. */
+int q4k_read_ceiling(void* stream, int device, const void* const* buffers, uint32_t count, uint64_t bytes, uint32_t reps, double* gbs);
+
 /* The device layout as a host transform (for tests and tooling):
  * GGUF-order block_q4_K bytes <-> the kernels' tiled order.  Both buffers are
  * n * (k / 256) * 144 bytes. */

@@ -12,7 +12,7 @@ from ._lib import DTYPE_F16, DTYPE_F32, GGML_TYPE_IQ4_XS, GGML_TYPE_Q4_K, GGML_T
     PHASE_PREFILL_SMALL, POST_ADD, POST_GATE, POST_STORE, KERNEL_STAGE, KERNEL_GEMV, KERNEL_GEMV_GATED, KERNEL_GEMM, \
     KERNEL_AUX, ECAPTURE, ENOMEM, Q4KError, lib
 from .gguf import GGUFFile, TensorInfo
-from .linear import (PHASE_NAMES, Weight, embedding, embedding_batch, gather_rows, linear, linear_norm, mfma_ceiling, mlp, mlp_gate_up, pack_queries,
+from .linear import (PHASE_NAMES, Weight, embedding, embedding_batch, gather_rows, linear, linear_norm, mfma_ceiling, read_ceiling, mlp, mlp_gate_up, pack_queries,
                      profile_enable, profile_query, q4k_nbytes, relayout_host, rms_norm, rms_norm_gather, select_phase,
                      unrelayout_host)
 
@@ -22,6 +22,6 @@ __all__ = [
     "GGML_TYPE_Q6_K", "GGML_TYPE_Q8_0", "GGML_TYPE_Q5_K", "GGML_TYPE_IQ4_XS",
     "POST_STORE", "POST_ADD", "POST_GATE", "PHASE_DECODE", "PHASE_PREFILL", "PHASE_PREFILL_SMALL",
     "PHASE_GATED_DECODE", "KERNEL_STAGE", "KERNEL_GEMV", "KERNEL_GEMV_GATED", "KERNEL_GEMM", "profile_enable",
-    "profile_query", "mfma_ceiling", "embedding", "embedding_batch", "rms_norm", "rms_norm_gather", "KERNEL_AUX", "GGUFFile", "TensorInfo",
+    "profile_query", "mfma_ceiling", "read_ceiling", "embedding", "embedding_batch", "rms_norm", "rms_norm_gather", "KERNEL_AUX", "GGUFFile", "TensorInfo",
     "ECAPTURE", "ENOMEM"
 ]

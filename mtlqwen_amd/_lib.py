@@ -77,6 +77,7 @@ def _load():
         "q4k_profile_query": (c_int, [u32, pu32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_double)]),
         "q4k_mfma_ceiling": (c_int, [p, c_int, u32, ctypes.POINTER(ctypes.c_double)]),
+        "q4k_read_ceiling": (c_int, [p, c_int, ctypes.POINTER(p), u32, ctypes.c_uint64, u32, ctypes.POINTER(ctypes.c_double)]),
         "q4k_relayout_host": (c_int, [p, p, u32, u32]),
         "q4k_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(p)]),
         "q4k_gguf_close": (c_int, [p]),

@@ -1294,6 +1294,47 @@ int q4k_mfma_ceiling(void* stream, int device, uint32_t iters, double* tflops) {
   return Q4K_OK;
 }
 
+int q4k_read_ceiling(void* stream, int device, const void* const* buffers, uint32_t count, uint64_t bytes, uint32_t reps, double* gbs) {
+  if (!gbs || !buffers || count == 0 || reps == 0 || bytes == 0 || bytes % 16 != 0)
+    return fail(Q4K_EINVAL, "gbs and buffers must be non-NULL; count, reps and bytes (a multiple of 16) positive");
+  for (uint32_t i = 0; i < count; ++i)
+    if (!buffers[i] || reinterpret_cast<uintptr_t>(buffers[i]) % 16 != 0)
+      return fail(Q4K_EINVAL, "buffer %u is NULL or not 16-byte aligned", i);
+  int rc = set_device(device);
+  if (rc)
+    return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int blocks = 8 * device_cus(device);
+  uint32_t* out = nullptr;
+  Q4K_TRY_HIP(hipMalloc(&out, (size_t)blocks * sizeof(uint32_t)), "hipMalloc");
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t err = hipEventCreate(&e0);
+  if (err == hipSuccess)
+    err = hipEventCreate(&e1);
+  for (uint32_t i = 0; i < count && err == hipSuccess; ++i)  // warm-up: one pass over every buffer
+    err = launch_stream_read(s, buffers[i], bytes, out, blocks);
+  if (err == hipSuccess)
+    err = hipEventRecord(e0, s);
+  for (uint32_t r = 0; r < reps && err == hipSuccess; ++r)
+    err = launch_stream_read(s, buffers[r % count], bytes, out, blocks);
+  if (err == hipSuccess)
+    err = hipEventRecord(e1, s);
+  if (err == hipSuccess)
+    err = hipEventSynchronize(e1);
+  float ms = 0.0f;
+  if (err == hipSuccess)
+    err = hipEventElapsedTime(&ms, e0, e1);
+  if (e0)
+    (void)hipEventDestroy(e0);
+  if (e1)
+    (void)hipEventDestroy(e1);
+  (void)hipFree(out);
+  if (err != hipSuccess)
+    return fail(Q4K_EHIP, "read ceiling: %s", hipGetErrorString(err));
+  *gbs = ms > 0.0f ? (double)bytes * reps / (ms * 1e-3) / 1e9 : 0.0;
+  return Q4K_OK;
+}
+
 int q4k_profile_query(uint32_t kernel, uint32_t* launches, double* total_ms, double* min_ms, double* max_ms) {
   if (kernel > Q4K_KERNEL_AUX)
     return fail(Q4K_EINVAL, "kernel family %u out of range", kernel);

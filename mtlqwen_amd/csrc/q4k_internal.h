@@ -438,6 +438,9 @@ hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int c
 // One MFMA-ceiling launch: `blocks` workgroups of 4 waves, each wave issuing
 // 32 * iters v_mfma_f32_16x16x32_f16 (16384 FLOP each); out holds blocks * 256 floats.
 hipError_t launch_mfma_ceiling(hipStream_t s, float* out, int blocks, int iters);
+// Streaming read of `bytes` (a multiple of 16) at p; `out` takes `blocks`
+// words (almost never written).
+hipError_t launch_stream_read(hipStream_t s, const void* p, size_t bytes, uint32_t* out, int blocks);
 
 hipError_t launch_gather(hipStream_t s, const void* x, void* out, int k, int dtype, const GatherIndex& idx);
 

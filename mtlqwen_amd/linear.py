@@ -337,6 +337,25 @@ def mfma_ceiling(device=0, iters=20000, stream=None):
     return t.value
 
 
+def read_ceiling(buffers, reps=50, stream=None):
+    """Measured streaming-read rate in GB/s over equal-sized device byte
+    buffers read in turn (non-temporal 16-byte loads); synchronises the
+    stream."""
+    bufs = list(buffers)
+    if not bufs:
+        raise ValueError("read_ceiling needs at least one buffer")
+    nbytes = bufs[0].numel() * bufs[0].element_size()
+    for b in bufs:
+        _ptr(b)  # a contiguous GPU tensor
+        if b.numel() * b.element_size() != nbytes:
+            raise ValueError("read_ceiling buffers must have equal sizes")
+    dev = bufs[0].device.index
+    arr = (ctypes.c_void_p * len(bufs))(*[b.data_ptr() for b in bufs])
+    g = ctypes.c_double()
+    check(lib.q4k_read_ceiling(_stream(stream, dev), dev, arr, len(bufs), nbytes, int(reps), ctypes.byref(g)))
+    return g.value
+
+
 def relayout_host(gguf, n, k, ggml_type=GGML_TYPE_Q4_K):
     """GGUF-order bytes of type Q4_K or Q6_K -> the kernels' tiled order."""
     src = np.ascontiguousarray(gguf, dtype=np.uint8).reshape(-1)
@@ -356,5 +375,5 @@ def unrelayout_host(tiled, n, k, ggml_type=GGML_TYPE_Q4_K):
 
 __all__ = ["Weight", "linear", "linear_norm", "mlp_gate_up", "mlp", "select_phase", "pack_queries", "gather_rows", "embedding", "rms_norm",
            "rms_norm_gather", "relayout_host",
-           "profile_enable", "profile_query", "mfma_ceiling",
+           "profile_enable", "profile_query", "mfma_ceiling", "read_ceiling",
            "unrelayout_host", "q4k_nbytes", "Q4KError", "PHASE_NAMES"]

@@ -273,3 +273,13 @@ def test_mfma_ceiling(q4k, gpu):
     """The measured MFMA ceiling is positive and below the published dense peak."""
     tf = q4k.mfma_ceiling(0, iters=2000)
     assert 100.0 < tf < 2600.0
+
+
+def test_read_ceiling(q4k, gpu):
+    """The measured streaming-read rate is positive and below the published
+    8 TB/s; buffers of unequal size are refused before any launch."""
+    bufs = [torch.empty(4 << 20, dtype=torch.uint8, device=gpu) for _ in range(2)]
+    gbs = q4k.read_ceiling(bufs, reps=8)
+    assert 1.0 < gbs < 8000.0
+    with pytest.raises(ValueError):
+        q4k.read_ceiling([bufs[0], torch.empty(1 << 20, dtype=torch.uint8, device=gpu)])
