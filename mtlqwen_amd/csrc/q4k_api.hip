@@ -1304,7 +1304,9 @@ int q4k_read_ceiling(void* stream, int device, const void* const* buffers, uint3
   if (rc)
     return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int blocks = 8 * device_cus(device);
+  // 32 workgroups per CU: the fastest grid measured (57 MB reads: 5.93 TB/s,
+  // against 5.46 with 16, 5.34 with 8 and 5.26 with 4).
+  const int blocks = 32 * device_cus(device);
   uint32_t* out = nullptr;
   Q4K_TRY_HIP(hipMalloc(&out, (size_t)blocks * sizeof(uint32_t)), "hipMalloc");
   hipEvent_t e0 = nullptr, e1 = nullptr;

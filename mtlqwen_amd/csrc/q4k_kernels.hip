@@ -1746,8 +1746,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 // ----------------------------------------------------------------------------
 // Measured streaming-read ceiling: a plain read of n16 16-byte words with
-// non-temporal loads (as the GEMVs stream their weights), four in flight per
-// lane, over 8 workgroups per CU.  The xor of each lane's words is stored only
+// non-temporal loads (as the GEMVs stream their weights), up to four in
+// flight per lane, over the grid the caller gives.  The xor of each lane's words is stored only
 // if it hits a fixed value, which keeps the loads alive without a store
 // stream of its own.
 // ----------------------------------------------------------------------------
