@@ -345,11 +345,15 @@ def read_ceiling(buffers, reps=50, stream=None):
     if not bufs:
         raise ValueError("read_ceiling needs at least one buffer")
     nbytes = bufs[0].numel() * bufs[0].element_size()
+    dev = bufs[0].device.index
     for b in bufs:
         _ptr(b)  # a contiguous GPU tensor
         if b.numel() * b.element_size() != nbytes:
             raise ValueError("read_ceiling buffers must have equal sizes")
-    dev = bufs[0].device.index
+        if b.device.index != dev:
+            raise ValueError("read_ceiling buffers must be on one GPU")
+    if nbytes % 16 != 0:
+        raise ValueError("read_ceiling buffer sizes must be a multiple of 16 bytes")
     arr = (ctypes.c_void_p * len(bufs))(*[b.data_ptr() for b in bufs])
     g = ctypes.c_double()
     check(lib.q4k_read_ceiling(_stream(stream, dev), dev, arr, len(bufs), nbytes, int(reps), ctypes.byref(g)))
