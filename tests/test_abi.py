@@ -138,3 +138,17 @@ def test_neighbour_entry_points_validate_before_hip(q4k):
     assert lib.q4k_rms_norm_gather(None, fake, fake, ctypes.c_void_p(0x100000), 16, counts, samples, 2,
                                    ctypes.c_float(1e-6), 0, None) == -1
     assert "exceed" in lib.q4k_last_error().decode()
+
+
+def test_ceiling_entry_points_validate_before_hip(q4k):
+    """The measurement entry points refuse bad arguments before any HIP call."""
+    lib = q4k.lib
+    out = ctypes.c_double()
+    assert lib.q4k_mfma_ceiling(None, 0, 0, ctypes.byref(out)) == -1
+    assert lib.q4k_mfma_ceiling(None, 0, 10, None) == -1
+    bufs = (ctypes.c_void_p * 2)(0x1000, 0x2008)  # the second is not 16-byte aligned
+    assert lib.q4k_read_ceiling(None, 0, None, 1, 4096, 1, ctypes.byref(out)) == -1
+    assert lib.q4k_read_ceiling(None, 0, bufs, 1, 4100, 1, ctypes.byref(out)) == -1  # not a multiple of 16
+    assert lib.q4k_read_ceiling(None, 0, bufs, 1, 4096, 0, ctypes.byref(out)) == -1
+    assert lib.q4k_read_ceiling(None, 0, bufs, 2, 4096, 1, ctypes.byref(out)) == -1
+    assert "aligned" in lib.q4k_last_error().decode()
