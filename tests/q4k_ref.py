@@ -220,6 +220,39 @@ def silu64(g):
     return g / (1.0 + np.exp(-g))
 
 
+def _to_f16(v):
+    return np.asarray(v, np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+def prefill_arithmetic(x, w, n, k):
+    """The reference's prefill arithmetic for Q4_K, in float64: activations
+    rounded once to fp16 (the engine's activation type; an fp32 row is first
+    scaled by a power of two, which is exact, so that its largest magnitude
+    lies in [2^14, 2^15)), weights at the prefill tile value
+    h(fp32(d*sc*q - dmin*m)) (quant_linear.metal:43,45), products summed
+    exactly.  Returns the [m, n] contraction."""
+    x = np.asarray(x)
+    if x.dtype == np.float16:
+        a = x.astype(np.float64)
+    else:
+        x64 = x.astype(np.float64)
+        mx = np.abs(x64).max(axis=1)
+        ex = np.frexp(np.where(mx > 0, mx, 1.0))[1]
+        s = np.ldexp(1.0, 15 - ex)
+        a = _to_f16(x64 * s[:, None]) / s[:, None]
+    return a @ _to_f16(dequant_numpy(w, n, k)).T
+
+
+def gated_prefill_arithmetic(x, wg, wu, n, k, f16_out=False):
+    """SiLU(gate) * up over prefill_arithmetic's projections, with the fp16
+    rounding points of the reference's post-2 epilogue for fp16 outputs
+    (h(silu(h(g)) * h(u)), quant_linear.metal:146-147)."""
+    g, u = prefill_arithmetic(x, wg, n, k), prefill_arithmetic(x, wu, n, k)
+    if f16_out:
+        return _to_f16(silu64(_to_f16(g)) * _to_f16(u))
+    return silu64(g) * u
+
+
 # --------------------------------------------------------------------------
 # Oracle binding.
 # --------------------------------------------------------------------------

@@ -1,11 +1,9 @@
 """The five benchmark configurations at their full shapes, HIP path vs oracle.
 
-Config 4 (M=2048) is checked against the oracle on a row subset that holds
-one row of every 16-row MFMA tile (cycling through the 16 positions), the
-first and last row of every 128-row GEMM tile and rows 2040..2047 (the GPU
-computes all rows; the oracle recomputes the subset), and on every row through
-size-independent properties: all outputs finite, and stage-wise linearity
-y(x_a + x_b) = y(x_a) + y(x_b).
+Config 4 (M=2048) is checked against the oracle on every row of the gate
+buffer and of the down projection's output (the oracle recomputes all 2048
+rows, a few seconds on 16 host threads), and through size-independent
+properties: all outputs finite, and linearity y(x_a + x_b) = y(x_a) + y(x_b).
 """
 import numpy as np
 import pytest
@@ -120,13 +118,11 @@ def test_config4_long_prefill(q4k, oracle, gpu):
     out = torch.empty((m, 4096), device=gpu)
     q4k.linear(gate, D, m, out, query_counts=[m])
     torch.cuda.synchronize()
-    tiles = np.arange(m // 16)
-    rows = np.unique(np.concatenate([16 * tiles + tiles % 16, np.arange(0, m, 128), np.arange(127, m, 128), np.arange(m - 8, m)]))
     g_gpu = gate.cpu().numpy()
     assert np.all(np.isfinite(g_gpu)) and np.all(np.isfinite(out.cpu().numpy()))
-    err_g = row_rel_err(g_gpu[rows], oracle.mlp_gate_up(x[rows], wg, wu, 12288, 4096))
-    err_d = row_rel_err(out.cpu().numpy()[rows], oracle.linear(g_gpu[rows], wd, 4096, 12288))
-    print(f"config4: gated {err_g:.3e} down {err_d:.3e} over {len(rows)} rows")
+    err_g = row_rel_err(g_gpu, oracle.mlp_gate_up(x, wg, wu, 12288, 4096))
+    err_d = row_rel_err(out.cpu().numpy(), oracle.linear(g_gpu, wd, 4096, 12288))
+    print(f"config4: gated {err_g:.3e} down {err_d:.3e} over all {m} rows")
     assert err_g <= TOL and err_d <= TOL
     # Linearity over every row of the full-size gate projection.
     xa = acts(44, m, 4096)

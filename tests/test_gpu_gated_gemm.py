@@ -2,27 +2,21 @@
 single launch (q4k_mlp_gate_up / q4k_mlp at prefill row counts), against the
 reference's two-call form (forward.cpp:116-118: gate stored with post 0, then
 up with post 2 over it in place) run through linear(): the same buffer bit for
-bit, one GEMM launch instead of two, and the oracle on the first and last row
-of every 128-row block.  Cases: ragged row blocks and column blocks (a
+bit, one GEMM launch instead of two, and the oracle on every row.  Cases: ragged row blocks and column blocks (a
 workgroup with one live output tile), one block of K, fp16 activations, the
 config-4 shape, long K with few tiles (two K-halves per tile, summed by the
 second half to finish), and the ffn_norm folded into the shared staging.
-Bar for the oracle: max row-relative error 1e-3."""
+Bar for the oracle: max row-relative error 1e-3, or, in rows where SiLU(gate)
+* up is ill-conditioned, no further from the oracle than the reference's own
+prefill arithmetic (see test_gated_gemm_matches_two_calls)."""
 import numpy as np
 import pytest
 import torch
 
-from q4k_ref import make_q4k, make_x, row_rel_err
+from q4k_ref import gated_prefill_arithmetic, make_q4k, make_x, row_rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-
-
-def _edge_rows(m):
-    rows = set()
-    for r0 in range(0, m, 128):
-        rows.update((r0, min(r0 + 127, m - 1)))
-    return np.array(sorted(rows))
 
 
 def _gemm_launches(q4k, fn):
@@ -59,9 +53,24 @@ def test_gated_gemm_matches_two_calls(q4k, oracle, gpu, m, n, k, dtype):
     assert torch.isfinite(y2).all()
     diff = (y1 != y2).nonzero()
     assert diff.numel() == 0, f"{diff.shape[0]} outputs differ from the two-call form, first {diff[:4].tolist()}"
-    rows = _edge_rows(m)
-    ref = oracle.mlp_gate_up(x[rows], wg, wu, n, k)
-    assert row_rel_err(y2.float().cpu().numpy()[rows], ref.astype(np.float32)) <= TOL
+    # Every row against the oracle.  SiLU(gate) * up is ill-conditioned in
+    # rows whose gate values lie mostly far below zero: the few outputs that
+    # survive are small differences of large terms, so fp16 rounding of the
+    # activations and of the tile weights -- the reference's own prefill
+    # arithmetic -- can exceed the 1e-3 bar there (the benchmark
+    # configurations stay within it on every row).  The GEMM must then
+    # (1) compute that arithmetic: within 2e-4 of its float64 model (fp32
+    # outputs; 1e-3 for fp16 outputs, where one-ulp differences of a
+    # surviving output show), and (2) be within the bar or no further from
+    # the oracle than the reference's arithmetic is.
+    y = y2.float().cpu().numpy()
+    ref = oracle.mlp_gate_up(x, wg, wu, n, k)
+    model = gated_prefill_arithmetic(x, wg, wu, n, k, f16_out=dtype == torch.float16)
+    err, err_model, err_vs_model = row_rel_err(y, ref), row_rel_err(model, ref), row_rel_err(y, model)
+    print(f"gated ({m}, {n}, {k}, {dtype}): max row error {err:.3e} over all {m} rows; "
+          f"reference arithmetic {err_model:.3e}; GPU vs that arithmetic {err_vs_model:.3e}")
+    assert err_vs_model <= (1e-3 if dtype == torch.float16 else 2e-4)
+    assert err <= max(TOL, 1.05 * err_model)
 
 
 def test_gated_gemm_with_ffn_norm(q4k, gpu):
