@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=200,
                     help="untimed decode MLP steps before the timed ones (replayed from a graph like them)")
     ap.add_argument("--sets", type=int, default=10, help="rotating weight copies (85 MB each)")
+    ap.add_argument("--decode-warmup-ms", type=float, default=300.0,
+                    help="untimed decode graph replays (by wall time) after the W warmup steps: a fresh process "
+                         "runs its first couple of hundred decode steps about 10 %% slower")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--prefill-warmup-ms", type=float, default=300.0,
                     help="untimed prefill graph replays before the timed ones (the GEMMs run about 15 %% slower for the "
@@ -58,7 +61,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-types", action="store_true", help="skip the Q8_0 / Q5_K / IQ4_XS LM-head and the typed prefill GEMM timings")
     ap.add_argument("--part", default="all",
-                    choices=["all", "decode", "prefill", "config2", "config3", "lm_head", "types", "types_prefill", "shard", "neighbours"],
+                    choices=["all", "decode", "prefill", "config0", "config2", "config3", "lm_head", "types", "types_prefill", "shard",
+                             "neighbours"],
                     help="run one workload alone (for profiling runs that attribute kernel statistics to one configuration)")
     return ap.parse_args()
 
@@ -105,6 +109,9 @@ def decode_bench(args, dev):
     for i in range(len(sets)):
         step(i)
     torch.cuda.synchronize()
+    # Then, whatever W is, replays of a 50-step graph until decode_warmup_ms
+    # of wall time have passed, so a short --warmup does not time the slow
+    # first steps of a fresh process.
     if args.warmup > 0:
         warm = torch.cuda.CUDAGraph()
         with torch.cuda.graph(warm):
@@ -112,6 +119,17 @@ def decode_bench(args, dev):
                 step(i % len(sets))
         warm.replay()
         torch.cuda.synchronize()
+        del warm
+    if args.decode_warmup_ms > 0:
+        warm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(warm):
+            for i in range(50):
+                step(i % len(sets))
+        t_end = time.perf_counter() + args.decode_warmup_ms * 1e-3
+        while True:
+            timed_graph(warm, 1)
+            if time.perf_counter() >= t_end:
+                break
         del warm
 
     # Timed region: exactly K steps, replayed from one HIP graph that cycles
@@ -154,6 +172,32 @@ def decode_bench(args, dev):
     act = 4 * (M * K + M * N)  # gate/up: x in, gate buffer out
     act += 4 * (M * N + 2 * M * K)  # down: gate buffer in, residual in + out
     step_bytes = wbytes + act
+
+    # The same step with fp16 activations (the engine's own activation type,
+    # quant_linear.metal:119-120): x, hidden and the gate buffer in fp16.
+    x16, hidden16, gate16 = (x * 0.2).half(), hidden.half(), gate.half()
+
+    def step16(s):
+        G, U, D = sets[s]
+        q4k.mlp(x16, G, U, D, hidden16, gate16, M, query_counts=counts)
+
+    for i in range(len(sets)):
+        step16(i)
+    g16 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g16):
+        for i in range(args.steps):
+            step16(i % len(sets))
+    timed_graph(g16, 3)
+    ms16 = timed_graph(g16, 1) / args.steps * 1e3
+    q4k.profile_enable(True)
+    for i in range(args.steps):
+        step16(i % len(sets))
+    torch.cuda.synchronize()
+    gated16_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMV_GATED)
+    down16_ms, _ = kernel_avg_ms(q4k, q4k.KERNEL_GEMV)
+    q4k.profile_enable(False)
+    step16_bytes = wbytes + act // 2
+    del g16
     gated_bytes = 2 * q4k_bytes(N, K) + 4 * (M * K + M * N)
     down_bytes = q4k_bytes(K, N) + 4 * (M * N + 2 * M * K)
     return {
@@ -168,7 +212,51 @@ def decode_bench(args, dev):
         "gated_norm_us": gated_norm_ms * 1e3,
         "norm_launches": aux_n,
         "weight_sets_mb": len(sets) * wbytes / 1e6,
+        "f16": {"ms_per_step": ms16, "gbs": step16_bytes / (ms16 * 1e-3) / 1e9, "step_bytes": step16_bytes,
+                "gate_up_us": gated16_ms * 1e3, "down_us": down16_ms * 1e3,
+                "gate_up_gbs": (2 * q4k_bytes(N, K) + 2 * (M * K + M * N)) / (gated16_ms * 1e-3) / 1e9},
     }
+
+
+def config0_bench(dev, sets=32, reps=64):
+    """Config 0 on the GPU: one Q4_K linear, M = 1 token, K = N = 4096 (the
+    decode GEMV), fp32 activations, weights rotating over 32 copies (302 MB,
+    past the 256 MB memory-side cache), launches replayed from a HIP graph;
+    plus per-launch times from dispatch-attached events.  The reference
+    publishes one kernel time for this shape, on another GPU (an M2 Pro:
+    62.08 us, agents/KERNELS.md:54); it is context, not a same-node
+    comparison."""
+    import numpy as np
+    import torch
+    import mtlqwen_amd as q4k
+
+    K = N = 4096
+    rng = np.random.default_rng(0x51A70000)
+    raw = torch.from_numpy(make_q4k(rng, N, K)).to(dev)
+    ws = [q4k.Weight(raw, N, K) for _ in range(sets)]
+    del raw
+    x = torch.randn(1, K, device=dev, generator=torch.Generator(device=dev).manual_seed(0x51A71000))
+    y = torch.empty(1, N, device=dev)
+    for w in ws:
+        q4k.linear(x, w, 1, y, query_counts=[1])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(reps):
+            q4k.linear(x, ws[i % sets], 1, y, query_counts=[1])
+    timed_graph(graph, 20)
+    us = timed_graph(graph, 20) / (20 * reps) * 1e6
+    q4k.profile_enable(True)
+    for i in range(reps):
+        q4k.linear(x, ws[i % sets], 1, y, query_counts=[1])
+    torch.cuda.synchronize()
+    ev_ms, launches = kernel_avg_ms(q4k, q4k.KERNEL_GEMV)
+    _, stage_n = kernel_avg_ms(q4k, q4k.KERNEL_STAGE)
+    q4k.profile_enable(False)
+    nbytes = q4k_bytes(N, K) + 4 * (K + N)
+    return {"workload": "config0: single Q4_K linear M=1, K=N=4096, fp32 x/y (decode GEMV)", "kernel": ws[0].kernel_name(0),
+            "us_per_linear": round(us, 3), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
+            "gemv_avg_us": round(ev_ms * 1e3, 3), "launches_per_linear": round((launches + stage_n) / reps, 2),
+            "reference_published_us_m2pro": 62.08}
 
 
 def shard_bench(args, dev):
@@ -577,6 +665,24 @@ def prefill_bench(args, dev):
     gu_ms, gu_n = timed_gemm(lambda: q4k.mlp_gate_up(x, G, U, M, gate, query_counts=counts))
     dn_ms, dn_n = timed_gemm(lambda: q4k.linear(gate, D, M, out, query_counts=counts))
     flop_gemm = 2.0 * M * N * K
+
+    # The same step with fp16 activations (the engine's activation type).
+    x16, gate16, out16 = (x * 0.05).half(), gate.half(), out.half()
+
+    def step16():
+        q4k.mlp_gate_up(x16, G, U, M, gate16, query_counts=counts)
+        q4k.linear(gate16, D, M, out16, query_counts=counts)
+
+    step16()
+    g16 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g16):
+        for _ in range(per_graph):
+            step16()
+    timed_graph(g16, 10)
+    ms16 = timed_graph(g16, args.prefill_steps) / (args.prefill_steps * per_graph) * 1e3
+    gu16_ms, _ = timed_gemm(lambda: q4k.mlp_gate_up(x16, G, U, M, gate16, query_counts=counts))
+    dn16_ms, _ = timed_gemm(lambda: q4k.linear(gate16, D, M, out16, query_counts=counts))
+    del g16
     return {
         "ms_per_step": ms,
         "tflops": 3 * flop_gemm / (ms * 1e-3) / 1e12,
@@ -585,6 +691,9 @@ def prefill_bench(args, dev):
         "gated_gemm_tflops": 2 * flop_gemm / (gu_ms * 1e-3) / 1e12,
         "down_gemm_avg_us": dn_ms * 1e3,
         "down_gemm_tflops": flop_gemm / (dn_ms * 1e-3) / 1e12,
+        "f16": {"ms_per_step": round(ms16, 4), "tflops": round(3 * flop_gemm / (ms16 * 1e-3) / 1e12, 1),
+                "gated_gemm_avg_us": round(gu16_ms * 1e3, 2), "gated_gemm_tflops": round(2 * flop_gemm / (gu16_ms * 1e-3) / 1e12, 1),
+                "down_gemm_avg_us": round(dn16_ms * 1e3, 2), "down_gemm_tflops": round(flop_gemm / (dn16_ms * 1e-3) / 1e12, 1)},
     }
 
 
@@ -734,6 +843,8 @@ def main():
         res = {"part": args.part}
         if args.part == "prefill":
             res["prefill"] = prefill_bench(args, dev)
+        elif args.part == "config0":
+            res["config0"] = config0_bench(dev)
         elif args.part in ("config2", "config3"):
             res.update(configs_bench(dev, parts=(args.part,), sets=args.sets if args.part == "config2" else 1))
         elif args.part == "lm_head":
@@ -752,6 +863,7 @@ def main():
         return
 
     dec = decode_bench(args, dev)
+    cfg0 = config0_bench(dev) if want("config0") else None
     pre = None if args.no_prefill or not want("prefill") else prefill_bench(args, dev)
     shard = shard_bench(args, dev) if want("shard") else None
     neighbours = neighbours_bench(args, dev) if want("neighbours") else None
@@ -806,6 +918,12 @@ def main():
             "gate_up_gemv_with_ffn_norm_us": round(dec["gated_norm_us"], 3),
             "norm_launches_per_step": dec["norm_launches"] / dec["steps"],
         },
+        # config 1 with fp16 activations (x, hidden, gate buffer): the engine's own activation type
+        "f16_activations": {"ms_per_step": round(dec["f16"]["ms_per_step"], 5), "gbs": round(dec["f16"]["gbs"], 1),
+                            "step_bytes": dec["f16"]["step_bytes"], "gate_up_us": round(dec["f16"]["gate_up_us"], 3),
+                            "gate_up_gbs": round(dec["f16"]["gate_up_gbs"], 1), "down_us": round(dec["f16"]["down_us"], 3)},
+        "decode_warmup_ms": args.decode_warmup_ms,
+        "config0": cfg0,
         "shard_1of8": shard,
         "neighbours": neighbours,
         "configs_2_3": cfgs,
@@ -837,6 +955,8 @@ def main():
             "down_gemm": {"kernel": "q4k_gemm2_kernel<float,false,false> (K=12288 -> N=4096, 206.16 GFLOP)",
                           "avg_us": round(pre["down_gemm_avg_us"], 2), "tflops": round(pre["down_gemm_tflops"], 1),
                           "frac": round(pre["down_gemm_tflops"] / FP16_DENSE_PEAK_TFLOPS, 4)},
+            # the same step with fp16 activations (x scaled by 0.05 to stay in fp16 range)
+            "f16_activations": pre["f16"],
         }
     print(json.dumps(line), flush=True)
 

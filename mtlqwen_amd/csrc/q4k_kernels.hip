@@ -580,8 +580,9 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 // workgroups of one L2 read different parts of x first) of the workgroup's T
 // column tiles of both matrices: U = 4T tile-blocks ("units").  It loads its
 // two blocks of x (one coalesced 1 KB load per (block, row)), then keeps two
-// units in flight ahead of the one it computes (per unit one header dword and
-// the two quant slabs, 16 B per lane).  No staging launch precedes it: while
+// units in flight ahead of the pair it computes (per unit the 16-byte header
+// row of the lane's column and the two quant slabs, 16 B per lane).  No
+// staging launch precedes it: while
 // the first units are in flight the wave turns its blocks of x into the MFMA
 // operands in registers, with the same arithmetic as the decode pack
 // (pack_block_row):
@@ -595,11 +596,12 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 //    8..15 carrying the low parts;
 //  - each lane's 32 elements are one sub-block; their sums / 32 (hi / lo)
 //    are gathered into the min-term operand of v_mfma_f32_16x16x16_f16.
-// Per unit the header's 16 bytes of this lane's column come from the four
-// lanes that loaded them (ds_bpermute).  The partial sums of a unit are
-// unscaled and accumulated in registers; hi and lo rows are combined (lanes
-// l, l + 32) and the eight waves' sums are added in wave order through LDS
-// before the SiLU(gate) * up epilogue.
+// Units are computed two at a time, their instruction streams interleaved.
+// The partial sums of a unit are unscaled and accumulated in registers; hi
+// and lo rows are combined (lanes l, l + 32) and the eight waves' sums are
+// added in wave order through LDS before the SiLU(gate) * up epilogue.  The
+// kernel is bound by its vector ALU: about 135 VALU instructions per unit
+// and 500 for the pack, two waves per SIMD.
 // ----------------------------------------------------------------------------
 constexpr int kDppRowRor8 = 0x128;  // lane i <- lane (i + 8) % 16 within 16 lanes
 
@@ -688,9 +690,13 @@ __device__ __forceinline__ void pack_x_regs(const float (&xv)[32], int lane, XBl
 
 // x of wave w, re-ordered for the register pack: [block][lane][32 + 4]
 // floats (the 4-float pad makes the 16-byte reads of 16 lanes hit 64
-// distinct banks).  The partial sums reuse the wave's own region at the end.
+// distinct banks), BPW blocks per wave.  The partial sums reuse the wave's
+// own region at the end.
 constexpr int kGuXRow = 36;
-constexpr int kGuWaveFloats = 2 * 64 * kGuXRow;
+template <int BPW>
+constexpr int gu_wave_floats() {
+  return BPW * 64 * kGuXRow;
+}
 
 // The x of one item of the fused gate/up GEMV, packed: wave w loads K-blocks
 // bw, bw + 1 of all 8 rows (one coalesced load per (block, row), lane l
@@ -702,10 +708,9 @@ constexpr int kGuWaveFloats = 2 * 64 * kGuXRow;
 // them, so each row's sum of squares is their partial sums (ssq [wave][row])
 // added after one barrier, and every element becomes
 // (x * rsqrt(sum / k + eps)) * w before the pack.
-template <typename OutT, bool NORM, typename Issue>
-__device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int bw, XBlock (&xb)[2],
+template <typename OutT, bool NORM, int W, int BPW, typename Issue>
+__device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float* xl, float (*ssq)[8], int bw, XBlock (&xb)[BPW],
                                                Issue&& issue_first) {
-  constexpr int W = 8, BPW = 2;
   constexpr int kXRow = kGuXRow;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -773,7 +778,7 @@ __device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float (*xl)[kG
   }
   // Element e = 4 lane of row r goes to pack lane 16 (e / 64) + r + 8 ((e / 32) & 1),
   // float (e & 31) of its 32.
-  float* const xw = xl[wave];
+  float* const xw = xl + (size_t)wave * gu_wave_floats<BPW>();
   const int dl = 16 * (lane >> 4) + 8 * ((lane >> 3) & 1), doff = 4 * (lane & 7);
 #pragma unroll
   for (int j = 0; j < BPW; ++j)
@@ -809,13 +814,14 @@ __device__ __forceinline__ void gate_up_pack_x(const GemvArgs& a, float (*xl)[kG
 // The end of an item: C row 4g + v of each (matrix, tile) pair, lanes g < 2
 // adding the low part held 32 lanes up, goes to the wave's LDS region; the
 // eight waves' sums are added in wave order and SiLU(gate) * up is stored.
-template <int T, typename OutT>
-__device__ __forceinline__ void gate_up_finish(const GemvArgs& a, float (*xl)[kGuWaveFloats], const f4_t (&acc)[2 * T], int item) {
-  constexpr int W = 8, MT = 2 * T;
+template <int T, typename OutT, int W, int BPW>
+__device__ __forceinline__ void gate_up_finish(const GemvArgs& a, float* xl, const f4_t (&acc)[2 * T], int item) {
+  constexpr int MT = 2 * T, WF = gu_wave_floats<BPW>();
+  static_assert(MT * 8 * 16 <= WF, "partials fit the x region");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  float* const xw = xl[wave];
+  float* const xw = xl + (size_t)wave * WF;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -832,8 +838,8 @@ __device__ __forceinline__ void gate_up_finish(const GemvArgs& a, float (*xl)[kG
     float gv = 0.0f, uv = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      gv += xl[w][(t * 8 + row) * 16 + cc];
-      uv += xl[w][((T + t) * 8 + row) * 16 + cc];
+      gv += xl[w * WF + (t * 8 + row) * 16 + cc];
+      uv += xl[w * WF + ((T + t) * 8 + row) * 16 + cc];
     }
     if (sizeof(OutT) == 2) {
       gv = round_half(gv);
@@ -845,10 +851,10 @@ __device__ __forceinline__ void gate_up_finish(const GemvArgs& a, float (*xl)[kG
 
 // One item (T column tiles of both matrices) of the fused gate/up GEMV, by the
 // 8 waves of the workgroup.
-template <int T, typename OutT, bool NORM>
-__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int item) {
-  constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT;
-  static_assert(MT * 8 * 16 <= BPW * 64 * kGuXRow, "partials fit the x region");
+template <int T, typename OutT, bool NORM, int W, int BPW>
+__device__ __forceinline__ void gate_up_item(const GemvArgs& a, float* xl, float (*ssq)[8], int item) {
+  constexpr int NM = 2, MT = NM * T, U = BPW * MT;
+  static_assert(W * BPW == 16, "the waves cover the 16 blocks of K = 4096");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
@@ -861,19 +867,25 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
   // landed).  A shallow window keeps the memory queues short, so x and each
   // wave's next unit arrive early; issuing more units ahead measured slower
   // (they queue ahead of the x of later workgroups).
+  // Units are loaded into registers two ahead of the pair being computed:
+  // the header row of the lane's own column (16 bytes; four lanes share
+  // one row), then the two quant slabs.  The scheduling barriers keep the
+  // issue order: x first, then unit by unit, the first units once x has
+  // landed.  A shallow window keeps the memory queues short, so x and each
+  // wave's next units arrive early (deeper windows measured no faster).
   constexpr int DQ = 2;
-  uint32_t hw[U];
-  u4_t q0[U], q1[U];
+  static_assert(U % 2 == 0 && MT % 2 == 0, "pairs of units within one block");
+  u4_t hdr[U], q0[U], q1[U];
   auto issue_unit = [&](int u) {
     const int j = u / MT, mt = u - j * MT, mi = mt / T, t = mt - mi * T;
     const uint8_t* src = (mi ? a.wu : a.w) + ((size_t)item * T + t) * tile_bytes + (size_t)(bw + j) * kTileBlockBytes;
-    hw[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + kHeaderOffset) + lane);
+    hdr[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kHeaderOffset) + col);
     q0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
     q1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
     __builtin_amdgcn_sched_barrier(0);
   };
   XBlock xb[BPW];
-  gate_up_pack_x<OutT, NORM>(a, xl, ssq, bw, xb, [&] {
+  gate_up_pack_x<OutT, NORM, W, BPW>(a, xl, ssq, bw, xb, [&] {
 #pragma unroll
     for (int u = 0; u < (DQ < U ? DQ : U); ++u)
       issue_unit(u);
@@ -883,40 +895,55 @@ __device__ __forceinline__ void gate_up_item(const GemvArgs& a, float (*xl)[kGuW
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
     acc[mt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // Two units per step, their instruction streams interleaved: the block
+  // constants, nibble decode, MFMA chains and accumulator updates of two
+  // independent tile-blocks of one K-block.  Units 2p + 2, 2p + 3 are
+  // loaded during step p.
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int j = u / MT, mt = u - j * MT;
+  for (int p = 0; p < U / 2; ++p) {
+    const int u0 = 2 * p, j = u0 / MT, mt0 = u0 - j * MT;
     __builtin_amdgcn_sched_barrier(0);
-    if (u + DQ < U)
-      issue_unit(u + DQ);
-    u4_t hd;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      hd[w] = (uint32_t)__shfl((int)hw[u], 4 * col + w);
-    const BlockConsts kc = block_consts(hd, g);
-    f4_t cl = f4_t{0.0f, 0.0f, 0.0f, 0.0f}, ch = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u4_t qq = s < 2 ? q0[u] : q1[u];
-      const uint32_t wa = qq[2 * (s & 1)], wb = qq[2 * (s & 1) + 1];
-      const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
-      const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
-      cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[j].frag[s], blo, cl, 0, 0, 0);
-      ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[j].frag[4 + s], bhi, ch, 0, 0, 0);
+    if (u0 + DQ < U) {
+      issue_unit(u0 + 2);
+      issue_unit(u0 + 3);
     }
-    const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xb[j].xs, kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    BlockConsts kc[2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      acc[mt][v] += fmaf(kc.d, cl[v] + ch[v], -kc.dmin * cm[v]) * xb[j].dv[v];
+    for (int e = 0; e < 2; ++e)
+      kc[e] = block_consts(hdr[u0 + e], g);
+    f4_t cl[2], ch[2], cm[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      cl[e] = ch[e] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const u4_t qq = s < 2 ? q0[u0 + e] : q1[u0 + e];
+        const uint32_t wa = qq[2 * (s & 1)], wb = qq[2 * (s & 1) + 1];
+        const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc[e].mul_lo, kc[e].add_lo);
+        const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc[e].mul_hi, kc[e].add_hi);
+        cl[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[j].frag[s], blo, cl[e], 0, 0, 0);
+        ch[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[j].frag[4 + s], bhi, ch[e], 0, 0, 0);
+      }
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      cm[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(xb[j].xs, kc[e].bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[mt0 + e][v] += fmaf(kc[e].d, cl[e][v] + ch[e][v], -kc[e].dmin * cm[e][v]) * xb[j].dv[v];
   }
-  gate_up_finish<T, OutT>(a, xl, acc, item);
+  gate_up_finish<T, OutT, W, BPW>(a, xl, acc, item);
 }
 
-template <int T, typename OutT, bool NORM>
-__global__ __launch_bounds__(512) void q4k_gemv_gate_up_kernel(GemvArgs a) {
-  __shared__ __attribute__((aligned(16))) float xl[8][kGuWaveFloats];
-  __shared__ float ssq[8][8];
-  gate_up_item<T, OutT, NORM>(a, xl, ssq, blockIdx.x);
+template <int T, typename OutT, bool NORM, int W>
+__global__ __launch_bounds__(64 * W) void q4k_gemv_gate_up_kernel(GemvArgs a) {
+  constexpr int BPW = 16 / W;
+  __shared__ __attribute__((aligned(16))) float xl[W * gu_wave_floats<BPW>()];
+  __shared__ float ssq[W][8];
+  gate_up_item<T, OutT, NORM, W, BPW>(a, xl, ssq, blockIdx.x);
 }
 
 // ----------------------------------------------------------------------------
@@ -2246,9 +2273,8 @@ __device__ __forceinline__ void typed_epilogue(const GemvArgs& a, const float* p
 // item's x packing and epilogue (gate_up_pack_x, gate_up_finish) around the
 // type's tile-block units (F::load, F::mac), two units in flight per wave.
 template <class F, int T, typename OutT, bool NORM>
-__device__ __forceinline__ void typed_gate_up_item(const GemvArgs& a, float (*xl)[kGuWaveFloats], float (*ssq)[8], int item) {
+__device__ __forceinline__ void typed_gate_up_item(const GemvArgs& a, float* xl, float (*ssq)[8], int item) {
   constexpr int W = 8, BPW = 2, NM = 2, MT = NM * T, U = BPW * MT, DQ = 2;
-  static_assert(MT * 8 * 16 <= BPW * 64 * kGuXRow, "partials fit the x region");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nb = a.nb, bw = ((wave + item) % W) * BPW;
@@ -2260,7 +2286,7 @@ __device__ __forceinline__ void typed_gate_up_item(const GemvArgs& a, float (*xl
     __builtin_amdgcn_sched_barrier(0);
   };
   XBlock xb[BPW];
-  gate_up_pack_x<OutT, NORM>(a, xl, ssq, bw, xb, [&] {
+  gate_up_pack_x<OutT, NORM, W, BPW>(a, xl, ssq, bw, xb, [&] {
 #pragma unroll
     for (int u = 0; u < (DQ < U ? DQ : U); ++u)
       issue_unit(u);
@@ -2288,12 +2314,12 @@ __device__ __forceinline__ void typed_gate_up_item(const GemvArgs& a, float (*xl
       issue_unit(u + DQ);
     F::mac(un[u], xf[j], lane, acc[mt]);
   }
-  gate_up_finish<T, OutT>(a, xl, acc, item);
+  gate_up_finish<T, OutT, W, BPW>(a, xl, acc, item);
 }
 
 template <class F, int T, typename OutT, bool NORM>
 __global__ __launch_bounds__(512) void typed_gate_up_kernel(GemvArgs a) {
-  __shared__ __attribute__((aligned(16))) float xl[8][kGuWaveFloats];
+  __shared__ __attribute__((aligned(16))) float xl[8 * gu_wave_floats<2>()];
   __shared__ float ssq[8][8];
   typed_gate_up_item<F, T, OutT, NORM>(a, xl, ssq, blockIdx.x);
 }
@@ -3100,12 +3126,16 @@ bool gemv_gate_up_supported(int m, int nb, int n) {
   return enabled && m >= 1 && m <= 8 && nb == 16 && n % 16 == 0;
 }
 
+// Eight waves per workgroup, two K-blocks each.  (Sixteen waves of one
+// block each need more than their 128 registers and spill.)
+constexpr int kGuWaves = 8;
+
 template <int T, bool NORM>
 hipError_t gate_up_launch(hipStream_t s, const GemvArgs& a, int dtype, unsigned grid) {
   if (dtype == kF32)
-    (void)dispatch(q4k_gemv_gate_up_kernel<T, float, NORM>, dim3(grid), dim3(512), s, a);
+    (void)dispatch(q4k_gemv_gate_up_kernel<T, float, NORM, kGuWaves>, dim3(grid), dim3(64 * kGuWaves), s, a);
   else
-    (void)dispatch(q4k_gemv_gate_up_kernel<T, _Float16, NORM>, dim3(grid), dim3(512), s, a);
+    (void)dispatch(q4k_gemv_gate_up_kernel<T, _Float16, NORM, kGuWaves>, dim3(grid), dim3(64 * kGuWaves), s, a);
   return hipGetLastError();
 }
 
