@@ -36,7 +36,7 @@ extern "C" {
 
 #define Q4K_OK 0
 #define Q4K_EINVAL (-1) /* null pointer, bad post code, bad dtype, bad count table */
-#define Q4K_ETYPE (-2)  /* ggml type other than Q4_K / Q6_K (or not Q4_K where only Q4_K is served) */
+#define Q4K_ETYPE (-2)  /* ggml type the path does not serve (not Q4_K / Q6_K / Q5_K / Q8_0 / IQ4_XS), or a type an entry point does not take (q4k_embedding: Q4_K only) */
 #define Q4K_ESHAPE (-3) /* k % 256 != 0, n % 16 != 0, m out of range, byte count mismatch */
 #define Q4K_EALIAS (-4) /* x overlaps y (aux may alias y) */
 #define Q4K_EHIP (-5)   /* HIP runtime failure */
@@ -82,10 +82,14 @@ const char* q4k_last_error(void);
  * The bytes are re-laid out for the kernels during the upload; the caller's
  * buffer is not retained.  Replaces the zero-copy Weight view built by
  * loadWeights (model/qwen35/forward.cpp:12-23, qwen35.hpp:34-37), whose
- * Weight keys its kernels on the type (forward.cpp:55-57).  The types other
- * than Q4_K serve q4k_linear and the two-call form of the gated projection;
- * the fused gate/up kernel and q4k_embedding take Q4_K only (Q4K_ETYPE
- * otherwise). */
+ * Weight keys its kernels on the type (forward.cpp:55-57).  Every type
+ * serves q4k_linear, q4k_linear_norm, q4k_mlp_gate_up and q4k_mlp in every
+ * phase.  Decode passes of a gated pair run one fused gate/up kernel for
+ * Q4_K pairs, and for Q5_K and IQ4_XS pairs with m <= 8 and k = 4096 (the
+ * types the reference fuses, fused_kernels.metal:44-200); other gated
+ * decode passes (Q6_K, Q8_0, pairs of two types) make the reference's two
+ * calls.  q4k_embedding and q4k_embedding_batch take Q4_K tables only
+ * (Q4K_ETYPE otherwise). */
 int q4k_weight_create(const void* gguf_bytes, size_t bytes, uint32_t n, uint32_t k, uint32_t ggml_type, int device, q4k_weight** out);
 
 /* Same, from bytes already in device memory of `device` (GGUF order). */
@@ -257,9 +261,10 @@ int q4k_gguf_tensor_data(const q4k_gguf* g, uint64_t i, const void** data, uint6
 int q4k_gguf_meta_int(const q4k_gguf* g, const char* key, int64_t* value);
 int q4k_gguf_meta_str(const q4k_gguf* g, const char* key, char* buf, size_t len);
 
-/* Upload the Q4_K matrix called name to device as a weight with n = ne[1]
- * rows of k = ne[0] (the Weight loadWeights builds, forward.cpp:18-21);
- * Q4K_ETYPE if it is not Q4_K. */
+/* Upload the matrix called name to device as a weight with n = ne[1] rows
+ * of k = ne[0] (the Weight loadWeights builds, forward.cpp:18-21), as
+ * q4k_weight_create does; Q4K_ETYPE if its ggml type is not one of Q4_K,
+ * Q6_K, Q5_K, Q8_0 and IQ4_XS, Q4K_ESHAPE if it is not a 2-D matrix. */
 int q4k_weight_from_gguf(const q4k_gguf* g, const char* name, int device, q4k_weight** out);
 
 /* Kernel families, for q4k_profile_query. */

@@ -495,8 +495,10 @@ int set_device(int device) {
 // GEMM below.
 constexpr uint32_t kTypedGemmRows = 64;
 // Prefill-sized batches with the other types (m >= 64): x staged in the GEMM
-// order (fp16, power-of-two row scales, zero rows up to the 128-row tile; the
-// attn/ffn norm folded in), then the type's MFMA GEMM, which dequantises the
+// order (fp16, power-of-two row scales, the attn/ffn norm folded in; only the
+// m live rows are stored: the padded rows up to the 128-row tile keep whatever
+// the workspace held, which no stored output reads, since each MFMA output row
+// depends on its own A row only), then the type's MFMA GEMM, which dequantises the
 // weights to the reference's prefill tile values in registers and applies the
 // epilogue (row unscale, post 0/1/2, fp16 rounding) in place.
 int run_typed_gemm_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, const void* x, void* y, const void* aux, uint32_t m, uint32_t post,
@@ -1455,12 +1457,12 @@ int q4k_embedding_batch(void* stream, const q4k_weight* table, const int32_t* to
   }
   if (rows == 0 || rows > 65535)
     return fail(Q4K_ESHAPE, "the batch must have 1..65535 rows (got %llu)", (unsigned long long)rows);
-  if ((uint64_t)(max_slot + 1) * capacity > 0x7fffffffull)
+  if (((uint64_t)max_slot + 1) * capacity > 0x7fffffffull)
     return fail(Q4K_ESHAPE, "slot %u x capacity %u exceeds the token buffer's 32-bit index", max_slot, capacity);
   if (rows_out)
     *rows_out = (uint32_t)rows;
   const size_t es = dtype == Q4K_DTYPE_F32 ? 4 : 2;
-  if (overlaps(tokens, (size_t)(max_slot + 1) * capacity * 4, y, (size_t)rows * table->k * es))
+  if (overlaps(tokens, ((size_t)max_slot + 1) * capacity * 4, y, (size_t)rows * table->k * es))
     return fail(Q4K_EALIAS, "y must not overlap tokens");
   int rc = set_device(table->device);
   if (rc)

@@ -69,7 +69,7 @@ def _check_tensor(t, numel, what, device=None):
 
 
 class Weight:
-    """A Q4_K (or Q6_K) weight uploaded once to HBM (re-laid out for the kernels).
+    """A quantized weight (Q4_K, Q6_K, Q5_K, Q8_0 or IQ4_XS) uploaded once to HBM (re-laid out for the kernels).
 
     ``data`` holds GGUF block_q4_K (or block_q6_K, ``ggml_type=14``) bytes for
     n rows of k/256 blocks: a host numpy/bytes buffer, or a uint8 CUDA tensor

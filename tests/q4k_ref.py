@@ -385,6 +385,14 @@ class Oracle:
         fn(self._p(np.ascontiguousarray(blk, np.uint8)), self._p(out))
         return out
 
+    def dequant_block_f16(self, blk, ggml_type=TYPE_Q4_K):
+        """The 256 fp16 bit patterns of one block at the reference's prefill
+        tile value (Q4_K and Q6_K: q4o_ / q6o_dequant_block_f16)."""
+        out = np.empty(256, np.uint16)
+        fn = self.lib.q6o_dequant_block_f16 if ggml_type == TYPE_Q6_K else self.lib.q4o_dequant_block_f16
+        fn(self._p(np.ascontiguousarray(blk, np.uint8)), self._p(out))
+        return out
+
     def q6_fields(self, blk):
         """(quants 0..63, int8 scales) of the 256 elements of one block_q6_K."""
         b = np.ascontiguousarray(blk, np.uint8)

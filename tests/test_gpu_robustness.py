@@ -1,5 +1,7 @@
 """Host-side guards of the C ABI on the GPU: graph capture that would need
 workspace growth, and mis-sized tensors handed to the Python wrappers."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -72,3 +74,23 @@ def test_wrapper_size_checks(q4k, gpu):
     q4k.linear(x, W, 4, y)
     torch.cuda.synchronize()
     assert torch.isfinite(y).all()
+
+
+def test_embedding_batch_slot_index_wrap_refused(q4k, gpu):
+    """A slot whose (slot + 1) * capacity does not fit the token buffer's
+    32-bit index (here slot 0xFFFFFFFF, where slot + 1 wraps to 0 in 32-bit
+    arithmetic) is refused with Q4K_ESHAPE before any launch; a valid slot
+    in the same call shape goes through."""
+    W = q4k.Weight(make_q4k(np.random.default_rng(1214), 64, 256), 64, 256)
+    tokens = torch.zeros(16, dtype=torch.int32, device=gpu)
+    y = torch.zeros((1, 256), device=gpu)
+    u32 = ctypes.c_uint32
+    one, zero = (u32 * 1)(1), (u32 * 1)(0)
+    for slot, cap in ((0xFFFFFFFF, 8), (0x7FFFFFFF, 2), (0x10000000, 8)):
+        rc = q4k.lib.q4k_embedding_batch(None, W.handle, ctypes.c_void_p(tokens.data_ptr()), cap, one, zero, (u32 * 1)(slot), 1,
+                                         ctypes.c_void_p(y.data_ptr()), 0, None)
+        assert rc == -3, (slot, cap, rc)
+        assert "32-bit" in q4k.lib.q4k_last_error().decode()
+    rows = q4k.embedding_batch(W, tokens, 8, [1], [0], [1], y)
+    torch.cuda.synchronize()
+    assert rows == 1 and torch.isfinite(y).all()

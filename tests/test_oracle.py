@@ -88,6 +88,22 @@ def test_dequant_matches_embedding_addressing(oracle):
     np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-7)
 
 
+def test_dequant_block_f16_tile_value(oracle):
+    """q4o_dequant_block_f16 stores the reference's prefill tile value
+    half(fp32(d * sc * q - dmin * m)) (quant_linear.metal:43,45): the kmask
+    form in float64 (its two products are exact) rounded to fp32, then to
+    fp16, bit for bit, over random blocks and blocks whose d and dmin push
+    values into fp16 denormals and past the fp16 range."""
+    rng = np.random.default_rng(41)
+    for dmax in (0.01, 1e-7, 100.0):
+        w = make_q4k(rng, 64, 256, dmax=dmax)
+        ref = dequant_numpy(w, 64, 256)
+        with np.errstate(over="ignore"):
+            want = ref.astype(np.float32).astype(np.float16).view(np.uint16)
+        got = np.stack([oracle.dequant_block_f16(b) for b in w.reshape(64, 144)])
+        np.testing.assert_array_equal(got, want)
+
+
 def test_one_hot_element_map(oracle):
     """x = e_k gives y[n] = W[n, k]: pins every (element -> byte, nibble, sub-block) position."""
     rng = np.random.default_rng(5)

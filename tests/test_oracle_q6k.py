@@ -111,11 +111,27 @@ def test_brute_force_numpy(oracle):
     np.testing.assert_allclose(oracle.linear_f64(x, w, n, k, ggml_type=TYPE_Q6_K), ref, rtol=1e-12, atol=1e-12)
 
 
-def test_dequant_block_and_f16_store(oracle):
+def test_dequant_block_f32(oracle):
     rng = np.random.default_rng(9)
     blk = make_q6k(rng, 1, 256)[0]
     f32 = oracle.dequant_block(blk, ggml_type=TYPE_Q6_K)
     np.testing.assert_allclose(f32, dequant_q6k_numpy(blk, 1, 256)[0], rtol=1e-6, atol=0)
+
+
+def test_dequant_block_f16_tile_value(oracle):
+    """q6o_dequant_block_f16 stores the reference's prefill tile value
+    half(fp32(d * sc * (q - 32))) (quant_linear.metal:83): the bit-mask form
+    in float64 (its products are exact) rounded to fp32, then to fp16, bit
+    for bit, over random blocks and blocks whose d pushes values into fp16
+    denormals and past the fp16 range."""
+    rng = np.random.default_rng(91)
+    for dmax in (0.01, 1e-7, 40.0):
+        w = make_q6k(rng, 64, 256, dmax=dmax)
+        ref = dequant_q6k_numpy(w, 64, 256)
+        with np.errstate(over="ignore"):
+            want = ref.astype(np.float32).astype(np.float16).view(np.uint16)
+        got = np.stack([oracle.dequant_block_f16(b, ggml_type=TYPE_Q6_K) for b in w.reshape(64, Q6_BLOCK_BYTES)])
+        np.testing.assert_array_equal(got, want)
 
 
 def test_posts_and_gate_up(oracle):
