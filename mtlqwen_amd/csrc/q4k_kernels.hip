@@ -1179,27 +1179,40 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   constexpr int EPI = 16 * T;  // outputs per row of a group
-  for (int o = tid; o < a.m * EPI; o += 64 * W) {
+  // The outputs of the group this thread finishes (at most PER of them), with
+  // all their loads (the KS slice partials, and aux) issued before a single
+  // wait: the reduction costs one memory round trip, not two per output.
+  constexpr int PER = (8 * EPI + 64 * W - 1) / (64 * W);
+  float pv[PER][NM][KS], av[PER];
+  size_t offs[PER];
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int o0 = tid + r * 64 * W, o = o0 < a.m * EPI ? o0 : 0;
     const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
-    float pv[NM][KS];
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
       for (int k2 = 0; k2 < KS; ++k2)
-        pv[mi][k2] = load_coherent(part + ((((size_t)grp * KS + k2) * MT + mi * T + t) * 8 + row) * 16 + cc);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        pv[r][mi][k2] = load_coherent(part + ((((size_t)grp * KS + k2) * MT + mi * T + t) * 8 + row) * 16 + cc);
+    offs[r] = (size_t)row * a.n + ((size_t)grp * T + t) * 16 + cc;
+    av[r] = NM == 1 && a.post != 0 ? load_elem(aux, offs[r]) : 0.0f;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    if (tid + r * 64 * W >= a.m * EPI)
+      break;
     float sm[NM];
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
       float v = 0.0f;
 #pragma unroll
       for (int k2 = 0; k2 < KS; ++k2) {
-        hold(pv[mi][k2]);
-        v += pv[mi][k2];
+        hold(pv[r][mi][k2]);
+        v += pv[r][mi][k2];
       }
       sm[mi] = v;
     }
-    const size_t off = (size_t)row * a.n + ((size_t)grp * T + t) * 16 + cc;
     float out;
     if (NM == 2) {
       float gv = sm[0], uv = sm[NM - 1];
@@ -1212,9 +1225,9 @@ __device__ __forceinline__ void splitk_slice(const GemvArgs& a, uint8_t* lds, in
       float acc_v = sm[0];
       if (sizeof(OutT) == 2)
         acc_v = round_half(acc_v);
-      out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+      out = a.post == 1 ? acc_v + av[r] : a.post == 2 ? silu(av[r]) * acc_v : acc_v;
     }
-    store_elem(y, off, out);
+    store_elem(y, offs[r], out);
   }
   if (tid == 0)
     reset_counter(&counters[grp]);  // ready for the next launch
