@@ -267,6 +267,14 @@ int q4k_gguf_meta_str(const q4k_gguf* g, const char* key, char* buf, size_t len)
  * Q6_K, Q5_K, Q8_0 and IQ4_XS, Q4K_ESHAPE if it is not a 2-D matrix. */
 int q4k_weight_from_gguf(const q4k_gguf* g, const char* name, int device, q4k_weight** out);
 
+/* Number of device allocations (hipMalloc) the library has made for its
+ * workspaces (staging, split-K partials and counters, normalised inputs) in
+ * this process, on every device.  No counterpart in the reference; it lets
+ * a caller or a test show that a call allocated nothing (the count does not
+ * change across it).  Weight uploads and the measurement entry points
+ * (q4k_mfma_ceiling, q4k_read_ceiling) are not counted. */
+int q4k_workspace_allocations(uint64_t* count);
+
 /* Kernel families, for q4k_profile_query. */
 #define Q4K_KERNEL_STAGE 0u      /* activation staging (fp16 + row scale) */
 #define Q4K_KERNEL_GEMV 1u       /* MFMA GEMV, phases 0/2 and small prefill */

@@ -63,6 +63,7 @@ def _load():
         "q4k_weight_prepare": (c_int, [p, u32]),
         "q4k_linear": (c_int, [p, p, p, p, p, u32, pu32, u32, u32, u32]),
         "q4k_linear_noalloc": (c_int, [p, p, p, p, p, u32, pu32, u32, u32, u32]),
+        "q4k_workspace_allocations": (c_int, [ctypes.POINTER(ctypes.c_uint64)]),
         "q4k_linear_norm": (c_int, [p, p, p, ctypes.c_float, p, p, p, u32, pu32, u32, u32, u32]),
         "q4k_mlp_gate_up": (c_int, [p, p, p, p, p, u32, pu32, u32, u32]),
         "q4k_mlp": (c_int, [p, p, p, p, p, ctypes.c_float, p, p, p, u32, pu32, u32, u32]),

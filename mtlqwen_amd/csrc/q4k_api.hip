@@ -6,6 +6,7 @@
 // linear() picks the phase from the packed batch's per-query row counts.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -336,6 +337,10 @@ Workspace& workspace(int device) {
 // stream captures a graph, and a failure there would look like a lack of
 // memory: a call on a capturing stream that needs more workspace than the
 // device already holds fails with Q4K_ECAPTURE instead, before allocating.
+// Device allocations made for workspaces since the library was loaded
+// (q4k_workspace_allocations).
+std::atomic<uint64_t> g_ws_allocations{0};
+
 int ws_alloc(hipStream_t stream, int device, void** p, size_t bytes, const char* what) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone)
@@ -347,6 +352,7 @@ int ws_alloc(hipStream_t stream, int device, void** p, size_t bytes, const char*
     *p = nullptr;
     return fail(Q4K_ENOMEM, "cannot allocate %zu-byte %s on device %d", bytes, what, device);
   }
+  g_ws_allocations.fetch_add(1, std::memory_order_relaxed);
   return Q4K_OK;
 }
 
@@ -1247,6 +1253,13 @@ int q4k_mlp(void* stream, q4k_weight* wg, q4k_weight* wu, q4k_weight* wd, const 
   if (rc)
     return rc;
   return q4k_linear(stream, wd, gate, hidden, hidden, m, query_counts, nqueries, Q4K_POST_ADD, dtype);
+}
+
+int q4k_workspace_allocations(uint64_t* count) {
+  if (!count)
+    return fail(Q4K_EINVAL, "null argument");
+  *count = g_ws_allocations.load(std::memory_order_relaxed);
+  return Q4K_OK;
 }
 
 int q4k_profile_enable(int on) {

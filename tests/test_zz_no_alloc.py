@@ -2,7 +2,10 @@
 q4k_linear through the C ABI: the same kernels on the same inputs, so the
 outputs must be identical, on two calls in a row (the second smaller) for
 every kernel family the entry point reaches, Q4_K and the other weight
-types' prefill GEMM; and its refusals."""
+types' prefill GEMM; the library's workspace allocation count
+(q4k_workspace_allocations) unchanged across every no-allocation call; a
+capture of the entry point on shapes q4k_linear was never called with,
+replayed several times; and its refusals."""
 import ctypes
 
 import numpy as np
@@ -21,6 +24,12 @@ def _noalloc(q4k, x, w, m, y, aux=None, post=0, counts=None):
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     return q4k.lib.q4k_linear_noalloc(stream, w.handle, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
                                       None if aux is None else ctypes.c_void_p(aux.data_ptr()), m, arr, len(counts), post, dt)
+
+
+def _allocations(q4k):
+    c = ctypes.c_uint64()
+    assert q4k.lib.q4k_workspace_allocations(ctypes.byref(c)) == 0
+    return c.value
 
 
 # (label, n, k, first (m, counts), second (m, counts), post, dtype)
@@ -56,10 +65,51 @@ def test_noalloc_matches_linear(q4k, gpu, label, n, k, first, second, post, dtyp
         y_ref = aux0.clone() if post else torch.empty((m, n), device=gpu, dtype=dtype)
         q4k.linear(x, W, m, y_ref, auxiliary=y_ref if post else None, gated=(post == 2), query_counts=counts)
         y = aux0.clone() if post else torch.full((m, n), float("nan"), device=gpu, dtype=dtype)
+        torch.cuda.synchronize()
+        before = _allocations(q4k)
         rc = _noalloc(q4k, x, W, m, y, aux=y if post else None, post=post, counts=counts)
         assert rc == 0, q4k.lib.q4k_last_error().decode()
         torch.cuda.synchronize()
+        assert _allocations(q4k) == before, f"{label} m={m}: the call allocated device memory"
         assert torch.equal(y, y_ref), f"{label} m={m}"
+
+
+def test_noalloc_captures_on_fresh_shapes(q4k, gpu):
+    """Captured in a HIP graph on shapes this process never passed to
+    q4k_linear (whose workspace would have to grow, which the capture
+    forbids): the capture succeeds, allocates nothing, and every replay --
+    with eager work and a synchronisation between replays -- gives the
+    output of q4k_linear called eagerly after the capture.  The split-K
+    GEMV and the GEMM's two K-halves clear their counters with a fill
+    kernel inside the graph."""
+    rng = np.random.default_rng(1320)
+    # The split-K GEMV (K = 12288), the GEMM in two K-halves and the staged
+    # GEMV at K = 16640, a K no other test of this suite uses.
+    cases = [(8192, 12288, 8, [1] * 8, 1), (1024, 16640, 200, [200], 1), (1536, 16640, 40, [5] * 8, 0)]
+    for n, k, m, counts, post in cases:
+        W = q4k.Weight(make_q4k(rng, n, k), n, k)
+        x = torch.from_numpy(make_x(rng, m, k, 0.25)).to(gpu)
+        aux0 = torch.from_numpy(make_x(rng, m, n, 0.5)).to(gpu)
+        y = aux0.clone()
+        s = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        before = _allocations(q4k)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            rc = _noalloc(q4k, x, W, m, y, aux=y if post else None, post=post, counts=counts)
+        assert rc == 0, q4k.lib.q4k_last_error().decode()
+        assert _allocations(q4k) == before
+        y_ref = aux0.clone()
+        q4k.linear(x, W, m, y_ref, auxiliary=y_ref if post else None, query_counts=counts)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            y.copy_(aux0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, y_ref), f"n={n} k={k} m={m}: replay {rep}"
+            _ = (aux0 * 2.0).sum().item()  # eager work between replays
+        assert _allocations(q4k) >= before
 
 
 def test_noalloc_refusals(q4k, gpu):
