@@ -726,7 +726,12 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.rows = rows;
     a.split = split ? 1 : 0;
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr, device_cus(w->device)), wu != nullptr), "gemv launch");
+    const int rows_tiles = gemv_rows_tiles(rows, a.nb, a.n, wu != nullptr, device_cus(w->device));
+    if (rows_tiles > 0)
+      Q4K_TRY_HIP(launch_gemv_rows(stream, a, (int)dtype, rows_tiles, wu != nullptr), "gemv rows launch");
+    else
+      Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr, device_cus(w->device)), wu != nullptr),
+                  "gemv launch");
   } else {
     GemmArgs a;
     a.w = w->data;

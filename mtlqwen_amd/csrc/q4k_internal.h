@@ -402,6 +402,11 @@ GemvShape gemv_shape(int rows, int n, int nb, bool gated, int cus);
 // staging launch); reads a.x, a.w, a.wu (and a.norm_w when set) and writes a.y.
 bool gemv_gate_up_supported(int m, int nb, int n);
 hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus);
+// GEMV over staged x of 17..48 fragment rows: T column tiles of NM matrices
+// per workgroup, 8 waves splitting K (K = 2048 .. 12288), each block of x
+// read once per wave.  gemv_rows_tiles returns T (0: not this kernel).
+int gemv_rows_tiles(int rows, int nb, int n, bool gated, int cus);
+hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, int tiles, bool gated);
 // The same for gate and up weights of one other type with a fused decode
 // kernel in the reference (Q5_K, IQ4_XS).
 bool typed_gate_up_supported(uint32_t type, int m, int nb, int n);

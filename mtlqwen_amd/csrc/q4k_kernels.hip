@@ -947,6 +947,156 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_gate_up_kernel(GemvArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// GEMV for staged activations of 17..48 fragment rows (the decode pass of a
+// speculative batch, up to 8 queries x 5 rows), K = 2048 .. 12288.
+//
+// The work split of the fused gate/up GEMV over the staged fp16 fragments
+// (stage_x_kernel, one power-of-two scale per row; split rows carry the low
+// parts) of the RT row tiles: workgroup = one item of T column tiles of NM
+// matrices (NM = 2: gate and up), 8 waves; wave w owns K-blocks bw ..
+// bw + BPW - 1 (bw = BPW ((w + item) % 8)) of the item's NM T (matrix, tile)
+// pairs, U = BPW NM T units.  The wave loads a block's fragments for all RT
+// row tiles once (RT x 8 KB from the staging) and every unit of that block
+// multiplies them: RT x 8 v_mfma_f32_16x16x32_f16 and RT min-term MFMAs per
+// tile-block dequantised once.  A CU thus reads the staged x once per T
+// column tiles of NM matrices; the one-tile GEMV reads it once per column
+// tile, and at M = 40 its gated launch was bound by those reads (768
+// workgroups x 384 KB).  Units stream two ahead as in the fused gate/up
+// GEMV; a block's fragments replace the previous block's after its units
+// (one L2 round trip per block and wave, which the SIMD's other wave
+// covers).  The 8 waves' partial sums meet in LDS in wave order.
+// ----------------------------------------------------------------------------
+template <int NM, int T, int RT, int BPW, typename OutT>
+__global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
+  constexpr int W = 8, MT = NM * T, U = BPW * MT, ROWS = 16 * RT, DQ = 2;
+  __shared__ float red[W][MT][ROWS][16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int item = blockIdx.x, nb = a.nb, bw = BPW * ((wave + item) % W);
+  const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
+
+  u4_t hdr[U], q0[U], q1[U];
+  auto issue_unit = [&](int u) {
+    const int j = u / MT, mt = u - j * MT, mi = mt / T, t = mt - mi * T;
+    const uint8_t* src = (mi ? a.wu : a.w) + ((size_t)item * T + t) * tile_bytes + (size_t)(bw + j) * kTileBlockBytes;
+    hdr[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kHeaderOffset) + col);
+    q0[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src) + lane);
+    q1[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(src + kSlabBytes) + lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Dead fragment rows (>= a.rows inside the last row tile) are loaded as
+  // they are: a garbage A row reaches only its own C row, never stored.
+  h8_t xa[RT][8];
+  h4_t xsa[RT];
+  auto load_x = [&](int b) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const h8_t* xp = reinterpret_cast<const h8_t*>(a.xf) + (size_t)(rt * nb + b) * 8 * 64 + lane;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        xa[rt][s] = xp[s * 64];
+      xsa[rt] = reinterpret_cast<const h4_t*>(a.xs)[(size_t)(rt * nb + b) * 32 + (lane & 31)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  load_x(bw);
+#pragma unroll
+  for (int u = 0; u < (DQ < U ? DQ : U); ++u)
+    issue_unit(u);
+
+  f4_t acc[MT][RT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      acc[mt][rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = u / MT, mt = u - j * MT;
+    __builtin_amdgcn_sched_barrier(0);
+    if (u > 0 && mt == 0)
+      load_x(bw + j);
+    if (u + DQ < U)
+      issue_unit(u + DQ);
+    const BlockConsts kc = block_consts(hdr[u], g);
+    f4_t cq[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      cq[rt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u4_t qq = s < 2 ? q0[u] : q1[u];
+      const uint32_t wa = qq[2 * (s & 1)], wb = qq[2 * (s & 1) + 1];
+      const h8_t blo = quant_times_scale(wa, wb, 0x000F000Fu, 0x64006400u, kc.mul_lo, kc.add_lo);
+      const h8_t bhi = quant_times_scale(wa, wb, 0x00F000F0u, 0x64006400u, kc.mul_hi, kc.add_hi);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        cq[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][s], blo, cq[rt], 0, 0, 0);
+        cq[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rt][4 + s], bhi, cq[rt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      // min term: sum_j (xs_j / 32) * (32 m_j), k = sub-block
+      const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[mt][rt][v] = fmaf(kc.d, cq[rt][v], fmaf(-kc.dmin, cm[v], acc[mt][rt][v]));
+      // Each unit's sums are folded here: otherwise the compiler defers the
+      // folds and keeps every unit's MFMA results live.
+      asm volatile("" : "+v"(acc[mt][rt]));
+    }
+  }
+
+  // C fragment of lane l: rows 4 (l / 16) + v of each row tile, column l % 16.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        red[wave][mt][rt * 16 + 4 * g + v][col] = acc[mt][rt][v];
+  __syncthreads();
+  OutT* y = reinterpret_cast<OutT*>(a.y);
+  const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
+  constexpr int EPI = 16 * T;
+  for (int o = tid; o < a.m * EPI; o += 64 * W) {
+    const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
+    float s[NM];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        v += red[w][mi * T + t][row][cc];
+      if (a.split) {
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          v += red[w][mi * T + t][a.m + row][cc];
+      }
+      s[mi] = v * a.rowscale[row];
+    }
+    const size_t off = (size_t)row * a.n + ((size_t)item * T + t) * 16 + cc;
+    float out;
+    if (NM == 2) {
+      float gv = s[0], uv = s[NM - 1];
+      if (sizeof(OutT) == 2) {
+        gv = round_half(gv);
+        uv = round_half(uv);
+      }
+      out = silu(gv) * uv;
+    } else {
+      float acc_v = s[0];
+      if (sizeof(OutT) == 2)
+        acc_v = round_half(acc_v);
+      out = a.post == 1 ? acc_v + load_elem(aux, off) : a.post == 2 ? silu(load_elem(aux, off)) * acc_v : acc_v;
+    }
+    store_elem(y, off, out);
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Split-K GEMV (m <= 8 rows, split hi/lo into one 16-row activation tile).
 //
 // Each CU of a persistent launch would otherwise pull all of x from L2 (32 MB
@@ -3132,6 +3282,83 @@ hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const
   // Two block-steps in flight per wave: measured faster than four (shorter
   // memory queues, as for the fused gate/up GEMV).
   return splitk_launch<1, 8, 8, 6, 2>(s, a, dtype, plan.grid, part, counters);
+}
+
+// Column tiles per workgroup of the rows GEMV (0: not this kernel).  Gated
+// pairs at K = 4096 take 3 (one workgroup per CU at N = 12288): at M = 40
+// 19.4 us against 26.7 on the one-tile GEMV.  Plain projections with K =
+// 12288 take the most of 3, 2, 1 that still gives every CU a workgroup, or
+// 1 (M = 40, N = 4096: 19.1 against 20.5 us).  Plain projections at K = 4096
+// stay on the staged GEMV, which already splits K over 8 waves with two
+// column tiles where that fills the CUs (measured as fast or faster).
+int gemv_rows_tiles(int rows, int nb, int n, bool gated, int cus) {
+  static const int forced = env_int("Q4K_GEMV_ROWS", -1);  // -1 auto, 0 off, 1..3 column tiles
+  if (forced == 0 || rows <= 16 || rows > 16 * kGemvMaxRowTiles || n % 16 != 0)
+    return 0;
+  const int ctiles = n / 16;
+  if (gated) {
+    if (nb != 16)
+      return 0;
+    const int t = forced > 0 ? forced : 3;
+    return ctiles % t == 0 && (forced > 0 || ctiles / t >= cus) ? t : 0;
+  }
+  if (nb != 48 && !(forced > 0 && nb == 16))
+    return 0;
+  if (forced > 0)
+    return ctiles % forced == 0 ? forced : 0;
+  for (int t = 3; t >= 1; --t)
+    if (ctiles % t == 0 && ctiles / t >= cus)
+      return t;
+  return 1;
+}
+
+template <int NM, int T, int RT, int BPW>
+hipError_t gemv_rows_launch(hipStream_t s, const GemvArgs& a, int dtype) {
+  const dim3 grid((unsigned)(a.n / (16 * T))), block(512);
+  if (dtype == kF32)
+    (void)dispatch(q4k_gemv_rows_kernel<NM, T, RT, BPW, float>, grid, block, s, a);
+  else
+    (void)dispatch(q4k_gemv_rows_kernel<NM, T, RT, BPW, _Float16>, grid, block, s, a);
+  return hipGetLastError();
+}
+
+// K = 4096 (2 blocks per wave) and, for plain projections, K = 12288 (6).
+template <int NM, int T, int RT>
+hipError_t gemv_rows_bpw(hipStream_t s, const GemvArgs& a, int dtype) {
+  if (a.nb == 16)
+    return gemv_rows_launch<NM, T, RT, 2>(s, a, dtype);
+  if constexpr (NM == 1) {
+    if (a.nb == 48)
+      return gemv_rows_launch<NM, T, RT, 6>(s, a, dtype);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int NM, int T>
+hipError_t gemv_rows_rt(hipStream_t s, const GemvArgs& a, int dtype) {
+  return a.rows <= 32 ? gemv_rows_bpw<NM, T, 2>(s, a, dtype) : gemv_rows_bpw<NM, T, 3>(s, a, dtype);
+}
+
+hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, int tiles, bool gated) {
+  if (a.rows <= 16 || a.rows > 16 * kGemvMaxRowTiles || (a.nb != 16 && a.nb != 48) || a.n % (16 * tiles) != 0 ||
+      a.rows != (a.split ? 2 * a.m : a.m))
+    return hipErrorInvalidValue;
+  if (gated) {
+    if (a.nb != 16)
+      return hipErrorInvalidValue;
+    switch (tiles) {
+      case 3: return gemv_rows_rt<2, 3>(s, a, dtype);
+      case 2: return gemv_rows_rt<2, 2>(s, a, dtype);
+      case 1: return gemv_rows_rt<2, 1>(s, a, dtype);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (tiles) {
+    case 3: return gemv_rows_rt<1, 3>(s, a, dtype);
+    case 2: return gemv_rows_rt<1, 2>(s, a, dtype);
+    case 1: return gemv_rows_rt<1, 1>(s, a, dtype);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 bool gemv_gate_up_supported(int m, int nb, int n) {

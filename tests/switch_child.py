@@ -70,7 +70,7 @@ def check_gate_up(m, n, k, t=TYPE_Q4_K, seed=0, family=None, expect=None):
     x = make_x(rng, m, k, 0.5)
     G, U = q4k.Weight(wg, n, k, ggml_type=t), q4k.Weight(wu, n, k, ggml_type=t)
     y = torch.full((m, n), float("nan"), device=dev)
-    counts = [1] * m if m <= 8 else [m]
+    counts = [1] * m if m <= 8 else [m] if m > 48 else [5] * (m // 5) + ([m % 5] if m % 5 else [])
     run = lambda: q4k.mlp_gate_up(_t(x), G, U, m, y, query_counts=counts)
     if family is None:
         run()
@@ -82,7 +82,7 @@ def check_gate_up(m, n, k, t=TYPE_Q4_K, seed=0, family=None, expect=None):
     ref = oracle.mlp_gate_up(x, wg, wu, n, k, ggml_type=t)
     err = row_rel_err(out, ref)
     worst.append(err)
-    if m <= 8:
+    if m <= 8 or counts != [m]:
         assert err <= TOL, (m, n, k, t, err)
     else:
         assert t == TYPE_Q4_K
@@ -106,6 +106,27 @@ def case_gate_up_off():
     check_gate_up(8, 1536, 4096, t=TYPE_Q5_K, seed=21, family=q4k.KERNEL_GEMV_GATED, expect=lambda c: c == 0)
     for t in (TYPE_Q4_K, TYPE_Q5_K):
         check_gate_up(3, 512, 4096, t=t, seed=30 + t)
+
+
+def case_rows():
+    # Decode passes of 17..48 fragment rows: gated pairs at N = 12288 and
+    # plain projections (K = 4096 and 12288) with the rows GEMV off, or
+    # forced to a number of column tiles.
+    for m in (40, 24):
+        check_gate_up(m, 12288, 4096, seed=35 + m)
+    counts40 = [5] * 8
+    for n, k in ((6144, 4096), (4096, 12288)):
+        rng = np.random.default_rng(37 + k % 97)
+        w = make_weight(rng, n, k, TYPE_Q4_K)
+        x = make_x(rng, 40, k)
+        aux = make_x(rng, 40, n)
+        W = q4k.Weight(w, n, k)
+        y = _t(aux)
+        q4k.linear(_t(x), W, 40, y, auxiliary=y, query_counts=counts40)
+        torch.cuda.synchronize()
+        err = row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k, aux=aux, post=1))
+        worst.append(err)
+        assert err <= TOL, (n, k, err)
 
 
 def case_gemv_generic():
@@ -147,6 +168,7 @@ def case_q4k_persistent_off():
 CASES = {
     "splitk_off": case_splitk_off,
     "gate_up_off": case_gate_up_off,
+    "rows": case_rows,
     "gemv_generic": case_gemv_generic,
     "gemv_shape": case_gemv_shape,
     "gemm": case_gemm,
