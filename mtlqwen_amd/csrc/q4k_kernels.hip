@@ -2632,12 +2632,14 @@ __device__ __forceinline__ uint32_t move_bits(uint32_t h, int from, int to) {
   return from >= to ? h >> (from - to) : h << (to - from);
 }
 
-// Two fp32 values rounded to one fp16 pair.  The empty asm keeps the fp32
-// results apart from the conversion (fused, they become a dependent pair of
-// half-register writes).
-__device__ __forceinline__ uint32_t pack_h2(float a0, float a1) {
-  asm("" : "+v"(a0), "+v"(a1));
-  return as_u32(h2_t{(_Float16)a0, (_Float16)a1});
+// Two fp16 pairs from four fp32 values, each rounded once: the four values
+// are formed before either conversion (the empty asm keeps them apart from
+// it), so that no conversion directly follows the v_fma_mix that wrote its
+// source (that adjacency costs two wait states).
+__device__ __forceinline__ void pack_h2x2(float a0, float a1, float b0, float b1, uint32_t& lo, uint32_t& hi) {
+  asm("" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
+  lo = as_u32(h2_t{(_Float16)a0, (_Float16)a1});
+  hi = as_u32(h2_t{(_Float16)b0, (_Float16)b1});
 }
 
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) {
@@ -2690,16 +2692,16 @@ struct TgQ5K {
   // (q + 16h) * 2^-20 (nibble at bits 4..7, fifth bit at bit 8).
   static __device__ __forceinline__ void dequant(const K& k, const W& w, int u, h8_t& blo, h8_t& bhi) {
     const uint32_t lw[4] = {w.q.x, w.q.x >> 8, w.q.y, w.q.y >> 8};
-    u4_t lo, hi;
+    uint32_t lo[4], hi[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const h2_t ql = as_h2(and_or(lw[t], 0x000F000Fu, move_bits(k.h0, 4 * u + t, 4) & 0x00100010u));
       const h2_t qh = as_h2(and_or(lw[t], 0x00F000F0u, move_bits(k.h1, 4 * u + t, 8) & 0x01000100u));
-      lo[t] = pack_h2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl));
-      hi[t] = pack_h2(__builtin_fmaf((float)qh[0], k.dh, k.ch), __builtin_fmaf((float)qh[1], k.dh, k.ch));
+      pack_h2x2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl), __builtin_fmaf((float)qh[0], k.dh, k.ch),
+                __builtin_fmaf((float)qh[1], k.dh, k.ch), lo[t], hi[t]);
     }
-    blo = __builtin_bit_cast(h8_t, lo);
-    bhi = __builtin_bit_cast(h8_t, hi);
+    blo = __builtin_bit_cast(h8_t, u4_t{lo[0], lo[1], lo[2], lo[3]});
+    bhi = __builtin_bit_cast(h8_t, u4_t{hi[0], hi[1], hi[2], hi[3]});
   }
 };
 
@@ -2761,13 +2763,14 @@ struct TgQ6K {
       o[3] = and_or(C << 4, m4, and_or(B << 6, m2, bias));
     }
     const float c = -96.0f * ds;
-    u4_t r;
+    uint32_t r[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const h2_t q = as_h2(o[t]);
-      r[t] = pack_h2(__builtin_fmaf((float)q[0], ds, c), __builtin_fmaf((float)q[1], ds, c));
+    for (int t = 0; t < 4; t += 2) {
+      const h2_t q = as_h2(o[t]), p = as_h2(o[t + 1]);
+      pack_h2x2(__builtin_fmaf((float)q[0], ds, c), __builtin_fmaf((float)q[1], ds, c), __builtin_fmaf((float)p[0], ds, c),
+                __builtin_fmaf((float)p[1], ds, c), r[t], r[t + 1]);
     }
-    return __builtin_bit_cast(h8_t, r);
+    return __builtin_bit_cast(h8_t, u4_t{r[0], r[1], r[2], r[3]});
   }
   // Scale of MFMA u: byte u / 2 of the lane's scale dword (stored sc + 128);
   // of MFMA 4 + u: byte 2 + u / 2.  d * sc = fma(sc + 128, d, -128 d), exact.
@@ -2864,13 +2867,14 @@ struct TgIQ4XS {
     const uint32_t vlo = FmtIQ4XS::lookup(wq), vhi = FmtIQ4XS::lookup(wq >> 4);
     const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, vlo, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, vlo, 0x04030402u),
                            __builtin_amdgcn_perm(0x64646464u, vhi, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, vhi, 0x04030402u)};
-    u4_t r;
+    uint32_t r[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const h2_t v = as_h2(p[t]);
-      r[t] = pack_h2(__builtin_fmaf((float)v[0], dl, cl), __builtin_fmaf((float)v[1], dl, cl));
+    for (int t = 0; t < 4; t += 2) {
+      const h2_t v = as_h2(p[t]), w = as_h2(p[t + 1]);
+      pack_h2x2(__builtin_fmaf((float)v[0], dl, cl), __builtin_fmaf((float)v[1], dl, cl), __builtin_fmaf((float)w[0], dl, cl),
+                __builtin_fmaf((float)w[1], dl, cl), r[t], r[t + 1]);
     }
-    return __builtin_bit_cast(h8_t, r);
+    return __builtin_bit_cast(h8_t, u4_t{r[0], r[1], r[2], r[3]});
   }
   static __device__ __forceinline__ void dequant(const K& k, const W& w, int, h8_t& blo, h8_t& bhi) {
     blo = frag(w.lo, k.dl, k.cl);
@@ -2916,15 +2920,15 @@ struct TgQ4K {
   }
   static __device__ __forceinline__ void dequant(const K& k, const W& w, int, h8_t& blo, h8_t& bhi) {
     const uint32_t lw[4] = {w.q.x, w.q.x >> 8, w.q.y, w.q.y >> 8};
-    u4_t lo, hi;
+    uint32_t lo[4], hi[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const h2_t ql = as_h2(lw[t] & 0x000F000Fu), qh = as_h2(lw[t] & 0x00F000F0u);
-      lo[t] = pack_h2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl));
-      hi[t] = pack_h2(__builtin_fmaf((float)qh[0], k.dh, k.ch), __builtin_fmaf((float)qh[1], k.dh, k.ch));
+      pack_h2x2(__builtin_fmaf((float)ql[0], k.dl, k.cl), __builtin_fmaf((float)ql[1], k.dl, k.cl), __builtin_fmaf((float)qh[0], k.dh, k.ch),
+                __builtin_fmaf((float)qh[1], k.dh, k.ch), lo[t], hi[t]);
     }
-    blo = __builtin_bit_cast(h8_t, lo);
-    bhi = __builtin_bit_cast(h8_t, hi);
+    blo = __builtin_bit_cast(h8_t, u4_t{lo[0], lo[1], lo[2], lo[3]});
+    bhi = __builtin_bit_cast(h8_t, u4_t{hi[0], hi[1], hi[2], hi[3]});
   }
 };
 
@@ -2994,22 +2998,32 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
   uint8_t* const bring = lds + AS * kG2ASlot + wave * (2 * CT * TB);
   const uint32_t bring0 = lds_addr(bring);
   const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
-  const _Float16* const xh = a.xh;
-
-  auto issue_a = [&](int t, int i) {
-    const int tc = t < steps ? t : steps - 1;
-    const int b = tc >> 2, u = tc & 3;
-    const int f = 4 * wave + i;
-    const _Float16* src = xh + ((((size_t)by * nb + b) * 4 + u) * 16 + f) * 512;
-    const uint32_t l = __builtin_amdgcn_readfirstlane(aring + (uint32_t)(t % AS) * kG2ASlot + (uint32_t)f * 1024);
-    lds_dma16<0>(uniform_ptr(reinterpret_cast<const uint8_t*>(src)), voff16, l);
+  // A: this wave's 4 fragments of u-step t are 4 consecutive KB at
+  // xa + 16 KB * t of the staging and at 4 KB * wave of ring slot t % AS;
+  // fragment i is the instruction offset 1 KB * i.  The ring addresses of
+  // the slot read (ar) and written (aw) roll from step to step.
+  const uint8_t* const xa = uniform_ptr(reinterpret_cast<const uint8_t*>(a.xh) + ((size_t)by * nb * 64 + 4 * (size_t)wave) * 1024);
+  const uint32_t aend = aring + AS * kG2ASlot;
+  auto frag_a = [&](const uint8_t* src, uint32_t l, int i) {
+    if (i == 0)
+      lds_dma16<0>(src, voff16, l);
+    else if (i == 1)
+      lds_dma16<1024>(src, voff16, l);
+    else if (i == 2)
+      lds_dma16<2048>(src, voff16, l);
+    else
+      lds_dma16<3072>(src, voff16, l);
   };
+  // B: column c's tile-blocks start at wcol[c] (column tiles past n read the
+  // last one); block blk goes to ring half blk & 1.
+  const uint8_t* wcol[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+    wcol[c] = uniform_ptr(a.w + (size_t)(ct0 + c < ntiles ? ct0 + c : ntiles - 1) * nb * TB);
   auto issue_b = [&](int blk, int c) {
     const int bc = blk < nb ? blk : nb - 1;
-    const int ct = ct0 + c < ntiles ? ct0 + c : ntiles - 1;
-    const uint8_t* src = uniform_ptr(a.w + ((size_t)ct * nb + bc) * TB);
     const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * CT + c) * TB);
-    P::issue(src, voff16, voff4, l, lane);
+    P::issue(wcol[c] + (size_t)bc * TB, voff16, voff4, l, lane);
   };
 
   f4_t acc[8][CT];
@@ -3025,10 +3039,13 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
   for (int c = 0; c < CT; ++c)
     issue_b(0, c);
 #pragma unroll
-  for (int t = 0; t < AD; ++t)
+  for (int t = 0; t < AD; ++t) {
+    const uint8_t* src = xa + (size_t)(t < steps ? t : steps - 1) * 16384;
+    const uint32_t l = aring + (uint32_t)t * kG2ASlot + 4096u * (uint32_t)wave;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      issue_a(t, i);
+      frag_a(src, l, i);
+  }
   vm_wait<4 * (AD - 1)>();  // B(0) and A(0)
   typename P::K kk[CT];
   h8_t bclo[CT], bchi[CT];
@@ -3049,10 +3066,13 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
     }
     P::words(wl, bring + (CT - 1) * TB, 0, lane);
   }
+  uint32_t ar = aring, aw = aring + AD * kG2ASlot + 4096u * (uint32_t)wave;
   for (int blk = 0; blk < nb; ++blk) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * blk + u;
+      const int ta = t + AD < steps ? t + AD : steps - 1;
+      const uint8_t* const asrc = xa + (size_t)ta * 16384;
       if (u == 0)
         vm_wait<tg_wait(0, AD, CT, NL)>();
       else if (u == 1)
@@ -3064,7 +3084,7 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
       __syncthreads();  // A(t) of every wave landed; u-step t - 1 fully read
       __builtin_amdgcn_sched_barrier(0);
       const int bn = u == 3 ? blk + 1 : blk, un = (u + 1) & 3;
-      const uint8_t* aslot = lds + (size_t)(t % AS) * kG2ASlot;
+      const uint8_t* aslot = lds + (ar - aring);
       h8_t af[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -3097,11 +3117,13 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
           P::dequant(kk[c - 1], wv[c - 1], un, bclo[c - 1], bchi[c - 1]);
 #pragma unroll
         for (int i = 4 * c / CT; i < 4 * (c + 1) / CT; ++i)
-          issue_a(t + AD, i);
+          frag_a(asrc, aw, i);
         if (u == 0)
           issue_b(blk + 1, c);
       }
       wl = wv[CT - 1];
+      ar = ar + kG2ASlot == aend ? aring : ar + kG2ASlot;
+      aw = aw + kG2ASlot >= aend ? aw + kG2ASlot - AS * kG2ASlot : aw + kG2ASlot;
       __builtin_amdgcn_sched_group_barrier(0x100, 64, 0);
 #pragma unroll
       for (int i = 0; i < 16 * CT; ++i) {
