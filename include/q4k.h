@@ -135,10 +135,11 @@ int q4k_linear_norm(void* stream, q4k_weight* w, const float* norm_w, float eps,
  * No counterpart in the reference, whose kernels allocate nothing; here the
  * staging, split-K partials and counters of q4k_linear normally live in a
  * workspace that grows on demand.  Same arguments, selection, kernels and
- * results as q4k_linear, but the workspace is a fixed 88 MiB device array
+ * results as q4k_linear, but the workspace is a fixed 120 MiB device array
  * that each GPU the library runs on holds until the process ends: 2 MiB of
- * decode pack (m <= 8, k <= 61440), 32 MiB of split-K partials (the decode
- * split-K GEMV and the prefill GEMM's two K-halves), 4096 split-K counters, 65536 row scales, and about 54 MiB of staged activations (e.g.
+ * decode pack (m <= 8, k <= 61440), 64 MiB of split-K partials (the decode
+ * split-K GEMV and the prefill GEMM's two K-segments), 4096 split-K
+ * counters, 65536 row scales, and about 54 MiB of staged activations (e.g.
  * m * k <= 28.1 million for prefill, rows padded to 128).  A call needing
  * more fails with Q4K_ESHAPE and a message naming the buffer.  Every weight
  * type is served, prefill included.  Calls allocate nothing (no hipMalloc,

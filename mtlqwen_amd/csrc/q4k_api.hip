@@ -410,13 +410,13 @@ int ensure_splitk_workspace(hipStream_t stream, Workspace& ws, int device, size_
   return Q4K_OK;
 }
 
-// The pipelined GEMM of a shape with few tiles for the CUs runs two K-halves
-// per tile (gemm2_split): their accumulators and arrival counters live in
-// the split-K workspace.
+// The pipelined GEMM of a shape with fewer tiles than CUs runs two
+// K-segments per tile (gemm2_split_b): their accumulators and arrival
+// counters live in the split-K workspace.
 int device_cus(int device);
 
 int gemm2_split_buffers(hipStream_t stream, Workspace& ws, int device, GemmArgs& a, bool gated) {
-  if (!gemm2_split(a.m, a.n, a.nb, device_cus(device)))
+  if (!gemm2_split_b(a.m, a.n, a.nb, device_cus(device)))
     return Q4K_OK;
   size_t part_floats = 0, counters = 0;
   gemm2_split_workspace(a.m, a.n, gated, &part_floats, &counters);
@@ -996,13 +996,13 @@ int check_linear(const q4k_weight* w, const void* x, const void* y, const void* 
 // address of each GPU's copy comes from hipGetSymbolAddress, taken once per
 // device at that device's first call (with the device current), and only
 // that address is used (kernel arguments, fills).
-constexpr size_t kScratchBytes = 88ull << 20;
+constexpr size_t kScratchBytes = 120ull << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 // Fixed regions of the scratch: decode pack, split-K partials and counters,
 // row scales; the rest holds the staged activations.
 constexpr size_t kScrPackBytes = 2ull << 20;
-constexpr size_t kScrPartBytes = 32ull << 20;  // the largest two-K-halves GEMM (128 tiles)
+constexpr size_t kScrPartBytes = 64ull << 20;  // two K-segments of a GEMM of up to 256 tiles
 constexpr size_t kScrCounterBytes = 16ull << 10;
 constexpr size_t kScrScaleBytes = 256ull << 10;
 constexpr size_t kScrXBytes = kScratchBytes - kScrPackBytes - kScrPartBytes - kScrCounterBytes - kScrScaleBytes;

@@ -337,10 +337,15 @@ struct GemmArgs {
   void* y;
   const void* aux;
   int m, n, k, nb, post;
-  // K-halves (gemm2_split): the halves' accumulators and per-tile arrival
-  // counters (zero before the launch; every launch leaves them zero).
+  // K-split (gemm2_split_plan): the two segments' accumulators and per-tile
+  // arrival counters (zero before the launch; every launch leaves them
+  // zero).  Segment 0 of a tile is blocks [0, split_b), segment 1 blocks
+  // [split_b, nb).  split_q > 0: segment 0 of tile t runs on workgroup t and
+  // the segments 1 split_q per workgroup on the workgroups past the tiles;
+  // split_q == 0: the 2 x tiles segments are dealt round robin.
   float* part = nullptr;
   int* counters = nullptr;
+  int split_b = 0, split_q = 0;
 };
 
 struct GatherIndex {
@@ -432,7 +437,7 @@ bool gemm2_supported(int m, int n);
 int gemm2_rows(int m);
 // Whether the pipelined GEMM (plain and gated alike) of this shape runs as two
 // K-halves per tile (few tiles for the CUs), and the workspace it then needs.
-bool gemm2_split(int m, int n, int nb, int cus);
+int gemm2_split_b(int m, int n, int nb, int cus);
 void gemm2_split_workspace(int m, int n, bool gated, size_t* part_floats, size_t* counters);
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus);
 // Gate and up projections of one prefill MLP in one launch (both Q4_K, the

@@ -1814,24 +1814,32 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
       asm volatile("" : "+a"(acc[rt][c]));
 
   if constexpr (SPLIT) {
-    // Two K-halves per tile (items 2 tile, 2 tile + 1): each stores its
-    // accumulators (written through to memory), and the second to arrive
-    // adds the other's and runs the epilogue.  fp32 addition commutes, so
-    // the result does not depend on which half arrives last.
+    // Two K-segments per tile (items 2 tile, 2 tile + 1).  A segment that
+    // finds the other already arrived (its accumulators in memory and the
+    // counter at 1) stores nothing; otherwise it stores its accumulators
+    // (written through to memory), counts its arrival, and the second to
+    // arrive adds the other's and runs the epilogue.  fp32 addition
+    // commutes, so the result does not depend on which segment is last.
     constexpr size_t kWaveFloats = 32 * 64 * 4;
-    float* const mine = a.part + ((size_t)item * 4 + wave) * kWaveFloats + 4 * lane;
-#pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        store_coherent4(mine + (rt * 4 + c) * 256, acc[rt][c]);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    int* const ctr = &a.counters[item >> 1];
     if (tid == 0)
-      *s_last = count_arrival(&a.counters[item >> 1]) == 1;
+      *s_last = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != 0;
     __syncthreads();
-    if (!*s_last)
-      return;
+    if (!*s_last) {
+      float* const mine = a.part + ((size_t)item * 4 + wave) * kWaveFloats + 4 * lane;
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          store_coherent4(mine + (rt * 4 + c) * 256, acc[rt][c]);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0)
+        *s_last = count_arrival(ctr) == 1;
+      __syncthreads();
+      if (!*s_last)
+        return;
+    }
     const float* const other = a.part + ((size_t)(item ^ 1) * 4 + wave) * kWaveFloats + 4 * lane;
     f4_t pv[8][4];
 #pragma unroll
@@ -1848,7 +1856,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
         acc[rt][c] += pv[rt][c];
       }
     if (tid == 0)
-      reset_counter(&a.counters[item >> 1]);  // ready for the next launch
+      reset_counter(ctr);  // ready for the next launch
   }
 
   // One straight-line epilogue per (post code, tile inside m or not).
@@ -1870,20 +1878,28 @@ __device__ __forceinline__ void gemm2_tile(const GemmArgs& a, uint8_t* lds, int 
 // Persistent launch: workgroup b takes its tiles in the order of the tile
 // map.  Consecutive tiles of a workgroup reuse its LDS rings; a barrier
 // separates the last reads of one tile from the first loads of the next.
-// SPLIT: items 2 t and 2 t + 1 are the two K-halves of tile t (plain tile
-// order), taken in turn by the workgroups.
+// SPLIT: items 2 t and 2 t + 1 are the two K-segments of tile t (plain tile
+// order): with a.split_q > 0 workgroup t < tiles takes segment 0 of tile t
+// and workgroup tiles + r segments 1 of tiles r, r + R, ... (R workgroups
+// past the tiles), else the workgroups take the items in turn.
 template <typename OutT, bool GATED, bool SPLIT = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void q4k_gemm2_kernel(GemmArgs a, TileMap map) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kG2AS * kG2ASlot + 4 * kG2BWave];
   __shared__ int s_last;
   if constexpr (SPLIT) {
-    const int half = a.nb >> 1;
-    for (int it = (int)blockIdx.x, i = 0; it < 2 * map.tiles; it += (int)gridDim.x, ++i) {
-      if (i > 0)
+    // This workgroup's items: first, first + step, ... below 2 x tiles (one
+    // call site of the tile body, which is inlined).
+    const int b = a.split_b, tiles = map.tiles, g = (int)blockIdx.x;
+    int first = g, step = (int)gridDim.x;
+    if (a.split_q > 0) {
+      first = g < tiles ? 2 * g : 2 * (g - tiles) + 1;
+      step = g < tiles ? 2 * tiles : 2 * ((int)gridDim.x - tiles);
+    }
+    for (int it = first; it < 2 * tiles; it += step) {
+      if (it != first)
         __syncthreads();
       const int tile = it >> 1, ks = it & 1;
-      gemm2_tile<OutT, GATED, true>(a, lds, tile % map.tiles_x, tile / map.tiles_x, a.n / 16, ks ? half : 0, ks ? a.nb - half : half, it,
-                                    &s_last);
+      gemm2_tile<OutT, GATED, true>(a, lds, tile % map.tiles_x, tile / map.tiles_x, a.n / 16, ks ? b : 0, ks ? a.nb - b : b, it, &s_last);
     }
   } else {
     const int count = tile_count(map);
@@ -2939,6 +2955,14 @@ struct Narrow : P {
   static constexpr int kCT = 2, kAS = 5;
 };
 
+// Three column tiles per wave (192 columns per workgroup): the B ring is
+// three quarters of the 4-tile form's, which leaves LDS for a deeper A ring
+// (Q6_K: 5 slots instead of 3) or more MFMAs per A fragment read (Q8_0).
+template <class P, int AS>
+struct Mid : P {
+  static constexpr int kCT = 3, kAS = AS;
+};
+
 // Load accounting of the typed GEMM.  A wave issues per u-step its 4 A
 // fragments of A(t + kAS - 1) spread over its kCT column groups, each group's
 // share followed, at u = 0, by the kNL loads of that column's tile-block of
@@ -3575,16 +3599,42 @@ bool gemm2_narrow(int tiles256, int tiles128, int cus) {
   return r2 * kGemmNarrowTileTime < r4 * 10;
 }
 
-// Two K-halves per tile when the tiles fill at most half the CUs and K is
-// long (K >= 8192: the halves' write-through exchange, about 20 us per
-// launch, is then smaller than what the second half of the CUs saves; at
-// M = 821 it takes the K = 12288 down projection from 119.7 us on the
-// 128-column template to 107.2 us, while the K = 4096 O projection went
-// from 48.6 to 54.4 us and keeps the template).
-bool gemm2_split(int m, int n, int nb, int cus) {
+// Segments 1 per workgroup on the CUs that `tiles` workgroups leave free.
+static int split_segments_per_wg(int tiles, int cus) {
+  const int free = cus - tiles;
+  return (tiles + free - 1) / free;
+}
+
+// K-split of the pipelined GEMM when its 256-column tiles leave CUs idle:
+// segment 0 of each tile (blocks [0, b)) on a workgroup of its own, segments
+// 1 (the other nb - b blocks) q to a workgroup on the CUs the tiles leave
+// free, q = tiles / free CUs rounded up.
+//  - q = 1 (the tiles fill at most half the CUs) and K >= 8192: two halves
+//    (b = nb / 2).  At M = 821 the K = 12288 down projection (112 tiles)
+//    measured 113.6 us against 123.9 on the 128-column template; longer
+//    segments 0 (b = 27, 30: 119.0, 128.0 us) do not pay for the exchange
+//    they hide.  At K = 4096 the 112-tile O projection measured 56.0 us split
+//    against 50.4 on the template, which it keeps.
+//  - q >= 2 and K >= 4096: b = q nb / (q + 1) rounded up, so that the q
+//    segments 1 of a workgroup take no longer than one segment 0.  The
+//    N = 6144 projection's 168 tiles at M = 821 (b = 11) measured 58.9-60.9
+//    us for b = 10..13 against 64.3 unsplit: the segments 0 run at 5.4 us
+//    per block against 4.0 unsplit, so that 252 workgroups gain only 8 %
+//    over 168.
+// Returns b, or 0 for no split.  Q4K_GEMM2_SPLIT=0 turns the split off;
+// Q4K_GEMM2_SPLIT_B forces b (for every shape with tiles < CUs and b < nb).
+int gemm2_split_b(int m, int n, int nb, int cus) {
   static const int on = env_int("Q4K_GEMM2_SPLIT", 1);
+  static const int b_env = env_int("Q4K_GEMM2_SPLIT_B", 0);
   const int tiles = ((n + kG2N - 1) / kG2N) * ((m + kG2M - 1) / kG2M);
-  return on && nb >= 32 && 2 * tiles <= cus;
+  if (!on || tiles >= cus)
+    return 0;
+  if (b_env > 0)
+    return b_env < nb ? b_env : 0;
+  const int q = split_segments_per_wg(tiles, cus);
+  if (q == 1)
+    return nb >= 32 ? nb / 2 : 0;
+  return nb >= 16 ? (q * nb + q) / (q + 1) : 0;
 }
 
 void gemm2_split_workspace(int m, int n, bool gated, size_t* part_floats, size_t* counters) {
@@ -3594,9 +3644,15 @@ void gemm2_split_workspace(int m, int n, bool gated, size_t* part_floats, size_t
 }
 
 namespace {
+// Segments 0 one per workgroup and segments 1 q per workgroup past them
+// when the launch's own tiles leave CUs free, else both dealt round robin
+// (the gated GEMM, twice the plain GEMM's tiles, takes the plain GEMM's b).
 template <bool GATED>
-hipError_t gemm2_split_launch(hipStream_t s, const GemmArgs& a, int dtype, int tiles_x, int tiles_y, int cus) {
-  const int tiles = tiles_x * tiles_y, grid = 2 * tiles < cus ? 2 * tiles : cus;
+hipError_t gemm2_split_launch(hipStream_t s, GemmArgs a, int dtype, int tiles_x, int tiles_y, int cus, int b) {
+  const int tiles = tiles_x * tiles_y;
+  a.split_b = b;
+  a.split_q = tiles < cus ? split_segments_per_wg(tiles, cus) : 0;
+  const int grid = a.split_q > 0 ? tiles + (tiles + a.split_q - 1) / a.split_q : (2 * tiles < cus ? 2 * tiles : cus);
   const TileMap map{tiles_x, tiles, 0, 0, 0};
   if (dtype == kF32)
     (void)dispatch(q4k_gemm2_kernel<float, GATED, true>, dim3((unsigned)grid), dim3(256), s, a, map);
@@ -3610,10 +3666,10 @@ hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   if (!gemm2_supported(a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
   const int tiles_x = (a.n + kG2N - 1) / kG2N, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
-  if (gemm2_split(a.m, a.n, a.nb, cus)) {
+  if (const int b = gemm2_split_b(a.m, a.n, a.nb, cus)) {
     if (!a.part || !a.counters)
       return hipErrorInvalidValue;
-    return gemm2_split_launch<false>(s, a, dtype, tiles_x, tiles_y, cus);
+    return gemm2_split_launch<false>(s, a, dtype, tiles_x, tiles_y, cus, b);
   }
   if (gemm2_narrow(tiles, ((a.n / 16 + 7) / 8) * tiles_y, cus))
     return typed_gemm_launch<TgQ4K>(s, a, dtype, cus);
@@ -3633,12 +3689,12 @@ hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int c
     return hipErrorInvalidValue;
   // 128 output columns (256 B columns: gate and up) per tile.
   const int tiles_x = (a.n / 16 + 7) / 8, tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
-  // K-halves exactly when the plain GEMM of this shape takes them, so that
-  // the gated launch stays bit-identical to the gate-then-up calls.
-  if (gemm2_split(a.m, a.n, a.nb, cus)) {
+  // K-segments exactly when, and where, the plain GEMM of this shape splits,
+  // so that the gated launch stays bit-identical to the gate-then-up calls.
+  if (const int b = gemm2_split_b(a.m, a.n, a.nb, cus)) {
     if (!a.part || !a.counters)
       return hipErrorInvalidValue;
-    return gemm2_split_launch<true>(s, a, dtype, tiles_x, tiles_y, cus);
+    return gemm2_split_launch<true>(s, a, dtype, tiles_x, tiles_y, cus, b);
   }
   const int grid = tiles > cus ? cus : tiles;
   const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
@@ -3804,6 +3860,16 @@ bool typed_gemm_supported(uint32_t type, int m, int n) {
   return served && m > 0 && n > 0 && n % 16 == 0;
 }
 
+// Rounds of workgroups of the 192-column Q8_0 tiling against the 128-column
+// one, each weighted by its columns per tile.
+static bool q8_mid(int ntiles, int tiles_y, int cus) {
+  static const int forced = env_int("Q4K_TYPED_MID", -1);
+  if (forced >= 0)
+    return forced == 1;
+  const int r3 = ((ntiles + 11) / 12 * tiles_y + cus - 1) / cus, r2 = ((ntiles + 7) / 8 * tiles_y + cus - 1) / cus;
+  return 3 * r3 <= 2 * r2;
+}
+
 hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, int dtype, int cus) {
   if (!typed_gemm_supported(type, a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
@@ -3815,7 +3881,15 @@ hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, in
     case kTypeQ6_K:
       return narrow ? typed_gemm_launch<Narrow<TgQ6K>>(s, a, dtype, cus) : typed_gemm_launch<TgQ6K>(s, a, dtype, cus);
     case kTypeQ8_0:
-      return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);  // two column tiles per wave already
+      // Two column tiles per wave (its 4-tile B ring does not fit beside an
+      // A ring), or three where the 192-column grid takes no more time in
+      // rounds: three tiles read each A fragment for half as many MFMAs
+      // again (at M = 2048 the N = 12288 GEMM measured 211 instead of 243
+      // us; Q6_K and Q5_K measured slower with three, also with a 5-slot A
+      // ring).  Q4K_TYPED_MID: -1 auto, 0 never, 1 always.
+      if (q8_mid(ntiles, tiles_y, cus))
+        return typed_gemm_launch<Mid<TgQ8_0, 3>>(s, a, dtype, cus);
+      return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);
     default:
       return narrow ? typed_gemm_launch<Narrow<TgIQ4XS>>(s, a, dtype, cus) : typed_gemm_launch<TgIQ4XS>(s, a, dtype, cus);
   }

@@ -19,7 +19,7 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 
 import mtlqwen_amd as q4k  # noqa: E402
-from q4k_ref import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, Oracle, gated_prefill_arithmetic, make_weight, make_x, row_rel_err  # noqa: E402
+from q4k_ref import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, Oracle, gated_prefill_arithmetic, make_weight, make_x, row_rel_err  # noqa: E402
 
 TOL = 1e-3
 dev = torch.device("cuda:0")
@@ -143,13 +143,23 @@ def case_gemv_shape():
 
 def case_gemm():
     # Prefill GEMMs under the switch: plain (few tiles, and more tiles than
-    # CUs), long K with few tiles (two K-halves by default), gated, and the
+    # CUs), long K with few tiles (two K-segments by default; a forced split
+    # point gives segments of 3 and nb - 3 blocks here), gated, and the
     # typed GEMM (Q6_K).
     check_linear(200, 1024, 4096, post=1, seed=60)
     check_linear(2048, 6144, 1024, post=1, seed=61)
     check_linear(200, 4096, 12288, seed=62)
     check_gate_up(160, 1024, 2048, seed=63)
     check_linear(64, 1024, 4096, t=TYPE_Q6_K, seed=64)
+
+
+def case_typed_gemm():
+    # Q8_0 prefill GEMMs with two or three column tiles per wave: ragged
+    # rows, a last 192-column block with one live column tile (n = 592 is 37
+    # column tiles), with and without the residual epilogue.
+    check_linear(300, 592, 1024, t=TYPE_Q8_0, post=1, seed=90)
+    check_linear(129, 3072, 2048, t=TYPE_Q8_0, seed=91)
+    check_linear(200, 1536, 512, t=TYPE_Q8_0, post=1, seed=92)
 
 
 def case_typed_gemv():
@@ -172,6 +182,7 @@ CASES = {
     "gemv_generic": case_gemv_generic,
     "gemv_shape": case_gemv_shape,
     "gemm": case_gemm,
+    "typed_gemm": case_typed_gemm,
     "typed_gemv": case_typed_gemv,
     "q4k_persistent_off": case_q4k_persistent_off,
 }
