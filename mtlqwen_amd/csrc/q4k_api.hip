@@ -710,6 +710,15 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     Q4K_TRY_HIP(launch_stage_x(stream, x, (int)dtype, ws.x, xs, ws.scale, (int)m, (int)w->k, mode, norm_w, eps), "stage_x launch");
   }
   if (gemv) {
+    const RowsPlan rows_plan = gemv_rows_plan(rows, (int)(w->k / 256), (int)w->n, wu != nullptr, device_cus(w->device));
+    if (rows_plan.slices > 1) {
+      const size_t groups = (size_t)(w->n / (16 * rows_plan.tiles));
+      rc = ensure_splitk_workspace(stream, ws, w->device, gemv_rows_part_floats(rows_plan, (int)w->n), groups);
+      if (rc)
+        return rc;
+      if (ws.fixed)  // the scratch's counters start at zero for this launch (a fill kernel: capture-safe)
+        Q4K_TRY_HIP(launch_fill_u32(stream, reinterpret_cast<uint32_t*>(ws.counters), 0u, (uint32_t)groups), "counter fill launch");
+    }
     GemvArgs a;
     a.w = w->data;
     a.wu = wu ? wu->data : w->data;
@@ -725,10 +734,13 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     a.post = (int)post;
     a.rows = rows;
     a.split = split ? 1 : 0;
+    if (rows_plan.slices > 1) {
+      a.part = ws.part;
+      a.counters = ws.counters;
+    }
     LaunchTimer timer(stream, wu ? Q4K_KERNEL_GEMV_GATED : Q4K_KERNEL_GEMV);
-    const int rows_tiles = gemv_rows_tiles(rows, a.nb, a.n, wu != nullptr, device_cus(w->device));
-    if (rows_tiles > 0)
-      Q4K_TRY_HIP(launch_gemv_rows(stream, a, (int)dtype, rows_tiles, wu != nullptr), "gemv rows launch");
+    if (rows_plan.tiles > 0)
+      Q4K_TRY_HIP(launch_gemv_rows(stream, a, (int)dtype, rows_plan, wu != nullptr), "gemv rows launch");
     else
       Q4K_TRY_HIP(launch_gemv(stream, a, (int)dtype, gemv_shape(rows, (int)w->n, a.nb, wu != nullptr, device_cus(w->device)), wu != nullptr),
                   "gemv launch");

@@ -327,6 +327,10 @@ struct GemvArgs {
   // x * rsqrt(sum(x^2) / k + eps) * norm_w (native_ops.metal:6-40).
   const float* norm_w = nullptr;
   float eps = 0.0f;
+  // Rows GEMV in K-slices: the slices' sums and per-group arrival counters
+  // (zero before the launch; every launch leaves them zero).
+  float* part = nullptr;
+  int* counters = nullptr;
 };
 
 struct GemmArgs {
@@ -409,9 +413,15 @@ bool gemv_gate_up_supported(int m, int nb, int n);
 hipError_t launch_gemv_gate_up(hipStream_t s, const GemvArgs& a, int dtype, int cus);
 // GEMV over staged x of 17..48 fragment rows: T column tiles of NM matrices
 // per workgroup, 8 waves splitting K (K = 2048 .. 12288), each block of x
-// read once per wave.  gemv_rows_tiles returns T (0: not this kernel).
-int gemv_rows_tiles(int rows, int nb, int n, bool gated, int cus);
-hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, int tiles, bool gated);
+// read once per wave.  gemv_rows_plan returns T (0: not this kernel) and the
+// K-slices (1, or 3 for K = 12288: partials and counters in the split-K
+// workspace, gemv_rows_part_floats floats and n / (16 T) counters).
+struct RowsPlan {
+  int tiles = 0, slices = 1;
+};
+RowsPlan gemv_rows_plan(int rows, int nb, int n, bool gated, int cus);
+size_t gemv_rows_part_floats(const RowsPlan& p, int n);
+hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, const RowsPlan& p, bool gated);
 // The same for gate and up weights of one other type with a fused decode
 // kernel in the reference (Q5_K, IQ4_XS).
 bool typed_gate_up_supported(uint32_t type, int m, int nb, int n);

@@ -965,15 +965,23 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_gate_up_kernel(GemvArgs a) {
 // GEMV; a block's fragments replace the previous block's after its units
 // (one L2 round trip per block and wave, which the SIMD's other wave
 // covers).  The 8 waves' partial sums meet in LDS in wave order.
+// KS > 1 K-slices: workgroup b takes slice b % KS (blocks 8 BPW of them) of
+// column group b / KS, so that KS times fewer column groups, each of KS
+// times more column tiles, read all of x; each slice's workgroup writes its
+// sums (written through to memory) and the last of the KS to arrive (a
+// per-group counter, reset by it) adds them in slice order and runs the
+// epilogue.  No workgroup waits for another.
 // ----------------------------------------------------------------------------
-template <int NM, int T, int RT, int BPW, typename OutT>
+template <int NM, int T, int RT, int BPW, typename OutT, int KS = 1>
 __global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
   constexpr int W = 8, MT = NM * T, U = BPW * MT, ROWS = 16 * RT, DQ = 2;
   __shared__ float red[W][MT][ROWS][16];
+  __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int item = blockIdx.x, nb = a.nb, bw = BPW * ((wave + item) % W);
+  const int item = blockIdx.x / KS, ks = blockIdx.x % KS, nb = a.nb;
+  const int bw = ks * (W * BPW) + BPW * ((wave + item) % W);
   const size_t tile_bytes = (size_t)nb * kTileBlockBytes;
 
   u4_t hdr[U], q0[U], q1[U];
@@ -1061,22 +1069,81 @@ __global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   constexpr int EPI = 16 * T;
-  for (int o = tid; o < a.m * EPI; o += 64 * W) {
+  // This workgroup's sum of output o (row o / EPI, column o % EPI) of
+  // matrix mi: the waves in order, then (split rows) the low parts.
+  auto wave_sum = [&](int o, int mi) {
+    const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      v += red[w][mi * T + t][row][cc];
+    if (a.split) {
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        v += red[w][mi * T + t][a.m + row][cc];
+    }
+    return v;
+  };
+  // K-slices: outputs of slice k2 of matrix mi at part + ((item KS + k2) NM
+  // + mi) ROWS EPI + o.  Per thread at most PER outputs (o = tid + 512 r).
+  constexpr int PER = (ROWS * EPI + 64 * W - 1) / (64 * W);
+  float sl[PER][NM];
+  if constexpr (KS > 1) {
+    float* const mine = a.part + ((size_t)item * KS + ks) * NM * ROWS * EPI;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int o = tid + r * 64 * W;
+      if (o < a.m * EPI) {
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi)
+          store_coherent(mine + mi * ROWS * EPI + o, wave_sum(o, mi));
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+      s_last = count_arrival(&a.counters[item]) == KS - 1;
+    __syncthreads();
+    if (!s_last)
+      return;
+    // Every slice's sums, loaded together, then added in slice order.
+    float pv[PER][NM][KS];
+    const float* const grp = a.part + (size_t)item * KS * NM * ROWS * EPI;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int o0 = tid + r * 64 * W, o = o0 < a.m * EPI ? o0 : 0;
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+        for (int k2 = 0; k2 < KS; ++k2)
+          pv[r][mi][k2] = load_coherent(grp + (k2 * NM + mi) * ROWS * EPI + o);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < PER; ++r)
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < KS; ++k2) {
+          hold(pv[r][mi][k2]);
+          v += pv[r][mi][k2];
+        }
+        sl[r][mi] = v;
+      }
+    if (tid == 0)
+      reset_counter(&a.counters[item]);  // ready for the next launch
+  }
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int o = tid + r * 64 * W;
+    if (o >= a.m * EPI)
+      break;
     const int row = o / EPI, c = o % EPI, t = c >> 4, cc = c & 15;
     float s[NM];
 #pragma unroll
-    for (int mi = 0; mi < NM; ++mi) {
-      float v = 0.0f;
-#pragma unroll
-      for (int w = 0; w < W; ++w)
-        v += red[w][mi * T + t][row][cc];
-      if (a.split) {
-#pragma unroll
-        for (int w = 0; w < W; ++w)
-          v += red[w][mi * T + t][a.m + row][cc];
-      }
-      s[mi] = v * a.rowscale[row];
-    }
+    for (int mi = 0; mi < NM; ++mi)
+      s[mi] = (KS > 1 ? sl[r][mi] : wave_sum(o, mi)) * a.rowscale[row];
     const size_t off = (size_t)row * a.n + ((size_t)item * T + t) * 16 + cc;
     float out;
     if (NM == 2) {
@@ -3337,34 +3404,57 @@ hipError_t launch_gemv_splitk(hipStream_t s, const GemvArgs& a, int dtype, const
 // 1 (M = 40, N = 4096: 19.1 against 20.5 us).  Plain projections at K = 4096
 // stay on the staged GEMV, which already splits K over 8 waves with two
 // column tiles where that fills the CUs (measured as fast or faster).
-int gemv_rows_tiles(int rows, int nb, int n, bool gated, int cus) {
+RowsPlan gemv_rows_plan(int rows, int nb, int n, bool gated, int cus) {
   static const int forced = env_int("Q4K_GEMV_ROWS", -1);  // -1 auto, 0 off, 1..3 column tiles
+  static const int slices_env = env_int("Q4K_GEMV_ROWS_SLICES", -1);  // -1 auto, 1 one slice, 3 three
+  RowsPlan p;
   if (forced == 0 || rows <= 16 || rows > 16 * kGemvMaxRowTiles || n % 16 != 0)
-    return 0;
+    return p;
   const int ctiles = n / 16;
   if (gated) {
     if (nb != 16)
-      return 0;
+      return p;
     const int t = forced > 0 ? forced : 3;
-    return ctiles % t == 0 && (forced > 0 || ctiles / t >= cus) ? t : 0;
+    if (ctiles % t == 0 && (forced > 0 || ctiles / t >= cus))
+      p.tiles = t;
+    return p;
   }
   if (nb != 48 && !(forced > 0 && nb == 16))
-    return 0;
-  if (forced > 0)
-    return ctiles % forced == 0 ? forced : 0;
+    return p;
+  // K = 12288: three K-slices of 4 column tiles when the column groups fill
+  // the CUs in one round -- each CU then reads a third of x for 4 column
+  // tiles instead of all of it for one (M = 40, N = 4096: 64 groups x 3).
+  const bool slices_ok = nb == 48 && forced <= 0 && ctiles % 4 == 0 && (ctiles / 4) * 3 <= cus;
+  if (slices_env == 3 ? nb == 48 && ctiles % 4 == 0 : slices_env != 1 && slices_ok) {
+    p.tiles = 4;
+    p.slices = 3;
+    return p;
+  }
+  if (forced > 0) {
+    if (ctiles % forced == 0)
+      p.tiles = forced;
+    return p;
+  }
+  p.tiles = 1;
   for (int t = 3; t >= 1; --t)
-    if (ctiles % t == 0 && ctiles / t >= cus)
-      return t;
-  return 1;
+    if (ctiles % t == 0 && ctiles / t >= cus) {
+      p.tiles = t;
+      break;
+    }
+  return p;
 }
 
-template <int NM, int T, int RT, int BPW>
+size_t gemv_rows_part_floats(const RowsPlan& p, int n) {
+  return p.slices > 1 ? (size_t)(n / (16 * p.tiles)) * p.slices * (16 * kGemvMaxRowTiles) * (16 * p.tiles) : 0;
+}
+
+template <int NM, int T, int RT, int BPW, int KS = 1>
 hipError_t gemv_rows_launch(hipStream_t s, const GemvArgs& a, int dtype) {
-  const dim3 grid((unsigned)(a.n / (16 * T))), block(512);
+  const dim3 grid((unsigned)(a.n / (16 * T) * KS)), block(512);
   if (dtype == kF32)
-    (void)dispatch(q4k_gemv_rows_kernel<NM, T, RT, BPW, float>, grid, block, s, a);
+    (void)dispatch(q4k_gemv_rows_kernel<NM, T, RT, BPW, float, KS>, grid, block, s, a);
   else
-    (void)dispatch(q4k_gemv_rows_kernel<NM, T, RT, BPW, _Float16>, grid, block, s, a);
+    (void)dispatch(q4k_gemv_rows_kernel<NM, T, RT, BPW, _Float16, KS>, grid, block, s, a);
   return hipGetLastError();
 }
 
@@ -3385,10 +3475,17 @@ hipError_t gemv_rows_rt(hipStream_t s, const GemvArgs& a, int dtype) {
   return a.rows <= 32 ? gemv_rows_bpw<NM, T, 2>(s, a, dtype) : gemv_rows_bpw<NM, T, 3>(s, a, dtype);
 }
 
-hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, int tiles, bool gated) {
-  if (a.rows <= 16 || a.rows > 16 * kGemvMaxRowTiles || (a.nb != 16 && a.nb != 48) || a.n % (16 * tiles) != 0 ||
+hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, const RowsPlan& p, bool gated) {
+  const int tiles = p.tiles;
+  if (a.rows <= 16 || a.rows > 16 * kGemvMaxRowTiles || (a.nb != 16 && a.nb != 48) || tiles < 1 || a.n % (16 * tiles) != 0 ||
       a.rows != (a.split ? 2 * a.m : a.m))
     return hipErrorInvalidValue;
+  if (p.slices != 1) {
+    // Three K-slices of four column tiles (2 blocks per wave): K = 12288.
+    if (gated || p.slices != 3 || tiles != 4 || a.nb != 48 || !a.part || !a.counters)
+      return hipErrorInvalidValue;
+    return a.rows <= 32 ? gemv_rows_launch<1, 4, 2, 2, 3>(s, a, dtype) : gemv_rows_launch<1, 4, 3, 2, 3>(s, a, dtype);
+  }
   if (gated) {
     if (a.nb != 16)
       return hipErrorInvalidValue;

@@ -110,23 +110,24 @@ def case_gate_up_off():
 
 def case_rows():
     # Decode passes of 17..48 fragment rows: gated pairs at N = 12288 and
-    # plain projections (K = 4096 and 12288) with the rows GEMV off, or
-    # forced to a number of column tiles.
+    # plain projections (K = 4096 and 12288) with the rows GEMV off, forced
+    # to a number of column tiles, or with its K-slices off or forced.
     for m in (40, 24):
         check_gate_up(m, 12288, 4096, seed=35 + m)
-    counts40 = [5] * 8
-    for n, k in ((6144, 4096), (4096, 12288)):
-        rng = np.random.default_rng(37 + k % 97)
+    # K = 12288 at N = 4096 takes three K-slices of four column tiles by
+    # default; N = 8192 (128 column groups, 384 workgroups) only when forced.
+    for m, n, k in ((40, 6144, 4096), (40, 4096, 12288), (24, 8192, 12288)):
+        rng = np.random.default_rng(37 + k % 97 + n % 89)
         w = make_weight(rng, n, k, TYPE_Q4_K)
-        x = make_x(rng, 40, k)
-        aux = make_x(rng, 40, n)
+        x = make_x(rng, m, k)
+        aux = make_x(rng, m, n)
         W = q4k.Weight(w, n, k)
         y = _t(aux)
-        q4k.linear(_t(x), W, 40, y, auxiliary=y, query_counts=counts40)
+        q4k.linear(_t(x), W, m, y, auxiliary=y, query_counts=[5] * (m // 5) + ([m % 5] if m % 5 else []))
         torch.cuda.synchronize()
         err = row_rel_err(y.cpu().numpy(), oracle.linear(x, w, n, k, aux=aux, post=1))
         worst.append(err)
-        assert err <= TOL, (n, k, err)
+        assert err <= TOL, (m, n, k, err)
 
 
 def case_gemv_generic():

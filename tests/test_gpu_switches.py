@@ -26,6 +26,8 @@ SETTINGS = [
     ({"Q4K_GEMV_GATE_UP": "0"}, "gate_up_off"),
     ({"Q4K_GEMV_ROWS": "0"}, "rows"),
     ({"Q4K_GEMV_ROWS": "2"}, "rows"),
+    ({"Q4K_GEMV_ROWS_SLICES": "1"}, "rows"),
+    ({"Q4K_GEMV_ROWS_SLICES": "3"}, "rows"),
     ({"Q4K_GEMV_GENERIC": "1"}, "gemv_generic"),
     ({"Q4K_GEMV_WAVES": "4", "Q4K_GEMV_TILES": "1"}, "gemv_shape"),
     ({"Q4K_GEMV_WAVES": "16", "Q4K_GEMV_TILES": "2"}, "gemv_shape"),
