@@ -3696,6 +3696,25 @@ bool gemm2_narrow(int tiles256, int tiles128, int cus) {
   return r2 * kGemmNarrowTileTime < r4 * 10;
 }
 
+// 192 columns per workgroup (the typed template's Q4_K policy with three
+// column tiles per wave) when the 256-column tiles leave CUs idle and the
+// 192-column ones fill between three quarters of the CUs and all of them in
+// one round.  At M = 821 the N = 6144 projection (168 256-column tiles, 224
+// of 192) measured 55.0 us against 59.6 in K-segments and 64.3 unsplit; the
+// N = 4096 one (154 tiles) 59.4 against 51.5 on 128 columns, which it keeps.
+// The accumulation order and the dequantised values are those of the
+// 256-column GEMM, and the K-split defers to this rule, so the gated GEMM
+// stays bit-identical to the two-call form.  Q4K_GEMM_MID: -1 auto, 0
+// never, 1 always (for the plain Q4_K GEMM).
+bool gemm2_mid(int m, int n, int cus) {
+  static const int forced = env_int("Q4K_GEMM_MID", -1);
+  if (forced >= 0)
+    return forced == 1;
+  const int tiles_y = (m + kG2M - 1) / kG2M;
+  const int t4 = (n + kG2N - 1) / kG2N * tiles_y, t3 = (n / 16 + 11) / 12 * tiles_y;
+  return t4 < cus && t3 <= cus && 4 * t3 >= 3 * cus;
+}
+
 // Segments 1 per workgroup on the CUs that `tiles` workgroups leave free.
 static int split_segments_per_wg(int tiles, int cus) {
   const int free = cus - tiles;
@@ -3724,7 +3743,7 @@ int gemm2_split_b(int m, int n, int nb, int cus) {
   static const int on = env_int("Q4K_GEMM2_SPLIT", 1);
   static const int b_env = env_int("Q4K_GEMM2_SPLIT_B", 0);
   const int tiles = ((n + kG2N - 1) / kG2N) * ((m + kG2M - 1) / kG2M);
-  if (!on || tiles >= cus)
+  if (!on || tiles >= cus || gemm2_mid(m, n, cus))
     return 0;
   if (b_env > 0)
     return b_env < nb ? b_env : 0;
@@ -3768,6 +3787,8 @@ hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
       return hipErrorInvalidValue;
     return gemm2_split_launch<false>(s, a, dtype, tiles_x, tiles_y, cus, b);
   }
+  if (gemm2_mid(a.m, a.n, cus))
+    return typed_gemm_launch<Mid<TgQ4K, 5>>(s, a, dtype, cus);
   if (gemm2_narrow(tiles, ((a.n / 16 + 7) / 8) * tiles_y, cus))
     return typed_gemm_launch<TgQ4K>(s, a, dtype, cus);
   static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);

@@ -2,9 +2,9 @@
 
 Every routing rule of the library is a measured choice, and a few
 environment variables switch a kernel family off or force a shape for
-comparisons (split-K GEMV, fused gate/up, the GEMV shape, the GEMM tiling,
-the GEMM's K-segments, persistent grids and tile order, the Q8_0 GEMM tiling, the typed
-GEMV forms).  The
+comparisons (split-K GEMV, fused gate/up, the GEMV shape and K-slices, the
+GEMM tiling, the GEMM's K-segments and 192-column tiling, persistent grids
+and tile order, the Q8_0 GEMM tiling, the typed GEMV forms).  The
 library reads each once per process, so the default routing is all that the
 rest of the suite reaches.  Here each setting runs tests/switch_child.py in a
 child process with the variable set: the shapes whose routing the setting
@@ -35,6 +35,8 @@ SETTINGS = [
     ({"Q4K_GEMM_NARROW": "0", "Q4K_GEMM2_SPLIT": "0", "Q4K_GEMM2_PERSIST": "0"}, "gemm"),
     ({"Q4K_GEMM_XCD_ROWS": "0"}, "gemm"),
     ({"Q4K_GEMM2_SPLIT_B": "3"}, "gemm"),
+    ({"Q4K_GEMM_MID": "1"}, "gemm"),
+    ({"Q4K_GEMM_MID": "0"}, "gemm"),
     ({"Q4K_TYPED_MID": "1"}, "typed_gemm"),
     ({"Q4K_TYPED_MID": "0"}, "typed_gemm"),
     ({"Q6K_GEMV_PERSISTENT": "1"}, "typed_gemv"),
