@@ -37,6 +37,7 @@ CASES = [
     ("split-K down (K=12288)", 4096, 12288, (8, [1] * 8), (3, [1] * 3), 1, torch.float32),
     ("persistent GEMV (wide N)", 65536, 4096, (8, [1] * 8), (2, [1] * 2), 0, torch.float32),
     ("staged GEMV (40 rows)", 4096, 4096, (40, [5] * 8), (20, [5] * 4), 0, torch.float32),
+    ("rows GEMV in K-slices (K=12288)", 4096, 12288, (40, [5] * 8), (24, [4] * 6), 1, torch.float32),
     ("prefill GEMM", 4096, 4096, (300, [300]), (129, [129]), 2, torch.float32),
     ("prefill GEMM in two K-halves", 1024, 8192, (300, [300]), (129, [129]), 1, torch.float32),
     ("narrow prefill (GEMV groups)", 128, 1024, (100, [100]), (30, [30]), 0, torch.float32),
@@ -80,12 +81,13 @@ def test_noalloc_captures_on_fresh_shapes(q4k, gpu):
     forbids): the capture succeeds, allocates nothing, and every replay --
     with eager work and a synchronisation between replays -- gives the
     output of q4k_linear called eagerly after the capture.  The split-K
-    GEMV and the GEMM's two K-halves clear their counters with a fill
-    kernel inside the graph."""
+    GEMV, the GEMM's K-segments and the rows GEMV's K-slices clear their
+    counters with a fill kernel inside the graph."""
     rng = np.random.default_rng(1320)
-    # The split-K GEMV (K = 12288), the GEMM in two K-halves and the staged
-    # GEMV at K = 16640, a K no other test of this suite uses.
-    cases = [(8192, 12288, 8, [1] * 8, 1), (1024, 16640, 200, [200], 1), (1536, 16640, 40, [5] * 8, 0)]
+    # The split-K GEMV (K = 12288), the GEMM in two K-segments and the staged
+    # GEMV at K = 16640, a K no other test of this suite uses, and the rows
+    # GEMV in three K-slices at N = 2048.
+    cases = [(8192, 12288, 8, [1] * 8, 1), (1024, 16640, 200, [200], 1), (1536, 16640, 40, [5] * 8, 0), (2048, 12288, 40, [5] * 8, 1)]
     for n, k, m, counts, post in cases:
         W = q4k.Weight(make_q4k(rng, n, k), n, k)
         x = torch.from_numpy(make_x(rng, m, k, 0.25)).to(gpu)
