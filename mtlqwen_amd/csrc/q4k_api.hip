@@ -698,8 +698,9 @@ int run_linear_locked(hipStream_t stream, Workspace& ws, q4k_weight* w, q4k_weig
     return Q4K_OK;
   }
   const size_t ws_rows = gemv ? (size_t)((rows + 15) / 16) * 16 : (size_t)gemm2_rows((int)m);
-  // xs is read 32 lanes at a time from its start; +128 halves of slack.
-  const size_t xs_halves = gemv ? gemv_xs_halves(rows, (int)w->k) + 128 : 0;
+  // xs (and, for single fp16 fragments, the residual plane after it) is
+  // read 32 lanes at a time from its start; +128 halves of slack.
+  const size_t xs_halves = gemv ? 2 * gemv_xs_halves(rows, (int)w->k) + 128 : 0;
   int rc = ensure_workspace(stream, ws, w->device, ws_rows * w->k + xs_halves, ws_rows);
   if (rc)
     return rc;

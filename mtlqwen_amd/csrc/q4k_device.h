@@ -108,6 +108,7 @@ struct BlockConsts {
   float d, dmin;
   h2_t mul_lo, add_lo, mul_hi, add_hi;
   h4_t bmin;
+  h4_t bsc;  // 7.5 sc_j, j = 4(g - 2)..4(g - 2)+3 for g >= 2 (zero for g < 2): the mean-quant correction's B operand
 };
 
 __device__ __forceinline__ BlockConsts block_consts(u4_t hd, int g) {
@@ -135,6 +136,14 @@ __device__ __forceinline__ BlockConsts block_consts(u4_t hd, int g) {
   const h2_t m01 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04010400u)), k32, kneg32768);
   const h2_t m23 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, mb, 0x04030402u)), k32, kneg32768);
   k.bmin = h4_t{m01[0], m01[1], m23[0], m23[1]};
+  // k = 8..15 of the min-term MFMA: bytes 0..3 = sc_{4(g-2)}..sc_{4(g-2)+3}
+  // for g >= 2, zero for g < 2; (1024 + sc) * 7.5 - 7680 = 7.5 sc exactly
+  const uint32_t s03 = hd.y & 0x3F3F3F3Fu, s47 = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+  const uint32_t sb = g < 2 ? 0u : (g == 2 ? s03 : s47);
+  const h2_t k75 = {(_Float16)7.5f, (_Float16)7.5f}, kneg7680 = {(_Float16)-7680.0f, (_Float16)-7680.0f};
+  const h2_t s01 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, sb, 0x04010400u)), k75, kneg7680);
+  const h2_t s23 = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, sb, 0x04030402u)), k75, kneg7680);
+  k.bsc = h4_t{s01[0], s01[1], s23[0], s23[1]};
   return k;
 }
 
@@ -156,6 +165,13 @@ __device__ __forceinline__ size_t gemm_frag_offset(int row, int c, int nb) {
   const int kk = c * 8, b = kk >> 8, e = kk & 255, g = e >> 6, h = (e >> 5) & 1, u = (e >> 3) & 3;
   const int f = 2 * ((row >> 4) & 7) + h;
   return (((((size_t)(row >> 7) * nb + b) * 4 + u) * 16 + f) * 64 + (g * 16 + (row & 15))) * 8;
+}
+
+// Halves of one plane of min-term fragments (xs_offset) for `rows` staged
+// rows; single fp16 staging writes a second plane, of the sub-blocks' sums of
+// rounding residuals, right after the first.
+__host__ __device__ inline size_t xs_plane_halves(int rows, int nb) {
+  return (size_t)((rows + 15) / 16) * nb * 128;
 }
 
 // Half index of (row, sub-block j of block b) in the min-term fragments: per

@@ -74,16 +74,18 @@ struct RowNorm {
 // Converts and stores one 8-element chunk; all 256 threads of the workgroup
 // must call it together (the sub-block sum is reduced over 4 lanes).
 template <int MODE>
-__device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row, int c, bool live, int m, int k, int nb, const float* v,
-                                            float up) {
+__device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, _Float16* xe, int row, int c, bool live, int m, int k, int nb,
+                                            const float* v, float up) {
   h8_t hi, lo;
-  float sum = 0.0f;
+  float sum = 0.0f, res = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float t = v[i] * up;
     hi[i] = (_Float16)t;
-    lo[i] = (_Float16)(t - (float)hi[i]);
+    const float r = t - (float)hi[i];
+    lo[i] = (_Float16)r;
     sum += t;
+    res += r;
   }
   if (live) {
     *reinterpret_cast<h8_t*>(xo + frag_offset(row, c, nb)) = hi;
@@ -93,6 +95,8 @@ __device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row,
   // Chunks 4q..4q+3 (lanes 4q..4q+3) form one sub-block.
   sum += __shfl_xor(sum, 1);
   sum += __shfl_xor(sum, 2);
+  res += __shfl_xor(res, 1);
+  res += __shfl_xor(res, 2);
   if (live && (c & 3) == 0) {
     const float s32 = sum * 0.03125f;
     const _Float16 sh = (_Float16)s32;
@@ -100,6 +104,15 @@ __device__ __forceinline__ void stage_store(_Float16* xo, _Float16* xs, int row,
     xs[xs_offset(row, b, j, nb)] = sh;
     if (MODE == kStageFragSplit)
       xs[xs_offset(m + row, b, j, nb)] = (_Float16)(s32 - (float)sh);
+    // The sub-block's sum of fp16 rounding residuals (the mean-quant
+    // correction's A operand; |.| <= 32 half-ulps of 2^15), zero for hi/lo
+    // fragments, whose low parts carry the residuals.
+    if (MODE == kStageFrag) {
+      xe[xs_offset(row, b, j, nb)] = (_Float16)res;
+    } else {
+      xe[xs_offset(row, b, j, nb)] = (_Float16)0.0f;
+      xe[xs_offset(m + row, b, j, nb)] = (_Float16)0.0f;
+    }
   }
 }
 
@@ -126,6 +139,9 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
   const InT* xr = x + (size_t)row * k;
   const int chunks = k >> 3, nb = k >> 8;
   const bool in_regs = chunks <= 256 * kStageRegChunks;
+  // The residual sums' plane follows the sub-block sums (of m rows, or 2m
+  // for hi/lo fragments, whose residual sums are written as zeros).
+  _Float16* const xe = xs + xs_plane_halves(MODE == kStageFragSplit ? 2 * m : m, nb);
   float v[kStageRegChunks][8] = {};
   float mx = 0.0f, ss = 0.0f;
   if (in_regs) {
@@ -166,7 +182,7 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
     for (int j = 0; j < kStageRegChunks; ++j) {
       const int c = threadIdx.x + 256 * j;
       if (256 * j < chunks)  // uniform: whole groups of 4 lanes take part
-        stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, v[j], cs);
+        stage_store<MODE>(xo, xs, xe, row, c, c < chunks, m, k, nb, v[j], cs);
     }
   } else {
     for (int c0 = 0; c0 < chunks; c0 += 256) {
@@ -175,7 +191,7 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const InT* __restrict__ x,
       float unused = 0.0f;
       if (c < chunks)
         load8_norm<NORM>(xr, nrm.w, c, t, unused);
-      stage_store<MODE>(xo, xs, row, c, c < chunks, m, k, nb, t, cs);
+      stage_store<MODE>(xo, xs, xe, row, c, c < chunks, m, k, nb, t, cs);
     }
   }
 }
@@ -996,7 +1012,13 @@ __global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
   // Dead fragment rows (>= a.rows inside the last row tile) are loaded as
   // they are: a garbage A row reaches only its own C row, never stored.
   h8_t xa[RT][8];
+  // The min-term MFMA's A operand: lanes 0..31 (k = 0..7) the sub-block sums
+  // / 32; lanes 32..63 (k = 8..15) the sub-blocks' sums of fp16 rounding
+  // residuals, from the plane after the sums that stage_x_kernel writes
+  // (zeros for hi/lo fragments).  Each of the two MFMAs that read it has a
+  // zero B operand for the other half's k.
   h4_t xsa[RT];
+  const h4_t* const xsrc = reinterpret_cast<const h4_t*>(a.xs + (lane >= 32 ? xs_plane_halves(a.rows, nb) : 0));
   auto load_x = [&](int b) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -1004,7 +1026,7 @@ __global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
 #pragma unroll
       for (int s = 0; s < 8; ++s)
         xa[rt][s] = xp[s * 64];
-      xsa[rt] = reinterpret_cast<const h4_t*>(a.xs)[(size_t)(rt * nb + b) * 32 + (lane & 31)];
+      xsa[rt] = xsrc[(size_t)(rt * nb + b) * 32 + (lane & 31)];
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -1046,6 +1068,10 @@ __global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
     }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      // Mean-quant correction of the fp16 rounding: sum_j E_j * 7.5 sc_j
+      // (k = 8 + j), E_j = the sub-block's sum of rounding residuals: the
+      // part of the q-term's error common to every column.
+      cq[rt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bsc, cq[rt], 0, 0, 0);
       // min term: sum_j (xs_j / 32) * (32 m_j), k = sub-block
       const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
@@ -3481,7 +3507,9 @@ hipError_t launch_gemv_rows(hipStream_t s, const GemvArgs& a, int dtype, const R
       a.rows != (a.split ? 2 * a.m : a.m))
     return hipErrorInvalidValue;
   if (p.slices != 1) {
-    // Three K-slices of four column tiles (2 blocks per wave): K = 12288.
+    // K = 12288: three K-slices of four column tiles (2 blocks per wave).
+    // (Two slices of two column tiles, 3 blocks per wave and all 256 CUs,
+    // measured the same config-2 pass: 78.9-81.3 against 79.4-79.7 us.)
     if (gated || p.slices != 3 || tiles != 4 || a.nb != 48 || !a.part || !a.counters)
       return hipErrorInvalidValue;
     return a.rows <= 32 ? gemv_rows_launch<1, 4, 2, 2, 3>(s, a, dtype) : gemv_rows_launch<1, 4, 3, 2, 3>(s, a, dtype);

@@ -17,6 +17,11 @@ from q4k_ref import make_q4k, make_x, row_rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+# Single fp16 rows (25..48) of fp32 activations: the mean-quant correction of
+# the rounding (each sub-block's sum of residuals times 7.5 sc) removes the
+# part of the error common to every column; measured 1.5e-4 .. 3.0e-4 (plain
+# and gated), against 4.6e-4 .. 9.7e-4 without it.
+CORRECTED_TOL = 5e-4
 
 # (m, n, k, counts): decode phase (counts <= 5 per query) unless noted
 SHAPES = [
@@ -106,7 +111,9 @@ def test_rows_gated_wide(q4k, oracle, gpu, m, dtype):
     assert torch.equal(y, y2)
     got = y.float().cpu().numpy()
     assert np.all(np.isfinite(got))
-    assert row_rel_err(got, oracle.mlp_gate_up(x, wg, wu, n, k)) <= TOL
+    err = row_rel_err(got, oracle.mlp_gate_up(x, wg, wu, n, k))
+    print(f"gated rows m={m} {dtype}: max row error {err:.3e}")
+    assert err <= (CORRECTED_TOL if m > 24 and dtype == torch.float32 else TOL)
 
 
 @pytest.mark.parametrize("m,n,post,dtype", [(40, 4096, 1, torch.float32), (17, 8192, 2, torch.float32), (33, 4096, 1, torch.float16),
@@ -128,4 +135,6 @@ def test_rows_k12288(q4k, oracle, gpu, m, n, post, dtype):
     got = y.float().cpu().numpy()
     assert np.all(np.isfinite(got))
     ref = oracle.linear(x, w, n, k, aux=aux, post=post)
-    assert row_rel_err(got, ref.astype(np.float32)) <= TOL
+    err = row_rel_err(got, ref.astype(np.float32))
+    print(f"rows K=12288 m={m} n={n} post={post} {dtype}: max row error {err:.3e}")
+    assert err <= (CORRECTED_TOL if m > 24 and dtype == torch.float32 else TOL)
