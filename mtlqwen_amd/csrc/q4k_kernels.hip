@@ -453,6 +453,10 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
   // loaded unmasked: in a matrix product a garbage A row only reaches its own
   // C row, which the epilogue never reads.  Branch-free loads keep the vmcnt
   // waits exact.
+  // The min-term operand: lanes 0..31 the sub-block sums / 32, lanes 32..63
+  // (k = 8..15) the sub-blocks' sums of fp16 rounding residuals from the
+  // plane after them (zeros for hi/lo rows), as in the rows GEMV.
+  const h4_t* const xsrc = reinterpret_cast<const h4_t*>(a.xs + (lane >= 32 ? xs_plane_halves(a.rows, nb) : 0));
   auto load_x = [&](h8_t (&xa)[RT][8], h4_t (&xsa)[RT], int b) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -460,7 +464,7 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int s = 0; s < 8; ++s)
         xa[rt][s] = xp[s * 64];
-      xsa[rt] = reinterpret_cast<const h4_t*>(a.xs)[(size_t)(rt * nb + b) * 32 + (lane & 31)];
+      xsa[rt] = xsrc[(size_t)(rt * nb + b) * 32 + (lane & 31)];
     }
   };
   auto compute = [&](const TileWords<T, NM>& cur, const h8_t (&xa)[RT][8], const h4_t (&xsa)[RT]) {
@@ -487,7 +491,11 @@ __global__ __launch_bounds__(64 * W) void q4k_gemv_kernel(GemvArgs a) {
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-          // min term: sum_j (xs_j / 32) * (32 m_j), k = sub-block
+          // mean-quant correction of the fp16 rounding (k = 8 + j; single
+          // fp16 rows, m >= 25, need at least two row tiles: one holds only
+          // hi/lo rows), then the min term: sum_j (xs_j / 32) * (32 m_j)
+          if constexpr (RT >= 2)
+            cq[rt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bsc, cq[rt], 0, 0, 0);
           const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
           for (int v = 0; v < 4; ++v)
@@ -1071,7 +1079,8 @@ __global__ __launch_bounds__(512) void q4k_gemv_rows_kernel(GemvArgs a) {
       // Mean-quant correction of the fp16 rounding: sum_j E_j * 7.5 sc_j
       // (k = 8 + j), E_j = the sub-block's sum of rounding residuals: the
       // part of the q-term's error common to every column.
-      cq[rt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bsc, cq[rt], 0, 0, 0);
+      if constexpr (RT >= 2)
+        cq[rt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bsc, cq[rt], 0, 0, 0);
       // min term: sum_j (xs_j / 32) * (32 m_j), k = sub-block
       const f4_t cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xsa[rt], kc.bmin, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll

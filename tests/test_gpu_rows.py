@@ -17,8 +17,8 @@ from q4k_ref import make_q4k, make_x, row_rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-# Single fp16 rows (25..48) of fp32 activations: the mean-quant correction of
-# the rounding (each sub-block's sum of residuals times 7.5 sc) removes the
+# Single fp16 rows (25..48) of fp32 activations, in the rows GEMV and the
+# staged GEMV: the mean-quant correction of the rounding (each sub-block's sum of residuals times 7.5 sc) removes the
 # part of the error common to every column; measured 1.5e-4 .. 3.0e-4 (plain
 # and gated), against 4.6e-4 .. 9.7e-4 without it.
 CORRECTED_TOL = 5e-4
@@ -51,7 +51,9 @@ def test_rows_store(q4k, oracle, gpu, m, n, k, counts):
     got = y.cpu().numpy()
     assert np.all(np.isfinite(got))
     assert torch.equal(y, y2)
-    assert row_rel_err(got, oracle.linear(x, w, n, k)) <= TOL
+    err = row_rel_err(got, oracle.linear(x, w, n, k))
+    print(f"rows store m={m} n={n} k={k}: max row error {err:.3e}")
+    assert err <= (CORRECTED_TOL if m > 24 else TOL)
 
 
 @pytest.mark.parametrize("m,post,dtype", [(40, 1, torch.float32), (17, 2, torch.float32), (33, 1, torch.float16),
