@@ -2828,9 +2828,10 @@ struct TgQ6K {
   struct R {
     uint32_t sc, d;
   };
+  // d * sc of the lane's four scale bytes (MFMAs u and 4 + u take bytes u / 2
+  // and 2 + u / 2), formed once per block.
   struct K {
-    float d;
-    uint32_t sc;
+    float ds[4];
   };
   // Triples u / 2 (MFMA u) and 2 + u / 2 (MFMA 4 + u); C only for odd u.
   struct W {
@@ -2848,9 +2849,12 @@ struct TgQ6K {
     r.sc = lds_u32(tb + kQ6ScaleOffset + 4 * lane);
     r.d = *reinterpret_cast<const uint16_t*>(tb + kQ6DOffset + 2 * (lane & 15));
   }
+  // Scale byte i is stored sc + 128: d * sc = fma(sc + 128, d, -128 d), exact.
   static __device__ __forceinline__ void consts(K& k, const R& r, int) {
-    k.d = half_bits_to_float(r.d);
-    k.sc = r.sc;
+    const float d = half_bits_to_float(r.d), m128 = -128.0f * d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      k.ds[i] = __builtin_fmaf((float)((r.sc >> (8 * i)) & 0xffu), d, m128);
   }
   static __device__ __forceinline__ uint32_t dword(const uint8_t* tb, int j, int lane) {
     return lds_u32(tb + (j >> 2) * 1024 + 16 * lane + 4 * (j & 3));
@@ -2890,14 +2894,11 @@ struct TgQ6K {
     }
     return __builtin_bit_cast(h8_t, u4_t{r[0], r[1], r[2], r[3]});
   }
-  // Scale of MFMA u: byte u / 2 of the lane's scale dword (stored sc + 128);
-  // of MFMA 4 + u: byte 2 + u / 2.  d * sc = fma(sc + 128, d, -128 d), exact.
+  // Scale of MFMA u: byte u / 2 of the lane's scale dword; of MFMA 4 + u:
+  // byte 2 + u / 2.
   static __device__ __forceinline__ void dequant(const K& k, const W& w, int u, h8_t& blo, h8_t& bhi) {
-    const float m128 = -128.0f * k.d;
-    const float dsl = __builtin_fmaf((float)((k.sc >> (8 * (u >> 1))) & 0xffu), k.d, m128);
-    const float dsh = __builtin_fmaf((float)((k.sc >> (8 * (2 + (u >> 1)))) & 0xffu), k.d, m128);
-    blo = triple(w.a0, w.b0, w.c0, u & 1, dsl);
-    bhi = triple(w.a1, w.b1, w.c1, u & 1, dsh);
+    blo = triple(w.a0, w.b0, w.c0, u & 1, k.ds[u >> 1]);
+    bhi = triple(w.a1, w.b1, w.c1, u & 1, k.ds[2 + (u >> 1)]);
   }
 };
 
