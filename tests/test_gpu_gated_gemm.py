@@ -32,10 +32,13 @@ def _gemm_launches(q4k, fn):
 # live output tile; k = 256 is one block; k = 8192 and 12288 with few tiles
 # run as two K-halves per tile in both forms; at (821, 6144) the plain GEMM
 # takes 192 columns per workgroup (the typed template) and neither form
-# splits K.
+# splits K; at (821, 5120, 4096) both split K at block 11 of 16, the plain
+# GEMM with its short segments two to a workgroup, the gated one (280 tiles)
+# dealing all segments round robin.
 SHAPES = [(300, 512, 1024, torch.float32), (257, 1296, 2048, torch.float32), (129, 272, 1024, torch.float32),
           (130, 512, 256, torch.float16), (2048, 12288, 4096, torch.float32),
-          (200, 1024, 8192, torch.float32), (130, 512, 12288, torch.float16), (821, 6144, 1024, torch.float32)]
+          (200, 1024, 8192, torch.float32), (130, 512, 12288, torch.float16), (821, 6144, 1024, torch.float32),
+          (821, 5120, 4096, torch.float32)]
 
 
 @pytest.mark.parametrize("m,n,k,dtype", SHAPES)

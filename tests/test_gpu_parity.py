@@ -72,9 +72,12 @@ def test_gemv_f16(q4k, oracle, gpu, m, post):
 # (49, 64, 256) .. (129, 80, 512): narrow outputs (the GEMV per 8-row group);
 # (130, 272, 1024), (77, 400, 512): the 128 x 128 GEMM (N not a multiple of 256).
 # N = 272, 400, 1296: a partial last 256-column block (1, 9 and 1 of its 16
-# column tiles live; waves with none).
+# column tiles live; waves with none).  At M = 821: N = 6144 and 6000 take
+# 192 columns per workgroup (6000: 3 of the last block's 12 column tiles
+# live); N = 5120 (140 tiles of 256 columns) two K-segments per tile, the
+# short ones two to a workgroup; (257, 4096, 12288) two K-halves.
 GEMM_SHAPES = [(49, 64, 256), (64, 128, 512), (65, 144, 768), (128, 256, 1024), (129, 80, 512), (130, 272, 1024), (77, 400, 512),
-               (300, 4096, 4096), (821, 6144, 4096), (257, 4096, 12288), (257, 1296, 2048)]
+               (300, 4096, 4096), (821, 6144, 4096), (821, 6000, 1024), (821, 5120, 4096), (257, 4096, 12288), (257, 1296, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)

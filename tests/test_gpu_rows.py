@@ -119,10 +119,11 @@ def test_rows_gated_wide(q4k, oracle, gpu, m, dtype):
 
 
 @pytest.mark.parametrize("m,n,post,dtype", [(40, 4096, 1, torch.float32), (17, 8192, 2, torch.float32), (33, 4096, 1, torch.float16),
-                                            (24, 12288, 0, torch.float32)])
+                                            (24, 12288, 0, torch.float32), (24, 4096, 1, torch.float32)])
 def test_rows_k12288(q4k, oracle, gpu, m, n, post, dtype):
     """Plain projections with K = 12288 (the config-2 down projection and
-    wider ones) on the rows GEMV: epilogues, fp16, hi/lo rows."""
+    wider ones) on the rows GEMV: epilogues, fp16, hi/lo rows (at N = 4096
+    also in K-slices)."""
     k = 12288
     rng = np.random.default_rng(1580 + m + n % 89)
     w = make_q4k(rng, n, k)
