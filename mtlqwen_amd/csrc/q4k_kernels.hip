@@ -3744,7 +3744,7 @@ bool gemm2_narrow(int tiles256, int tiles128, int cus) {
 // 256-column GEMM, and the K-split defers to this rule, so the gated GEMM
 // stays bit-identical to the two-call form.  Q4K_GEMM_MID: -1 auto, 0
 // never, 1 always (for the plain Q4_K GEMM).
-bool gemm2_mid(int m, int n, int cus) {
+static bool gemm2_mid(int m, int n, int cus) {
   static const int forced = env_int("Q4K_GEMM_MID", -1);
   if (forced >= 0)
     return forced == 1;
