@@ -54,8 +54,9 @@ def parse():
                          "runs its first couple of hundred decode steps about 10 %% slower")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--prefill-warmup-ms", type=float, default=300.0,
-                    help="untimed prefill graph replays before the timed ones (the GEMMs run about 15 %% slower for the "
-                         "first tens of milliseconds of sustained MFMA work)")
+                    help="untimed prefill graph replays before the timed ones, and as long again before each config-2/3 "
+                         "pass and each typed prefill GEMM shape (the GEMMs run about 15 %% slower for the first tens of "
+                         "milliseconds of sustained MFMA work)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -382,7 +383,7 @@ def neighbours_bench(args, dev):
     return out
 
 
-def configs_bench(dev, parts=("config2", "config3"), sets=3):
+def configs_bench(dev, parts=("config2", "config3"), sets=3, warm_ms=300.0):
     """Benchmark configurations 2 and 3, each as one HIP graph of
     its projections (random Q4_K weights as in config 0, seeded fp32
     activations), timed over replays:
@@ -422,8 +423,14 @@ def configs_bench(dev, parts=("config2", "config3"), sets=3):
         with torch.cuda.graph(graph, stream=s):
             for _ in range(reps):
                 fn()
-        graph.replay()
-        torch.cuda.synchronize()
+        # Untimed replays for warm_ms of wall time first, as the prefill leg
+        # does: kernels of a freshly started stream of work run slower.
+        t_end = time.perf_counter() + warm_ms * 1e-3
+        while True:
+            graph.replay()
+            torch.cuda.synchronize()
+            if time.perf_counter() >= t_end:
+                break
         return timed_graph(graph, 5) / (5 * reps)
 
     if "config2" in parts:
@@ -607,10 +614,11 @@ def _random_typed(dev, n, k, t, seed):
     return raw
 
 
-def types_prefill_bench(dev):
+def types_prefill_bench(dev, warm_ms=300.0):
     """The typed MFMA prefill GEMM at the config-4 shapes (M = 2048; gate
     K = 4096 -> N = 12288 and down K = 12288 -> N = 4096), per launch with
-    dispatch-attached events."""
+    dispatch-attached events, after warm_ms of untimed back-to-back launches
+    of the same call (as the prefill leg warms up)."""
     import torch
     import mtlqwen_amd as q4k
 
@@ -623,9 +631,13 @@ def types_prefill_bench(dev):
             W = q4k.Weight(_random_typed(dev, n, k, t, 0x51A70040 + t + n), n, k, ggml_type=t)
             x = torch.randn((M, k), device=dev, generator=torch.Generator(device=dev).manual_seed(0x51A70041 + t))
             y = torch.empty((M, n), device=dev)
-            for _ in range(3):
-                q4k.linear(x, W, M, y, query_counts=[M])
-            torch.cuda.synchronize()
+            t_end = time.perf_counter() + warm_ms * 1e-3
+            while True:
+                for _ in range(4):
+                    q4k.linear(x, W, M, y, query_counts=[M])
+                torch.cuda.synchronize()
+                if time.perf_counter() >= t_end:
+                    break
             q4k.profile_enable(True)
             for _ in range(10):
                 q4k.linear(x, W, M, y, query_counts=[M])
@@ -874,13 +886,13 @@ def main():
         elif args.part == "config0":
             res["config0"] = config0_bench(dev)
         elif args.part in ("config2", "config3"):
-            res.update(configs_bench(dev, parts=(args.part,), sets=args.sets if args.part == "config2" else 1))
+            res.update(configs_bench(dev, parts=(args.part,), sets=args.sets if args.part == "config2" else 1, warm_ms=args.prefill_warmup_ms))
         elif args.part == "lm_head":
             res["q4k_lm_head"], res["q6k_lm_head"] = lm_head_bench(dev, 12), lm_head_bench(dev, 14)
         elif args.part == "types":
             res["types_lm_head"] = types_bench(args, dev)
         elif args.part == "types_prefill":
-            res["types_prefill"] = types_prefill_bench(dev)
+            res["types_prefill"] = types_prefill_bench(dev, args.prefill_warmup_ms)
         elif args.part == "shard":
             res["shard_1of8"] = shard_bench(args, dev)
         elif args.part == "neighbours":
@@ -895,11 +907,11 @@ def main():
     pre = None if args.no_prefill or not want("prefill") else prefill_bench(args, dev)
     shard = shard_bench(args, dev) if want("shard") else None
     neighbours = neighbours_bench(args, dev) if want("neighbours") else None
-    cfgs = configs_bench(dev, sets=min(args.sets, 3)) if want("config2") else None
+    cfgs = configs_bench(dev, sets=min(args.sets, 3), warm_ms=args.prefill_warmup_ms) if want("config2") else None
     q4k_head = lm_head_bench(dev, 12) if want("lm_head") else None
     q6k = lm_head_bench(dev, 14) if want("lm_head") else None
     types = None if args.no_types or not want("types") else types_bench(args, dev)
-    types_pre = None if args.no_types or args.no_prefill or not want("types_prefill") else types_prefill_bench(dev)
+    types_pre = None if args.no_types or args.no_prefill or not want("types_prefill") else types_prefill_bench(dev, args.prefill_warmup_ms)
     copy_gbs = copy_ceiling(dev)
     mfma_tf = mtlqwen_amd.mfma_ceiling(0)
     read_ceil = read_ceiling(dev, dec["gated"]["avg_us"] if "avg_us" in dec.get("gated", {}) else None)
