@@ -2945,6 +2945,43 @@ struct TgQ8_0 {
   }
 };
 
+// Q8_0 with four column tiles per wave: two blocks of its 4352-byte
+// tile-blocks per column do not fit beside an A ring, so B streams in half
+// tile-blocks through three half-slots per column (typed_gemm_tile_half).
+// Half 0 of a tile-block holds the quant slabs of u-steps 0, 1 (slabs 0 and
+// 2: the low and high MFMA fragments) and the d row, half 1 the slabs of
+// u-steps 2, 3 (slabs 1 and 3).  A half-slot: [low slab 1 KB][high slab
+// 1 KB][d row 256 B].
+struct TgQ8_0W : TgQ8_0 {
+  static constexpr int kCT = 4, kAS = 3, kHS = 2304, kL0 = 3, kL1 = 2;
+  static constexpr bool kHalf = true;
+  static __device__ __forceinline__ void issue_half0(const uint8_t* src, uint32_t v16, uint32_t v4, uint32_t l) {
+    lds_dma16<0>(src, v16, l);
+    lds_dma16<1024>(src + 1024, v16, l);  // slab 2 into [1 KB, 2 KB)
+    lds_dma4<0>(src + 4096, v4, l + 2048);
+  }
+  static __device__ __forceinline__ void issue_half1(const uint8_t* src, uint32_t v16, uint32_t l) {
+    lds_dma16<0>(src + 1024, v16, l);     // slab 1
+    lds_dma16<1024>(src + 2048, v16, l);  // slab 3 into [1 KB, 2 KB)
+  }
+  static __device__ __forceinline__ void raw_half(R& r, const uint8_t* hs, int lane) {
+    r.dd = lds_u32(hs + 2048 + 4 * lane);
+  }
+  static __device__ __forceinline__ void words_half(W& w, const uint8_t* hs, int u, int lane) {
+    w.lo = *reinterpret_cast<const uint2*>(hs + 16 * lane + 8 * (u & 1));
+    w.hi = *reinterpret_cast<const uint2*>(hs + 1024 + 16 * lane + 8 * (u & 1));
+  }
+};
+
+template <class P, class = void>
+struct TgIsHalf {
+  static constexpr bool value = false;
+};
+template <class P>
+struct TgIsHalf<P, decltype((void)P::kHalf)> {
+  static constexpr bool value = P::kHalf;
+};
+
 struct TgIQ4XS {
   static constexpr int kTB = kTileN * kIQ4BlockBytes, kCT = 4, kAS = 5, kNL = 3, kVPM = 4;
   struct R {
@@ -3278,17 +3315,225 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
     full ? gemm2_epilogue<OutT, 2, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 2, false, CT>(a, acc, mt0, ct0, lane, nct);
 }
 
+// typed_gemm_tile with B in half tile-blocks (policies with kHalf): per
+// column three half-slots, half h (half h % 2 of block h / 2) in slot h % 3.
+// Half 1 of block blk + 1 is issued at u-step 1 of block blk into the slot of
+// half 0 of blk (last read at u-step 0), half 0 of block blk + 2 at u-step 3
+// into the slot of half 1 of blk (last read at u-step 2); each is read three
+// or four u-steps after its issue.  The A ring has kAS = 3 slots (A two
+// u-steps ahead).  Loads in issue order per u-step and column group c: A
+// fragment c of A(t + 2), then at u = 1 column c's half 1 (kL1 loads), at
+// u = 3 its half 0 (kL0 loads).  Every half read at u-step t was issued
+// before A(t), so the wait for A(t) covers it: the loads after A(t)'s last
+// fragment are column 3's half of u-step t - 2 and all of u-step t - 1, that
+// is 4 + CT kL0 (u = 0), kL0 + 4 (u = 1), 4 + CT kL1 (u = 2), kL1 + 4
+// (u = 3); at u-step 1 of the first block only A(2) follows A(1) (the
+// prologue issues no B after it), so the wait there is 4.
+template <class P, typename OutT>
+__device__ __forceinline__ void typed_gemm_tile_half(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles) {
+  constexpr int CT = P::kCT, AS = P::kAS, AD = AS - 1, TB = P::kTB, HS = P::kHS, L0 = P::kL0, L1 = P::kL1;
+  static_assert(AD == 2 && CT == 4, "the wait counts below assume A two u-steps ahead and four column groups");
+  constexpr int W0 = 4 + CT * L0, W1 = L0 + 4, W2 = 4 + CT * L1, W3 = L1 + 4;
+  static_assert(W0 < 64 && W2 < 64, "vmcnt field");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = a.nb, steps = 4 * nb;
+  const int mt0 = by * (kG2M / 16);
+  const int ct0 = bx * (4 * CT) + CT * wave;
+  const uint32_t aring = lds_addr(lds);
+  uint8_t* const bring = lds + AS * kG2ASlot + wave * (3 * CT * HS);
+  const uint32_t bring0 = lds_addr(bring);
+  const uint32_t voff16 = 16u * (uint32_t)lane, voff4 = 4u * (uint32_t)lane;
+  const uint8_t* const xa = uniform_ptr(reinterpret_cast<const uint8_t*>(a.xh) + ((size_t)by * nb * 64 + 4 * (size_t)wave) * 1024);
+  const uint32_t aend = aring + AS * kG2ASlot;
+  auto frag_a = [&](const uint8_t* src, uint32_t l, int i) {
+    if (i == 0)
+      lds_dma16<0>(src, voff16, l);
+    else if (i == 1)
+      lds_dma16<1024>(src, voff16, l);
+    else if (i == 2)
+      lds_dma16<2048>(src, voff16, l);
+    else
+      lds_dma16<3072>(src, voff16, l);
+  };
+  const uint8_t* wcol[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+    wcol[c] = uniform_ptr(a.w + (size_t)(ct0 + c < ntiles ? ct0 + c : ntiles - 1) * nb * TB);
+  // Half s of block blk (clamped to the last block) of column c into slot sl.
+  auto issue_half = [&](int blk, int s, int c, int sl) {
+    const int bc = blk < nb ? blk : nb - 1;
+    const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((sl * CT + c) * HS));
+    if (s == 0)
+      P::issue_half0(wcol[c] + (size_t)bc * TB, voff16, voff4, l);
+    else
+      P::issue_half1(wcol[c] + (size_t)bc * TB, voff16, l);
+  };
+  auto hslot = [&](int sl, int c) { return bring + (size_t)(sl * CT + c) * HS; };
+
+  f4_t acc[8][CT];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      acc[rt][c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      asm volatile("" : "+a"(acc[rt][c]));
+    }
+
+  // Prologue: half 0 and 1 of block 0 and half 0 of block 1 into slots 0, 1,
+  // 2, then A(0), A(1); everything but A(1) waited for.
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+    issue_half(0, 0, c, 0);
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+    issue_half(0, 1, c, 1);
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+    issue_half(1, 0, c, 2);
+#pragma unroll
+  for (int t = 0; t < AD; ++t) {
+    const uint8_t* src = xa + (size_t)(t < steps ? t : steps - 1) * 16384;
+    const uint32_t l = aring + (uint32_t)t * kG2ASlot + 4096u * (uint32_t)wave;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      frag_a(src, l, i);
+  }
+  vm_wait<4>();
+  typename P::K kk[CT];
+  h8_t bclo[CT], bchi[CT];
+  typename P::W wl;
+  {
+    typename P::R r[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      P::raw_half(r[c], hslot(0, c), lane);
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      P::consts(kk[c], r[c], lane);
+#pragma unroll
+    for (int c = 0; c < CT - 1; ++c) {
+      typename P::W w;
+      P::words_half(w, hslot(0, c), 0, lane);
+      P::dequant(kk[c], w, 0, bclo[c], bchi[c]);
+    }
+    P::words_half(wl, hslot(0, CT - 1), 0, lane);
+  }
+  uint32_t ar = aring, aw = aring + AD * kG2ASlot + 4096u * (uint32_t)wave;
+  // Slots of half 0 and half 1 of block blk and of half 0 of block blk + 1.
+  int s0 = 0, s1 = 1, s2 = 2;
+  for (int blk = 0; blk < nb; ++blk) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * blk + u;
+      const int ta = t + AD < steps ? t + AD : steps - 1;
+      const uint8_t* const asrc = xa + (size_t)ta * 16384;
+      if (u == 0)
+        vm_wait<W0>();
+      else if (u == 1) {
+        if (blk == 0)
+          vm_wait<4>();
+        else
+          vm_wait<W1>();
+      } else if (u == 2)
+        vm_wait<W2>();
+      else
+        vm_wait<W3>();
+      __syncthreads();  // A(t) of every wave landed; u-step t - 1 fully read
+      __builtin_amdgcn_sched_barrier(0);
+      const int un = (u + 1) & 3;
+      const int ws = u == 0 ? s0 : u == 3 ? s2 : s1;  // slot of the words of u-step t + 1
+      const uint8_t* aslot = lds + (ar - aring);
+      h8_t af[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        af[i] = *reinterpret_cast<const h8_t*>(aslot + i * 1024 + 16 * lane);
+      typename P::R r[CT];
+      if (u == 3) {
+#pragma unroll
+        for (int c = 0; c < CT; ++c)
+          P::raw_half(r[c], hslot(s2, c), lane);
+      }
+      typename P::W wv[CT];
+#pragma unroll
+      for (int c = 0; c < CT; ++c)
+        P::words_half(wv[c], hslot(ws, c), un, lane);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        if (c == 0)
+          P::dequant(kk[CT - 1], wl, u, bclo[CT - 1], bchi[CT - 1]);
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt], bclo[c], acc[rt][c], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt)
+          acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[2 * rt + 1], bchi[c], acc[rt][c], 0, 0, 0);
+        if (u == 3)
+          P::consts(kk[c], r[c], lane);
+        if (c > 0)
+          P::dequant(kk[c - 1], wv[c - 1], un, bclo[c - 1], bchi[c - 1]);
+        frag_a(asrc, aw, c);
+        if (u == 1)
+          issue_half(blk + 1, 1, c, s0);
+        else if (u == 3)
+          issue_half(blk + 2, 0, c, s1);
+      }
+      wl = wv[CT - 1];
+      ar = ar + kG2ASlot == aend ? aring : ar + kG2ASlot;
+      aw = aw + kG2ASlot >= aend ? aw + kG2ASlot - AS * kG2ASlot : aw + kG2ASlot;
+      __builtin_amdgcn_sched_group_barrier(0x100, 64, 0);
+#pragma unroll
+      for (int i = 0; i < 16 * CT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, P::kVPM, 0);
+      }
+    }
+    const int sn = s2;
+    s2 = s1;
+    s1 = s0;
+    s0 = sn;
+  }
+  vm_wait<0>();
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      asm volatile("" : "+a"(acc[rt][c]));
+
+  const bool full = mt0 * 16 + kG2M <= a.m;
+  const int nct = ntiles - ct0 >= CT ? CT : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
+  if (a.post == 0)
+    full ? gemm2_epilogue<OutT, 0, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 0, false, CT>(a, acc, mt0, ct0, lane, nct);
+  else if (a.post == 1)
+    full ? gemm2_epilogue<OutT, 1, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 1, false, CT>(a, acc, mt0, ct0, lane, nct);
+  else
+    full ? gemm2_epilogue<OutT, 2, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 2, false, CT>(a, acc, mt0, ct0, lane, nct);
+}
+
+template <class P>
+constexpr int tg_lds_bytes() {
+  if constexpr (TgIsHalf<P>::value)
+    return P::kAS * kG2ASlot + 4 * 3 * P::kCT * P::kHS;
+  else
+    return P::kAS * kG2ASlot + 4 * 2 * P::kCT * P::kTB;
+}
+
 // Persistent over the (column block, row block) tiles, as the Q4_K GEMM.
 template <class P, typename OutT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void typed_gemm_kernel(GemmArgs a, TileMap map, int ntiles) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[P::kAS * kG2ASlot + 4 * 2 * P::kCT * P::kTB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[tg_lds_bytes<P>()];
+  static_assert(tg_lds_bytes<P>() <= 160 * 1024, "LDS of one workgroup");
   const int count = tile_count(map);
   for (int i = 0; i < count; ++i) {
     if (i > 0)
       __syncthreads();
     int bx, by;
     tile_at(map, i, bx, by);
-    typed_gemm_tile<P, OutT>(a, lds, bx, by, ntiles);
+    if constexpr (TgIsHalf<P>::value)
+      typed_gemm_tile_half<P, OutT>(a, lds, bx, by, ntiles);
+    else
+      typed_gemm_tile<P, OutT>(a, lds, bx, by, ntiles);
   }
 }
 
@@ -4028,6 +4273,26 @@ static bool q8_mid(int ntiles, int tiles_y, int cus) {
   return 3 * r3 <= 2 * r2;
 }
 
+// Four column tiles per wave with B in half tile-blocks (TgQ8_0W) where its
+// rounds of workgroups over the CUs take no longer than those of the three-
+// and two-tile forms, each round weighted by the time of one tile of that
+// form: at M = 2048 a 192-column tile took 0.80 and a 128-column tile 0.61 of
+// a 256-column tile's time (N = 12288, K = 4096: 190.6 us against 202.1 with
+// three tiles per wave; N = 4096, K = 12288: 178.6 against 219.0 with two).
+// Q4K_TYPED_Q8W: -1 auto, 0 never, 1 always; Q4K_TYPED_MID set (0 or 1)
+// turns the auto choice of this form off as well.
+static bool q8_wide(int ntiles, int tiles_y, int cus) {
+  static const int forced = env_int("Q4K_TYPED_Q8W", -1);
+  static const int mid = env_int("Q4K_TYPED_MID", -1);
+  if (forced >= 0)
+    return forced == 1;
+  if (mid >= 0)
+    return false;
+  auto rounds = [&](int cols) { return ((ntiles * 16 + cols - 1) / cols * tiles_y + cus - 1) / cus; };
+  const int r4 = rounds(256), r3 = rounds(192), r2 = rounds(128);
+  return 100 * r4 <= 80 * r3 && 100 * r4 <= 61 * r2;
+}
+
 hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, int dtype, int cus) {
   if (!typed_gemm_supported(type, a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
@@ -4039,12 +4304,15 @@ hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, in
     case kTypeQ6_K:
       return narrow ? typed_gemm_launch<Narrow<TgQ6K>>(s, a, dtype, cus) : typed_gemm_launch<TgQ6K>(s, a, dtype, cus);
     case kTypeQ8_0:
-      // Two column tiles per wave (its 4-tile B ring does not fit beside an
-      // A ring), or three where the 192-column grid takes no more time in
-      // rounds: three tiles read each A fragment for half as many MFMAs
-      // again (at M = 2048 the N = 12288 GEMM measured 211 instead of 243
-      // us; Q6_K and Q5_K measured slower with three, also with a 5-slot A
-      // ring).  Q4K_TYPED_MID: -1 auto, 0 never, 1 always.
+      // Four column tiles per wave on the half tile-block ring (q8_wide), or
+      // two (two blocks of its tile-blocks per column fit beside an A ring),
+      // or three where the 192-column grid takes no more time in rounds:
+      // three tiles read each A fragment for half as many MFMAs again (at
+      // M = 2048 the N = 12288 GEMM measured 211 instead of 243 us; Q6_K and
+      // Q5_K measured slower with three, also with a 5-slot A ring).
+      // Q4K_TYPED_MID: -1 auto, 0 never, 1 always.
+      if (q8_wide(ntiles, tiles_y, cus))
+        return typed_gemm_launch<TgQ8_0W>(s, a, dtype, cus);
       if (q8_mid(ntiles, tiles_y, cus))
         return typed_gemm_launch<Mid<TgQ8_0, 3>>(s, a, dtype, cus);
       return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);

@@ -155,12 +155,14 @@ def case_gemm():
 
 
 def case_typed_gemm():
-    # Q8_0 prefill GEMMs with two or three column tiles per wave: ragged
-    # rows, a last 192-column block with one live column tile (n = 592 is 37
-    # column tiles), with and without the residual epilogue.
+    # Q8_0 prefill GEMMs with two, three or four column tiles per wave:
+    # ragged rows, a last column block with one live column tile (n = 592 is
+    # 37 column tiles), with and without the residual epilogue, and K of one
+    # block (the half tile-block ring's prologue and clamped loads).
     check_linear(300, 592, 1024, t=TYPE_Q8_0, post=1, seed=90)
     check_linear(129, 3072, 2048, t=TYPE_Q8_0, seed=91)
     check_linear(200, 1536, 512, t=TYPE_Q8_0, post=1, seed=92)
+    check_linear(70, 512, 256, t=TYPE_Q8_0, seed=93)
 
 
 def case_typed_gemv():

@@ -194,6 +194,15 @@ def test_prefill_gemm(q4k, oracle, gpu, t, m, n, k):
     assert W.kernel_name(1).endswith("_prefill_mfma16x16x32")
 
 
+@pytest.mark.parametrize("m,n,k,post,dtype", [(2048, 4096, 512, 0, torch.float32), (2000, 4016, 768, 1, torch.float16)])
+def test_prefill_gemm_q8_0_four_tiles(q4k, oracle, gpu, m, n, k, post, dtype):
+    """Q8_0 grids where the four-column-tile form (B in half tile-blocks)
+    takes fewer rounds than the three- and two-tile forms: 256 workgroups of
+    256 columns; 4016 = 16 * 251 columns leave the last column block 11 live
+    tiles (waves with 4, 4, 3 and none) and 2000 rows a partial row block."""
+    _linear(q4k, oracle, gpu, 8, 995 + m, m, n, k, post=post, dtype=dtype, counts=[m])
+
+
 @pytest.mark.parametrize("post,dtype", [(1, torch.float32), (2, torch.float32), (0, torch.float16), (1, torch.float16)])
 @pytest.mark.parametrize("t", ALL_TYPES)
 def test_prefill_gemm_epilogues(q4k, oracle, gpu, t, post, dtype):
