@@ -1589,14 +1589,16 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
   }
 }
 
-// Epilogue of the gated GEMM's 128 x 32 wave tile: the gate tiles (columns
-// 0, 1 of acc) and the up tiles (2, 3) of the same two output column tiles
-// combine as in the two-call form: SiLU(gate) * up, each of gate and up
-// first unscaled and, for fp16 outputs, rounded to fp16 (the gate value the
-// first call stores, the up value the second call's epilogue forms).  nct of
-// the two output tiles lie inside n.
-template <typename OutT, bool FULL>
-__device__ __forceinline__ void gemm2_epilogue_gated(const GemmArgs& a, const f4_t (&acc)[8][4], int mt0, int ct0, int lane, int nct) {
+// Epilogue of the gated GEMM's wave tile of 128 rows and CT / 2 output column
+// tiles: the gate tiles (columns 0 .. CT / 2 - 1 of acc) and the up tiles
+// (the rest) of the same output column tiles combine as in the two-call
+// form: SiLU(gate) * up, each of gate and up first unscaled and, for fp16
+// outputs, rounded to fp16 (the gate value the first call stores, the up
+// value the second call's epilogue forms).  nct of the output tiles lie
+// inside n.
+template <typename OutT, bool FULL, int CT = 4>
+__device__ __forceinline__ void gemm2_epilogue_gated(const GemmArgs& a, const f4_t (&acc)[8][CT], int mt0, int ct0, int lane, int nct) {
+  constexpr int H = CT / 2;  // output tiles: gate columns 0 .. H - 1, up columns H .. CT - 1
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const int g = lane >> 4, col = lane & 15;
   const int row0 = mt0 * 16 + 4 * g;
@@ -1613,10 +1615,10 @@ __device__ __forceinline__ void gemm2_epilogue_gated(const GemmArgs& a, const f4
       if (!FULL && row >= a.m)
         continue;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < H; ++c) {
         if (c >= nct)
           continue;
-        float gv = acc[rt][c][v] * rs[rt][v], uv = acc[rt][2 + c][v] * rs[rt][v];
+        float gv = acc[rt][c][v] * rs[rt][v], uv = acc[rt][H + c][v] * rs[rt][v];
         if (sizeof(OutT) == 2) {
           gv = round_half(gv);
           uv = round_half(uv);
@@ -3105,6 +3107,15 @@ struct Mid : P {
   static constexpr int kCT = 3, kAS = AS;
 };
 
+// Six column tiles per wave (384 columns per workgroup, or 192 output
+// columns of the gated GEMM: three gate and three up tiles) with a 3-slot A
+// ring (156 KB of LDS with Q4_K): each A fragment read from LDS feeds six
+// column tiles.
+template <class P>
+struct Six : P {
+  static constexpr int kCT = 6, kAS = 3;
+};
+
 // Load accounting of the typed GEMM.  A wave issues per u-step its 4 A
 // fragments of A(t + kAS - 1) spread over its kCT column groups, each group's
 // share followed, at u = 0, by the kNL loads of that column's tile-block of
@@ -3151,15 +3162,20 @@ __device__ __forceinline__ void vm_wait() {
 // raw B words of u-step t + 1), then per column tile its 16 MFMAs with the
 // dequantisation of the previous column for u-step t + 1 under them (the
 // last column's under the first column of the next u-step).
-template <class P, typename OutT>
+// GATED: the gated GEMM (SiLU(gate) * up of a.w and a.wu): the wave's
+// columns 0 .. CT / 2 - 1 are output column tiles ct0 .. of the gate matrix,
+// the others the same tiles of the up matrix; ct0 counts output tiles.
+template <class P, typename OutT, bool GATED = false>
 __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds, int bx, int by, int ntiles) {
   constexpr int CT = P::kCT, AS = P::kAS, AD = AS - 1, NL = P::kNL, TB = P::kTB;
+  constexpr int OT = GATED ? CT / 2 : CT;  // output column tiles per wave
   static_assert(tg_first_block_ok(AD, CT, NL), "first-block load accounting");
+  static_assert(!GATED || CT % 2 == 0, "gate and up tiles in pairs");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nb = a.nb, steps = 4 * nb;
   const int mt0 = by * (kG2M / 16);
-  const int ct0 = bx * (4 * CT) + CT * wave;
+  const int ct0 = bx * (4 * OT) + OT * wave;
   const uint32_t aring = lds_addr(lds);
   uint8_t* const bring = lds + AS * kG2ASlot + wave * (2 * CT * TB);
   const uint32_t bring0 = lds_addr(bring);
@@ -3184,8 +3200,10 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
   // last one); block blk goes to ring half blk & 1.
   const uint8_t* wcol[CT];
 #pragma unroll
-  for (int c = 0; c < CT; ++c)
-    wcol[c] = uniform_ptr(a.w + (size_t)(ct0 + c < ntiles ? ct0 + c : ntiles - 1) * nb * TB);
+  for (int c = 0; c < CT; ++c) {
+    const int oc = ct0 + (GATED ? c % OT : c);
+    wcol[c] = uniform_ptr((GATED && c >= OT ? a.wu : a.w) + (size_t)(oc < ntiles ? oc : ntiles - 1) * nb * TB);
+  }
   auto issue_b = [&](int blk, int c) {
     const int bc = blk < nb ? blk : nb - 1;
     const uint32_t l = __builtin_amdgcn_readfirstlane(bring0 + (uint32_t)((blk & 1) * CT + c) * TB);
@@ -3306,6 +3324,11 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
       asm volatile("" : "+a"(acc[rt][c]));
 
   const bool full = mt0 * 16 + kG2M <= a.m;
+  if constexpr (GATED) {
+    const int nct2 = ntiles - ct0 >= OT ? OT : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
+    full ? gemm2_epilogue_gated<OutT, true, CT>(a, acc, mt0, ct0, lane, nct2) : gemm2_epilogue_gated<OutT, false, CT>(a, acc, mt0, ct0, lane, nct2);
+    return;
+  }
   const int nct = ntiles - ct0 >= CT ? CT : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
   if (a.post == 0)
     full ? gemm2_epilogue<OutT, 0, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 0, false, CT>(a, acc, mt0, ct0, lane, nct);
@@ -3520,7 +3543,7 @@ constexpr int tg_lds_bytes() {
 }
 
 // Persistent over the (column block, row block) tiles, as the Q4_K GEMM.
-template <class P, typename OutT>
+template <class P, typename OutT, bool GATED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void typed_gemm_kernel(GemmArgs a, TileMap map, int ntiles) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[tg_lds_bytes<P>()];
   static_assert(tg_lds_bytes<P>() <= 160 * 1024, "LDS of one workgroup");
@@ -3533,7 +3556,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if constexpr (TgIsHalf<P>::value)
       typed_gemm_tile_half<P, OutT>(a, lds, bx, by, ntiles);
     else
-      typed_gemm_tile<P, OutT>(a, lds, bx, by, ntiles);
+      typed_gemm_tile<P, OutT, GATED>(a, lds, bx, by, ntiles);
   }
 }
 
@@ -3968,7 +3991,7 @@ TileMap make_tile_map(int tiles_x, int tiles_y, int grid) {
   return m;
 }
 
-template <class P>
+template <class P, bool GATED = false>
 hipError_t typed_gemm_launch(hipStream_t s, const GemmArgs& a, int dtype, int cus);
 
 // Rounds of workgroups (tiles / CUs, rounded up) of the 256-column and
@@ -4087,6 +4110,23 @@ hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   return hipGetLastError();
 }
 
+// The gated GEMM on the typed template with six B column tiles per wave
+// (three gate and three up tiles: 192 output columns per workgroup, against
+// 128 for q4k_gemm2_kernel) when its rounds of workgroups over the CUs take
+// no longer, a 192-column tile counted as 1.375 of a 128-column one (at
+// M = 2048, N = 12288, K = 4096 the plain GEMM measured 182.6 us with six
+// column tiles per wave against 199-202 us with four).  Its accumulation
+// order and dequantised values are those of q4k_gemm2_kernel, so it stays
+// bit-identical to the gate-then-up calls.  Q4K_GEMM_GATED_SIX: -1 auto, 0
+// never, 1 always.
+static bool gemm2_gated_six(int tiles128, int tiles192, int cus) {
+  static const int forced = env_int("Q4K_GEMM_GATED_SIX", -1);
+  if (forced >= 0)
+    return forced == 1;
+  const int r4 = (tiles128 + cus - 1) / cus, r6 = (tiles192 + cus - 1) / cus;
+  return 11 * r6 <= 8 * r4;
+}
+
 hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   if (!gemm2_supported(a.m, a.n) || a.nb < 1 || !a.wu)
     return hipErrorInvalidValue;
@@ -4099,6 +4139,8 @@ hipError_t launch_gemm2_gated(hipStream_t s, const GemmArgs& a, int dtype, int c
       return hipErrorInvalidValue;
     return gemm2_split_launch<true>(s, a, dtype, tiles_x, tiles_y, cus, b);
   }
+  if (gemm2_gated_six(tiles, ((a.n / 16 + 11) / 12) * tiles_y, cus))
+    return typed_gemm_launch<Six<TgQ4K>, true>(s, a, dtype, cus);
   const int grid = tiles > cus ? cus : tiles;
   const TileMap map = make_tile_map(tiles_x, tiles_y, grid);
   const dim3 block(256);
@@ -4244,17 +4286,18 @@ hipError_t launch_typed_gemv(hipStream_t s, const GemvArgs& a, uint32_t type, in
   }
 }
 
-template <class P>
+template <class P, bool GATED>
 hipError_t typed_gemm_launch(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
-  const int ntiles = a.n / 16, tiles_x = (ntiles + 4 * P::kCT - 1) / (4 * P::kCT);
+  constexpr int OT = GATED ? P::kCT / 2 : P::kCT;  // output column tiles per wave
+  const int ntiles = a.n / 16, tiles_x = (ntiles + 4 * OT - 1) / (4 * OT);
   const int tiles_y = (a.m + kG2M - 1) / kG2M, tiles = tiles_x * tiles_y;
   const int g = tiles > cus ? cus : tiles;
   const TileMap map = make_tile_map(tiles_x, tiles_y, g);
   const dim3 grid((unsigned)g), block(256);
   if (dtype == kF32)
-    (void)dispatch(typed_gemm_kernel<P, float>, grid, block, s, a, map, ntiles);
+    (void)dispatch(typed_gemm_kernel<P, float, GATED>, grid, block, s, a, map, ntiles);
   else
-    (void)dispatch(typed_gemm_kernel<P, _Float16>, grid, block, s, a, map, ntiles);
+    (void)dispatch(typed_gemm_kernel<P, _Float16, GATED>, grid, block, s, a, map, ntiles);
   return hipGetLastError();
 }
 

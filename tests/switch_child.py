@@ -154,6 +154,17 @@ def case_gemm():
     check_linear(64, 1024, 4096, t=TYPE_Q6_K, seed=64)
 
 
+def case_gated_six():
+    # The gated prefill GEMM with six B column tiles per wave (three gate and
+    # three up tiles) forced, or never taken: last column blocks with 9 and 5
+    # live output tiles (1296 = 16 * 81, 272 = 16 * 17: waves with 3, 3, 3,
+    # none and 3, 2, none, none), K of one block, and a grid where the default
+    # routing takes six tiles.
+    check_gate_up(257, 1296, 2048, seed=94)
+    check_gate_up(130, 272, 256, seed=95)
+    check_gate_up(821, 6144, 1024, seed=96)
+
+
 def case_typed_gemm():
     # Q8_0 prefill GEMMs with two, three or four column tiles per wave:
     # ragged rows, a last column block with one live column tile (n = 592 is
@@ -186,6 +197,7 @@ CASES = {
     "gemv_shape": case_gemv_shape,
     "gemm": case_gemm,
     "typed_gemm": case_typed_gemm,
+    "gated_six": case_gated_six,
     "typed_gemv": case_typed_gemv,
     "q4k_persistent_off": case_q4k_persistent_off,
 }
