@@ -985,7 +985,7 @@ def main():
             "unit": "TFLOP/s",
             "ms_per_step": round(pre["ms_per_step"], 4),
             "roofline": {
-                "kernel": "q4k_gemm2_kernel<float,true,false> (gated gate/up GEMM, M=2048, K=4096, N=12288 x2: 412.32 GFLOP per launch)",
+                "kernel": "typed_gemm_kernel<Six<TgQ4K>,float,true> (gated gate/up GEMM, six B column tiles per wave, M=2048, K=4096, N=12288 x2: 412.32 GFLOP per launch)",
                 "bound": "mfma",
                 "achieved": round(pre["gated_gemm_tflops"], 1),
                 "peak": FP16_DENSE_PEAK_TFLOPS,
