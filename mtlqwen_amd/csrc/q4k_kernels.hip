@@ -1536,7 +1536,8 @@ constexpr int kG2BWave = 2 * 4 * kTileBlockBytes;      // per wave: 2 blocks x 4
 // per-row checks.  CT column tiles per wave, of which the first nct lie
 // inside n.
 template <typename OutT, int POST, bool FULL, int CT = 4>
-__device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&acc)[8][CT], int mt0, int ct0, int lane, int nct = CT) {
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&acc)[8][CT], int mt0, int ct0, int lane, int nct = CT,
+                                               float* lrs = nullptr) {
   OutT* y = reinterpret_cast<OutT*>(a.y);
   const OutT* aux = reinterpret_cast<const OutT*>(a.aux);
   const int g = lane >> 4, col = lane & 15;
@@ -1544,10 +1545,22 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
   constexpr bool full = FULL;
   // Row scales exist for the padded rows (the staging buffers cover whole
   // 128-row tiles), so these 16-byte loads stay in bounds.
+  // Row scales of the 8 row tiles up front and the aux of row tile rt + 1
+  // loaded under the stores of row tile rt (two buffers).  With more than
+  // four column tiles per wave the registers of all that do not fit beside
+  // the six-tile loop's: the wave stages the tile's 128 row scales in its own
+  // LDS (lrs, its B ring, idle once its loads have landed) with one load and
+  // reads each row tile's from there, and loads each row tile's aux just
+  // before it.
+  constexpr bool ahead = CT <= 4;
   f4_t rs[8];
+  if constexpr (ahead) {
 #pragma unroll
-  for (int rt = 0; rt < 8; ++rt)
-    rs[rt] = *reinterpret_cast<const f4_t*>(a.rowscale + row0 + 16 * rt);
+    for (int rt = 0; rt < 8; ++rt)
+      rs[rt] = *reinterpret_cast<const f4_t*>(a.rowscale + row0 + 16 * rt);
+  } else {
+    *reinterpret_cast<float2*>(lrs + 2 * lane) = *reinterpret_cast<const float2*>(a.rowscale + mt0 * 16 + 2 * lane);
+  }
   const size_t col0 = (size_t)ct0 * 16 + col;
   float av[2][4][CT];
   auto load_aux = [&](int rt, float (&dst)[4][CT]) {
@@ -1559,13 +1572,17 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, const f4_t (&a
         dst[v][c] = (full || row < a.m) && c < nct ? load_elem(aux, (size_t)row * a.n + col0 + 16 * c) : 0.0f;
       }
   };
-  if (POST != 0)
+  if (POST != 0 && ahead)
     load_aux(0, av[0]);
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt) {
-    if (POST != 0 && rt + 1 < 8)
+    if (POST != 0 && ahead && rt + 1 < 8)
       load_aux(rt + 1, av[(rt + 1) & 1]);
-    const float (&cur)[4][CT] = av[rt & 1];
+    if (POST != 0 && !ahead)
+      load_aux(rt, av[0]);
+    if constexpr (!ahead)
+      rs[rt] = *reinterpret_cast<const f4_t*>(lrs + 16 * rt + 4 * g);
+    const float (&cur)[4][CT] = av[ahead ? rt & 1 : 0];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = row0 + 16 * rt + v;
@@ -3109,11 +3126,17 @@ struct Mid : P {
 
 // Six column tiles per wave (384 columns per workgroup, or 192 output
 // columns of the gated GEMM: three gate and three up tiles) with a 3-slot A
-// ring (156 KB of LDS with Q4_K): each A fragment read from LDS feeds six
-// column tiles.
+// ring (156 KB of LDS with Q4_K, 150 KB with IQ4_XS): each A fragment read
+// from LDS feeds six column tiles.
 template <class P>
 struct Six : P {
   static constexpr int kCT = 6, kAS = 3;
+};
+// IQ4_XS: six vector instructions per MFMA in the schedule (with 2 to 5 the
+// plain GEMM's epilogue spills two VGPRs around the loop).
+template <>
+struct Six<TgIQ4XS> : TgIQ4XS {
+  static constexpr int kCT = 6, kAS = 3, kVPM = 6;
 };
 
 // Load accounting of the typed GEMM.  A wave issues per u-step its 4 A
@@ -3330,12 +3353,13 @@ __device__ __forceinline__ void typed_gemm_tile(const GemmArgs& a, uint8_t* lds,
     return;
   }
   const int nct = ntiles - ct0 >= CT ? CT : ntiles - ct0 > 0 ? ntiles - ct0 : 0;
+  float* const lrs = reinterpret_cast<float*>(bring);  // this wave's B ring: its loads have landed
   if (a.post == 0)
-    full ? gemm2_epilogue<OutT, 0, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 0, false, CT>(a, acc, mt0, ct0, lane, nct);
+    full ? gemm2_epilogue<OutT, 0, true, CT>(a, acc, mt0, ct0, lane, nct, lrs) : gemm2_epilogue<OutT, 0, false, CT>(a, acc, mt0, ct0, lane, nct, lrs);
   else if (a.post == 1)
-    full ? gemm2_epilogue<OutT, 1, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 1, false, CT>(a, acc, mt0, ct0, lane, nct);
+    full ? gemm2_epilogue<OutT, 1, true, CT>(a, acc, mt0, ct0, lane, nct, lrs) : gemm2_epilogue<OutT, 1, false, CT>(a, acc, mt0, ct0, lane, nct, lrs);
   else
-    full ? gemm2_epilogue<OutT, 2, true, CT>(a, acc, mt0, ct0, lane, nct) : gemm2_epilogue<OutT, 2, false, CT>(a, acc, mt0, ct0, lane, nct);
+    full ? gemm2_epilogue<OutT, 2, true, CT>(a, acc, mt0, ct0, lane, nct, lrs) : gemm2_epilogue<OutT, 2, false, CT>(a, acc, mt0, ct0, lane, nct, lrs);
 }
 
 // typed_gemm_tile with B in half tile-blocks (policies with kHalf): per
@@ -4086,6 +4110,20 @@ hipError_t gemm2_split_launch(hipStream_t s, GemmArgs a, int dtype, int tiles_x,
 }
 }  // namespace
 
+// Six column tiles per wave (384 columns per workgroup) for a plain GEMM
+// when its rounds of workgroups over the CUs take no longer than those of
+// the 256-column tiling, a 384-column tile counted as 1.375 of a 256-column
+// one (at M = 2048, N = 12288, K = 4096: Q4_K 182.6 us against 199-202 with
+// four tiles per wave, IQ4_XS 208-210 against 224-225).  Q4K_GEMM_SIX: -1
+// auto, 0 never, 1 always (the Q4_K and IQ4_XS GEMMs).
+static bool gemm_six(int tiles256, int tiles384, int cus) {
+  static const int forced = env_int("Q4K_GEMM_SIX", -1);
+  if (forced >= 0)
+    return forced == 1;
+  const int r4 = (tiles256 + cus - 1) / cus, r6 = (tiles384 + cus - 1) / cus;
+  return 11 * r6 <= 8 * r4;
+}
+
 hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   if (!gemm2_supported(a.m, a.n) || a.nb < 1)
     return hipErrorInvalidValue;
@@ -4097,6 +4135,8 @@ hipError_t launch_gemm2(hipStream_t s, const GemmArgs& a, int dtype, int cus) {
   }
   if (gemm2_mid(a.m, a.n, cus))
     return typed_gemm_launch<Mid<TgQ4K, 5>>(s, a, dtype, cus);
+  if (gemm_six(tiles, ((a.n / 16 + 23) / 24) * tiles_y, cus))
+    return typed_gemm_launch<Six<TgQ4K>>(s, a, dtype, cus);
   if (gemm2_narrow(tiles, ((a.n / 16 + 7) / 8) * tiles_y, cus))
     return typed_gemm_launch<TgQ4K>(s, a, dtype, cus);
   static const int persist = env_int("Q4K_GEMM2_PERSIST", 1);
@@ -4360,6 +4400,8 @@ hipError_t launch_typed_gemm(hipStream_t s, const GemmArgs& a, uint32_t type, in
         return typed_gemm_launch<Mid<TgQ8_0, 3>>(s, a, dtype, cus);
       return typed_gemm_launch<TgQ8_0>(s, a, dtype, cus);
     default:
+      if (gemm_six(((ntiles + 15) / 16) * tiles_y, ((ntiles + 23) / 24) * tiles_y, cus))
+        return typed_gemm_launch<Six<TgIQ4XS>>(s, a, dtype, cus);
       return narrow ? typed_gemm_launch<Narrow<TgIQ4XS>>(s, a, dtype, cus) : typed_gemm_launch<TgIQ4XS>(s, a, dtype, cus);
   }
 }

@@ -19,7 +19,7 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 
 import mtlqwen_amd as q4k  # noqa: E402
-from q4k_ref import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, Oracle, gated_prefill_arithmetic, make_weight, make_x, row_rel_err  # noqa: E402
+from q4k_ref import TYPE_IQ4_XS, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, Oracle, gated_prefill_arithmetic, make_weight, make_x, row_rel_err  # noqa: E402
 
 TOL = 1e-3
 dev = torch.device("cuda:0")
@@ -165,6 +165,16 @@ def case_gated_six():
     check_gate_up(821, 6144, 1024, seed=96)
 
 
+def case_six():
+    # Plain GEMMs with six column tiles per wave forced, or never taken:
+    # Q4_K with a last 384-column block of 17 live tiles (1040 = 16 * 65:
+    # waves with 6, 6, 5, none) and one block of K, IQ4_XS with the residual
+    # epilogue and a last block of 13 live tiles (592 = 16 * 37).
+    check_linear(129, 1040, 256, seed=97)
+    check_linear(300, 592, 1280, t=TYPE_IQ4_XS, post=1, seed=98)
+    check_linear(200, 1536, 2048, post=1, seed=99)
+
+
 def case_typed_gemm():
     # Q8_0 prefill GEMMs with two, three or four column tiles per wave:
     # ragged rows, a last column block with one live column tile (n = 592 is
@@ -198,6 +208,7 @@ CASES = {
     "gemm": case_gemm,
     "typed_gemm": case_typed_gemm,
     "gated_six": case_gated_six,
+    "six": case_six,
     "typed_gemv": case_typed_gemv,
     "q4k_persistent_off": case_q4k_persistent_off,
 }

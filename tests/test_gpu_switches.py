@@ -43,6 +43,8 @@ SETTINGS = [
     ({"Q4K_TYPED_Q8W": "0"}, "typed_gemm"),
     ({"Q4K_GEMM_GATED_SIX": "1"}, "gated_six"),
     ({"Q4K_GEMM_GATED_SIX": "0"}, "gated_six"),
+    ({"Q4K_GEMM_SIX": "1"}, "six"),
+    ({"Q4K_GEMM_SIX": "0"}, "six"),
     ({"Q6K_GEMV_PERSISTENT": "1"}, "typed_gemv"),
     ({"Q6K_GEMV_PERSISTENT": "0", "Q6K_GEMV_TILES": "4"}, "typed_gemv"),
     ({"Q6K_GEMV_TILES": "2"}, "typed_gemv"),

@@ -203,6 +203,16 @@ def test_prefill_gemm_q8_0_four_tiles(q4k, oracle, gpu, m, n, k, post, dtype):
     _linear(q4k, oracle, gpu, 8, 995 + m, m, n, k, post=post, dtype=dtype, counts=[m])
 
 
+@pytest.mark.parametrize("m,n,k,post,dtype", [(2048, 6144, 512, 0, torch.float32), (2000, 6128, 768, 1, torch.float16)])
+@pytest.mark.parametrize("t", [12, 23])
+def test_prefill_gemm_six_tiles(q4k, oracle, gpu, t, m, n, k, post, dtype):
+    """Q4_K and IQ4_XS grids where six column tiles per wave (384 columns per
+    workgroup) take fewer rounds than four: 256 workgroups against 384;
+    6128 = 16 * 383 columns leave the last column block 23 live tiles (waves
+    with 6, 6, 6 and 5) and 2000 rows a partial row block."""
+    _linear(q4k, oracle, gpu, t, 985 + m + t, m, n, k, post=post, dtype=dtype, counts=[m])
+
+
 @pytest.mark.parametrize("post,dtype", [(1, torch.float32), (2, torch.float32), (0, torch.float16), (1, torch.float16)])
 @pytest.mark.parametrize("t", ALL_TYPES)
 def test_prefill_gemm_epilogues(q4k, oracle, gpu, t, post, dtype):
