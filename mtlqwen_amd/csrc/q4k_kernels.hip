@@ -2516,6 +2516,16 @@ struct FmtIQ4XS {
     const uint32_t m = __builtin_amdgcn_perm(0u, 0u, and_or(w >> 3, 0x01010101u, 0x0C0C0C0Cu));
     return (m & b) | (~m & a);
   }
+  // The same for the indices at bits 4..7 of each byte.  Bit 3 of index b is
+  // bit 7 of byte b, which selectors 8..11 turn into a byte mask directly
+  // (0x00 or 0xFF from bit 15 / 31 of the second source, bit 15 / 31 of the
+  // first): bytes 1, 3 from w, bytes 0, 2 from w << 8.
+  static __device__ __forceinline__ uint32_t lookup_hi(uint32_t w) {
+    const uint32_t t = (w >> 4) & 0x07070707u;
+    const uint32_t a = __builtin_amdgcn_perm(kT1, kT0, t), b = __builtin_amdgcn_perm(kT3, kT2, t);
+    const uint32_t m = __builtin_amdgcn_perm(w << 8, w, 0x090B080Au);
+    return (m & b) | (~m & a);
+  }
   static __device__ __forceinline__ void mac(const U& u, const XF& x, int lane, f4_t& acc) {
     const int g = lane >> 4;
     const uint32_t sh = u.hd.x >> 16, sl = u.hd.y;
@@ -2530,7 +2540,7 @@ struct FmtIQ4XS {
 #pragma unroll
     for (int fs = 0; fs < 8; ++fs) {
       const uint32_t w = (fs < 4 ? u.q0 : u.q1)[fs & 3];
-      const uint32_t vlo = lookup(w), vhi = lookup(w >> 4);
+      const uint32_t vlo = lookup(w), vhi = lookup_hi(w);
       const h2_t mul = fs < 4 ? mul0 : mul1, add = fs < 4 ? add0 : add1;
       auto f = [&](uint32_t v, uint32_t sel) {
         return as_u32(__builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(0x64646464u, v, sel)), mul, add));
@@ -3041,7 +3051,7 @@ struct TgIQ4XS {
   // Codebook value + 128 per byte (FmtIQ4XS::lookup) as fp16 1152 + v, then
   // dl * v exactly.
   static __device__ __forceinline__ h8_t frag(uint32_t wq, float dl, float cl) {
-    const uint32_t vlo = FmtIQ4XS::lookup(wq), vhi = FmtIQ4XS::lookup(wq >> 4);
+    const uint32_t vlo = FmtIQ4XS::lookup(wq), vhi = FmtIQ4XS::lookup_hi(wq);
     const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, vlo, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, vlo, 0x04030402u),
                            __builtin_amdgcn_perm(0x64646464u, vhi, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, vhi, 0x04030402u)};
     uint32_t r[4];
