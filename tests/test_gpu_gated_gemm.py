@@ -34,11 +34,12 @@ def _gemm_launches(q4k, fn):
 # takes 192 columns per workgroup (the typed template) and neither form
 # splits K; at (821, 5120, 4096) both split K at block 11 of 16, the plain
 # GEMM with its short segments two to a workgroup, the gated one (280 tiles)
-# dealing all segments round robin.
+# dealing all segments round robin.  At (2048, 12288) and (821, 6144) the
+# gated launch takes six B column tiles per wave (fp32 and fp16 outputs).
 SHAPES = [(300, 512, 1024, torch.float32), (257, 1296, 2048, torch.float32), (129, 272, 1024, torch.float32),
           (130, 512, 256, torch.float16), (2048, 12288, 4096, torch.float32),
           (200, 1024, 8192, torch.float32), (130, 512, 12288, torch.float16), (821, 6144, 1024, torch.float32),
-          (821, 5120, 4096, torch.float32)]
+          (821, 6144, 1024, torch.float16), (821, 5120, 4096, torch.float32)]
 
 
 @pytest.mark.parametrize("m,n,k,dtype", SHAPES)
