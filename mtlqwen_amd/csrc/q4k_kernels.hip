@@ -2773,7 +2773,10 @@ __global__ __launch_bounds__(64 * W) void typed_gemv_persistent_kernel(GemvArgs 
 // tile-block; kVPM vector instructions scheduled after each MFMA (measured:
 // 2 for Q5_K, Q6_K and Q8_0, 3-5 percent faster than 3 or 4 at M = 2048; 4
 // for IQ4_XS).  Column tiles past n (a multiple of 16, not of the
-// workgroup's width) load the last tile and store nothing.
+// workgroup's width) load the last tile and store nothing.  Wrappers set
+// other widths: Narrow (2 tiles), Mid (3), Six (6, with a 3-slot A ring;
+// also the gated Q4_K GEMM, GATED), and TgQ8_0W streams Q8_0's B in half
+// tile-blocks so that four tiles fit.
 // ----------------------------------------------------------------------------
 
 // Bit `from` (and from + 16) of h moved to bit `to` (and to + 16).
